@@ -1,0 +1,346 @@
+"""Benchmark of the MI355X GQA attention path (one GPU).
+
+Headline workload (config.workload = "cfg4_batched_decode_fp16"): batched
+independent-sequence decode attention, 256 sequences x 4096 positions of fp16
+KV at Granite shapes (16 q / 8 kv heads, d 64), over 24 layers' worth of
+independent caches (51.5 GB resident in HBM).  One step = one query token per
+sequence through all 24 layers (24 decode launches, 2.147 GB of KV each).
+`value` = microseconds per sequence-token across the 24 layers
+(step time / 256).  `roofline` is the decode kernel's achieved HBM GB/s
+(algorithmic bytes per launch / average launch time) against 8 TB/s.
+
+The other BASELINE configurations are reported under "detail" with their own
+rooflines.  The CPU baseline is the oracle (a restatement of the reference's
+single-threaded CPU attention) timed on a bounded sample on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-detail] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"f16": 2500.0, "bf16": 2500.0}
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def timed(fn, steps, warmup, stream):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per step
+
+
+def load_traffic(kernel_key):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f).get(kernel_key)
+    except (OSError, ValueError):
+        return None
+
+
+def roofline_hbm(bytes_per_launch, ms_per_launch, traffic=None):
+    gbs = bytes_per_launch / (ms_per_launch * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic}
+
+
+# ---------------------------------------------------------------------------
+# cfg4: batched fp16 decode, 256 x 4096, 24 layers of independent caches
+# ---------------------------------------------------------------------------
+def bench_cfg4(ctx, steps, warmup):
+    import torch
+    from qx_amd import abi
+    from qx_amd import runtime as rt
+
+    S, L, LAYERS = 256, 4096, 24
+    stream = torch.cuda.current_stream()
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, LAYERS, S, L, abi.F16)
+    q = torch.empty((LAYERS, S, 16, 64), device="cuda:0")
+    out = torch.empty_like(q)
+    with rt.Graph(ctx, stream) as g:
+        arena.fill_normal(g, seed=4, length=L)
+        rt.fill_normal(g, q, seed=44)
+    ws_bytes = rt.attention_workspace_bytes(arena, S, L)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda:0")
+
+    g = rt.Graph(ctx, stream)
+
+    def step():
+        for layer in range(LAYERS):
+            rt.attention(g, arena, layer, q[layer], L, out=out[layer], workspace=ws)
+
+    ms = timed(step, steps, warmup, stream)
+    g.finish()
+    kv_bytes = S * 8 * L * 64 * 2 * 2
+    io_bytes = 2 * S * 16 * 64 * 4
+    per_launch_ms = ms / LAYERS
+    res = {
+        "ms_per_step": ms,
+        "us_per_sequence_token": ms * 1000.0 / S,
+        "us_per_layer_step": per_launch_ms * 1000.0,
+        "bytes_per_launch": kv_bytes + io_bytes,
+        "roofline": roofline_hbm(kv_bytes + io_bytes, per_launch_ms, load_traffic("cfg4_decode")),
+        "launches_per_step": LAYERS,
+    }
+    del arena
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------------------
+# cfg1: one Granite layer, positions 0..511 (fp32), captured once, replayed
+# ---------------------------------------------------------------------------
+def bench_cfg1(ctx, steps, warmup):
+    import torch
+    from qx_amd import abi
+    from qx_amd import runtime as rt
+
+    P = 512
+    stream = torch.cuda.current_stream()
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, P, abi.F32)
+    q = torch.empty((P, 1, 1, 16, 64), device="cuda:0")
+    k = torch.empty((P, 1, 1, 8, 64), device="cuda:0")
+    v = torch.empty_like(k)
+    qo = torch.empty_like(q)
+    out = torch.empty((P, 1, 16, 64), device="cuda:0")
+    ws = torch.empty(max(rt.attention_workspace_bytes(arena, 1, P), 1), dtype=torch.uint8, device="cuda:0")
+    with rt.Graph(ctx, stream) as g:
+        for t, s in ((q, 1), (k, 2), (v, 3)):
+            rt.fill_normal(g, t, seed=s)
+    g = rt.Graph(ctx, stream)
+    g.capture_begin()
+    for p in range(P):
+        rt.rope_kv_batch(g, arena, 0, p, q[p], k[p], v[p], query_out=qo[p])
+        rt.attention(g, arena, 0, qo[p].view(1, 16, 64), p + 1, out=out[p], workspace=ws)
+    replay = g.capture_end()
+    g.discard()
+    ms = timed(lambda: replay.launch(stream), steps, warmup, stream)
+    total_kv = sum(4096 * (p + 1) for p in range(P))
+    return {"us_per_token": ms * 1000.0 / P, "ms_per_512_steps": ms,
+            "roofline": roofline_hbm(total_kv / P, ms / P, None),
+            "note": "one token = fused RoPE/append + decode attention (2 launches), HIP-graph replay"}
+
+
+# ---------------------------------------------------------------------------
+# cfg2: Granite 24-layer attention-only stack at ctx 4096 (fp32)
+# ---------------------------------------------------------------------------
+def bench_cfg2(ctx, steps, warmup):
+    import torch
+    from qx_amd import abi
+    from qx_amd import runtime as rt
+
+    LAYERS, POS = 24, 4095
+    stream = torch.cuda.current_stream()
+    sets = []
+    for s in range(2):  # two independent weight+cache sets (705 MB each) so the 256 MB MALL cannot hold a token
+        arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, LAYERS, 1, 4096, abi.F32)
+        layers = []
+        with rt.Graph(ctx, stream) as g:
+            arena.fill_normal(g, seed=10 + s, length=POS)
+            for layer in range(LAYERS):
+                norm = torch.ones(1024, device="cuda:0")
+                wq = torch.empty((1024, 1024), device="cuda:0")
+                wk = torch.empty((512, 1024), device="cuda:0")
+                wv = torch.empty((512, 1024), device="cuda:0")
+                wo = torch.empty((1024, 1024), device="cuda:0")
+                for i, w in enumerate((wq, wk, wv, wo)):
+                    rt.fill_normal(g, w, seed=1000 * s + 10 * layer + i, stddev=0.02)
+                layers.append(rt.GraniteLayer(norm, wq, wk, wv, wo))
+        hidden = [torch.empty(1024, device="cuda:0") for _ in range(LAYERS + 1)]
+        with rt.Graph(ctx, stream) as g:
+            rt.fill_normal(g, hidden[0], seed=77 + s)
+        ws = torch.empty(rt.granite_block_workspace_bytes(arena, POS + 1), dtype=torch.uint8, device="cuda:0")
+        g = rt.Graph(ctx, stream)
+        g.capture_begin()
+        for layer in range(LAYERS):
+            rt.granite_attention_block(g, arena, layer, POS, layers[layer], hidden[layer], hidden[layer + 1], ws)
+        replay = g.capture_end()
+        g.discard()
+        sets.append((arena, layers, hidden, ws, replay))
+    it = [0]
+
+    def step():
+        sets[it[0] & 1][4].launch(stream)
+        it[0] += 1
+
+    ms = timed(step, steps, warmup, stream)
+    weights = LAYERS * (1024 * 1024 * 2 + 512 * 1024 * 2) * 4
+    kv = LAYERS * 4096 * 8 * 64 * 4 * 2
+    return {"us_per_token": ms * 1000.0, "bytes_per_token": weights + kv,
+            "roofline": roofline_hbm(weights + kv, ms, None),
+            "note": "24 x (norm+QKV+RoPE+append, decode attention, O+residual) per token, HIP-graph replay, "
+                    "2 rotated weight/cache sets; roofline is for the whole token"}
+
+
+# ---------------------------------------------------------------------------
+# cfg5a: Qwen decode at ctx 32768, bf16 KV, 48 layers' caches rotated
+# ---------------------------------------------------------------------------
+def bench_cfg5a(ctx, steps, warmup):
+    import torch
+    from qx_amd import abi
+    from qx_amd import runtime as rt
+
+    LAYERS, L = 48, 32768
+    stream = torch.cuda.current_stream()
+    arena = rt.KvArena(ctx, abi.SHAPE_QWEN3, LAYERS, 1, L, abi.BF16)
+    q = torch.empty((LAYERS, 1, 32, 128), dtype=torch.bfloat16, device="cuda:0")
+    out = torch.empty_like(q)
+    with rt.Graph(ctx, stream) as g:
+        arena.fill_normal(g, seed=5, length=L)
+        rt.fill_normal(g, q, seed=55)
+    ws = torch.empty(max(rt.attention_workspace_bytes(arena, 1, L), 1), dtype=torch.uint8, device="cuda:0")
+    g = rt.Graph(ctx, stream)
+    g.capture_begin()
+    for layer in range(LAYERS):
+        rt.attention(g, arena, layer, q[layer], L, out=out[layer], workspace=ws)
+    replay = g.capture_end()
+    g.discard()
+    ms = timed(lambda: replay.launch(stream), steps, warmup, stream)
+    per_layer = ms / LAYERS
+    kv = L * 4 * 128 * 2 * 2
+    return {"us_per_layer": per_layer * 1000.0, "bytes_per_layer": kv,
+            "roofline": roofline_hbm(kv, per_layer, load_traffic("cfg5a_decode")),
+            "note": "48 layers' caches (3.2 GB) replayed per step; per-layer = decode + combine"}
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle's single-threaded Granite attention on a sample
+# ---------------------------------------------------------------------------
+def cpu_baseline(seconds=10.0):
+    import concurrent.futures as cf
+
+    import numpy as np
+
+    from oracle import oracle as O
+
+    L = 4096
+    rng = np.random.default_rng(0)
+    keys = rng.standard_normal((L, 8, 64), dtype=np.float32).astype(np.float16).astype(np.float32)
+    vals = rng.standard_normal((L, 8, 64), dtype=np.float32).astype(np.float16).astype(np.float32)
+    q = rng.standard_normal(1024, dtype=np.float32)
+
+    def make_cache():
+        c = O.KvCache(L)
+        c.extend(keys, vals)
+        return c
+
+    cache = make_cache()
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds or n < 3:
+        O.granite_attend(q, cache, L)
+        n += 1
+    t1 = (time.perf_counter() - t0) / n
+    cores = os.cpu_count() or 1
+    cores = min(cores, 16)
+    caches = [make_cache() for _ in range(cores)]
+    per_thread = max(2, n // cores)
+
+    def work(c):
+        for _ in range(per_thread):
+            O.granite_attend(q, c, L)
+
+    t0 = time.perf_counter()
+    with cf.ThreadPoolExecutor(cores) as ex:
+        list(ex.map(work, caches))
+    tall = (time.perf_counter() - t0) / (per_thread * cores)
+    return {
+        "value": round(t1 * 24 * 1e6, 1), "unit": "us/sequence-token (24 layers)", "cores": 1, "kind": "port",
+        "sample": f"{n} single-thread oracle attends of one Granite layer at ctx 4096 (fp16-rounded KV, "
+                  f"upcast fp32 math), x24 layers; cfg4 step = 256 sequences",
+        "all_core": {"value": round(tall * 24 * 1e6, 1), "cores": cores,
+                     "sample": f"{per_thread * cores} attends over {cores} threads (independent sequences)"},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-detail", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from qx_amd import runtime as rt
+
+    ctx = rt.Context(0)
+    side = torch.cuda.Stream()  # default priority; HIP-graph capture needs a non-null stream
+    with torch.cuda.stream(side):
+        run(ctx, args)
+
+
+def run(ctx, args):
+    import torch
+
+    only = set(filter(None, args.only.split(",")))
+    detail = {}
+    head = bench_cfg4(ctx, args.steps, args.warmup) if (not only or "cfg4" in only) else None
+    if head:
+        log("cfg4", json.dumps(head))
+    if not args.no_detail:
+        for name, fn in (("cfg1", bench_cfg1), ("cfg2", bench_cfg2), ("cfg5a", bench_cfg5a)):
+            if only and name not in only:
+                continue
+            try:
+                detail[name] = fn(ctx, max(3, args.steps), args.warmup)
+                log(name, json.dumps(detail[name]))
+            except Exception as e:  # report, keep the headline
+                detail[name] = {"error": str(e)}
+                log(name, "error", e)
+            torch.cuda.empty_cache()
+    cpu = None if args.no_cpu else cpu_baseline()
+    if head is None:
+        print(json.dumps({"detail": detail, "cpu_baseline": cpu}))
+        return
+    line = {
+        "metric": "decode attn µs/token & HBM GB/s (% peak); prefill attn TFLOP/s (% MFMA peak)",
+        "value": round(head["us_per_sequence_token"], 3),
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: N(0,1) KV and queries generated on device (SplitMix64 + Box-Muller), seeded",
+        "config": {"workload": "cfg4_batched_decode_fp16", "sequences": 256, "context": 4096, "layers": 24,
+                   "q_heads": 16, "kv_heads": 8, "head_dim": 64, "kv_dtype": "f16",
+                   "step": "one query token per sequence through 24 layers of independent caches"},
+        "roofline": head["roofline"],
+        "cpu_baseline": cpu,
+        "detail": {"cfg4": {k: v for k, v in head.items() if k != "roofline"}, **detail},
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

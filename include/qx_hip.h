@@ -1,0 +1,298 @@
+/*
+ * qx_hip.h -- C ABI of the MI355X (gfx950) grouped-query-attention path.
+ *
+ * This is the drop-in boundary for the attention path of blasrodri/qx: it
+ * replaces the attention encoders of `qx_metal::platform::DecodeGraph`
+ * (crates/qx-metal/src/lib.rs) for this path only.  Each entry point names
+ * the reference interface it replaces.  The library is built from
+ * hand-written HIP sources (the .hip files of qx_amd/csrc) into libqx_hip.so.
+ *
+ * Conventions
+ *  - Every call returns int32_t status: QXH_OK (0) or an error code; the
+ *    message is kept per thread and read with qxh_last_error().  This mirrors
+ *    the reference's `Result<(), String>`.  Errors never abort.
+ *  - Tensors are plain device pointers plus the caller's promise of their
+ *    shape; sizes the library cannot infer are passed explicitly.
+ *  - Encoders only enqueue work on the graph's HIP stream (the reference's
+ *    encode_* record into a command buffer); qxh_graph_wait / _finish is
+ *    where errors of enqueued work surface (SubmittedDecode::wait).
+ *  - Kernels never allocate.  Scratch memory is a caller-owned workspace.
+ *  - Tensor layouts (row-major):
+ *      decode query/output   [sequences][q_heads][head_dim]
+ *      batch query/output    [sequences][tokens][q_heads][head_dim]
+ *      key/value inputs      [sequences][tokens][kv_heads][head_dim]
+ *      KV arena (head-major) K: [layer][sequence][kv_head][capacity][head_dim]
+ *                            V: same, after the whole K region
+ *    The reference's KV rows are position-major [position][kv_head][head_dim]
+ *    (crates/qx-runtime/src/lib.rs:400-415); qxh_encode_kv_gather_token_rows
+ *    converts for consumers that read token rows.
+ */
+#ifndef QX_HIP_H
+#define QX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QXH_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define QXH_API __attribute__((visibility("default")))
+#else
+#define QXH_API
+#endif
+
+/* Status codes. */
+enum {
+    QXH_OK = 0,
+    QXH_ERR_INVALID_ARGUMENT = 1, /* shape, size, dtype or pointer validation failed */
+    QXH_ERR_KV_POSITION = 2,      /* append not at the cursor, or past capacity */
+    QXH_ERR_HIP = 3,              /* a HIP runtime call failed */
+    QXH_ERR_UNSUPPORTED = 4,      /* a valid request with no instantiated kernel */
+    QXH_ERR_NO_DEVICE = 5         /* no usable gfx950 device */
+};
+
+/* Element types.  QXH_F16 is IEEE binary16, QXH_BF16 is bfloat16; both are
+ * rounded to nearest even on store. */
+typedef enum { QXH_F32 = 0, QXH_F16 = 1, QXH_BF16 = 2 } qxh_dtype;
+
+/* Model attention shapes.
+ * GRANITE: crates/qx-model/src/lib.rs:20-36 (16 q heads, 8 KV heads, d 64,
+ *          softmax scale ATTENTION_MULTIPLIER = 0.015625, consensus RoPE
+ *          theta 1e4 with the pinned inverse-frequency table).
+ * QWEN3:   crates/qx-model/src/lib.rs:305-325 (32 q heads, 4 KV heads,
+ *          d 128, per-head q/k RMSNorm eps 1e-6, RoPE theta 1e6, scale
+ *          1/sqrt(128)). */
+typedef enum { QXH_SHAPE_GRANITE = 0, QXH_SHAPE_QWEN3 = 1 } qxh_shape;
+
+typedef struct {
+    uint32_t q_heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t hidden;      /* model hidden size */
+    float scale;          /* multiplier applied to q.k */
+    float rope_theta;
+    float rms_epsilon;
+    uint32_t qk_norm;     /* 1: per-head RMSNorm of q and k before RoPE */
+} qxh_shape_info;
+
+/* ---- library ------------------------------------------------------------ */
+
+QXH_API int32_t qxh_abi_version(void);
+
+/* Copies the calling thread's last error message (NUL-terminated, truncated
+ * to capacity) and returns its full length. */
+QXH_API size_t qxh_last_error(char* buffer, size_t capacity);
+
+/* Shape constants (crates/qx-model/src/lib.rs:20-36, :305-325). */
+QXH_API int32_t qxh_shape_query(int32_t shape, qxh_shape_info* out);
+
+/* ---- context -------------------------------------------------------------
+ * Replaces platform::MetalContext (crates/qx-metal/src/lib.rs:1628-1696):
+ * owns the device binding, a default stream and cumulative metrics. */
+typedef struct qxh_context qxh_context;
+
+typedef struct {
+    uint64_t graphs;        /* graphs waited on */
+    uint64_t dispatches;    /* kernels enqueued */
+    double gpu_ms;          /* sum of graph GPU time (event pairs) */
+} qxh_metrics;
+
+QXH_API int32_t qxh_context_create(int32_t device, qxh_context** out);
+QXH_API int32_t qxh_context_destroy(qxh_context* ctx);
+/* MetalContext::metrics, crates/qx-metal/src/lib.rs:9604-9618 */
+QXH_API int32_t qxh_context_metrics(const qxh_context* ctx, qxh_metrics* out);
+
+/* ---- graph -----------------------------------------------------------------
+ * Replaces DecodeGraph / SubmittedDecode (crates/qx-metal/src/lib.rs:9404-9514,
+ * begin_decode :9819-9845): ordered work on one HIP stream, bracketed by a
+ * pair of events for GPU time.  `stream` is a hipStream_t (NULL: the
+ * context's stream).  A graph is single-owner, like &mut DecodeGraph. */
+typedef struct qxh_graph qxh_graph;
+
+typedef struct {
+    uint32_t dispatches;
+    float gpu_ms;
+} qxh_graph_metrics;
+
+QXH_API int32_t qxh_graph_begin(qxh_context* ctx, void* stream, qxh_graph** out);
+/* DecodeGraph::submit: record the end event, do not wait. */
+QXH_API int32_t qxh_graph_submit(qxh_graph* graph);
+/* SubmittedDecode::wait: wait, surface errors, report metrics, free graph. */
+QXH_API int32_t qxh_graph_wait(qxh_graph* graph, qxh_graph_metrics* metrics);
+/* DecodeGraph::finish = submit + wait. */
+QXH_API int32_t qxh_graph_finish(qxh_graph* graph, qxh_graph_metrics* metrics);
+/* Release a graph without waiting (work already enqueued still runs). */
+QXH_API int32_t qxh_graph_discard(qxh_graph* graph);
+
+/* HIP-graph capture of everything encoded between capture_begin and
+ * capture_end, for launch-bound loops (replaces one command buffer per token,
+ * docs/qx-current-status.md:56-57).  Host-side KV cursors advance once, at
+ * capture; each replay re-executes the same positions. */
+typedef struct qxh_replay qxh_replay;
+QXH_API int32_t qxh_graph_capture_begin(qxh_graph* graph);
+QXH_API int32_t qxh_graph_capture_end(qxh_graph* graph, qxh_replay** out);
+QXH_API int32_t qxh_replay_launch(qxh_replay* replay, void* stream);
+QXH_API int32_t qxh_replay_destroy(qxh_replay* replay);
+
+/* ---- KV cache ----------------------------------------------------------------
+ * Replaces KvCache (crates/qx-runtime/src/lib.rs:349-431) and the KV arena of
+ * GpuRuntimeBuffers / ExecutionPlan (crates/qx-runtime-v2/src/lib.rs:6584-6664,
+ * :6774-6857).  A preallocated head-major HBM arena for `layers` x
+ * `sequences` caches of `capacity` positions, with one cursor per
+ * (layer, sequence).  Appends must land exactly at the cursor and below
+ * capacity (KvCache::append, crates/qx-runtime/src/lib.rs:382-405). */
+typedef struct qxh_kv_cache qxh_kv_cache;
+
+typedef struct {
+    int32_t shape;        /* qxh_shape */
+    int32_t key_dtype;    /* qxh_dtype of stored K */
+    int32_t value_dtype;  /* qxh_dtype of stored V */
+    uint32_t layers;
+    uint32_t sequences;
+    uint32_t capacity;    /* positions per cache */
+} qxh_kv_desc;
+
+typedef struct {
+    void* keys;                 /* K region base */
+    void* values;               /* V region base */
+    uint64_t head_stride;       /* elements between consecutive kv heads (= capacity*head_dim) */
+    uint64_t sequence_stride;   /* elements between sequences of one layer */
+    uint64_t layer_stride;      /* elements between layers */
+    uint32_t key_elem_bytes;
+    uint32_t value_elem_bytes;
+} qxh_kv_layout;
+
+/* Bytes of arena a descriptor needs (ExecutionPlan::kv_bytes counterpart). */
+QXH_API int32_t qxh_kv_cache_bytes(const qxh_kv_desc* desc, uint64_t* bytes);
+/* `arena` may be caller-owned device memory of at least qxh_kv_cache_bytes
+ * (GpuRuntimeBuffers-style views); NULL makes the library allocate it. */
+QXH_API int32_t qxh_kv_cache_create(qxh_context* ctx, const qxh_kv_desc* desc, void* arena, uint64_t arena_bytes,
+                            qxh_kv_cache** out);
+QXH_API int32_t qxh_kv_cache_destroy(qxh_kv_cache* cache);
+/* KvCache::len */
+QXH_API int32_t qxh_kv_cache_len(const qxh_kv_cache* cache, uint32_t layer, uint32_t sequence, uint32_t* length);
+/* KvCache::reset: every cursor to 0 (no memory traffic). */
+QXH_API int32_t qxh_kv_cache_reset(qxh_kv_cache* cache);
+/* rollback_kv (crates/qx-runtime-v2/src/lib.rs:3271-3285): cursor-only
+ * rewind of every layer of `sequence` to `length` <= current cursor. */
+QXH_API int32_t qxh_kv_cache_rollback(qxh_kv_cache* cache, uint32_t sequence, uint32_t length);
+/* commit_kv (crates/qx-runtime-v2/src/lib.rs:3290-3310) counterpart used for
+ * caches whose rows were written in bulk (fill / store): set every cursor of
+ * `sequence` (UINT32_MAX: all sequences) to `length` <= capacity. */
+QXH_API int32_t qxh_kv_cache_set_len(qxh_kv_cache* cache, uint32_t sequence, uint32_t length);
+QXH_API int32_t qxh_kv_cache_layout(const qxh_kv_cache* cache, qxh_kv_layout* out);
+QXH_API int32_t qxh_kv_cache_desc(const qxh_kv_cache* cache, qxh_kv_desc* out);
+
+/* ---- encoders (enqueue on graph) --------------------------------------------- */
+
+/* Fused RoPE + KV append for `tokens` consecutive positions starting at
+ * `start_position` in each of `sequences` caches (first_sequence...).
+ * Granite: rotate-half consensus RoPE of q (-> query_output) and k, k written
+ * rotated and v raw into the cache slot (encode_rope_kv_for_layer /
+ * encode_rope_kv_batch, crates/qx-metal/src/lib.rs:7959-8174;
+ * kernels/v2_decode.metal:292-443).
+ * Qwen3: per-head RMSNorm then RoPE of q and k, then the store
+ * (encode_qwen_qk_norm_rope + encode_qwen_store_kv,
+ * crates/qx-metal/src/lib.rs:1918-2018).  query_norm/key_norm are 128-float
+ * device vectors, or NULL for unit weights; ignored for Granite.
+ * Inputs are `input_dtype`; the rotated query is written as `output_dtype`.
+ * Every cursor of the batch must equal start_position and advances by tokens. */
+QXH_API int32_t qxh_encode_rope_kv_batch(qxh_graph* graph, qxh_kv_cache* cache, uint32_t layer,
+                                 uint32_t first_sequence, uint32_t sequences, uint32_t start_position,
+                                 uint32_t tokens, const void* query, const void* key, const void* value,
+                                 int32_t input_dtype, const float* query_norm, const float* key_norm,
+                                 void* query_output, int32_t output_dtype);
+
+/* encode_rope_kv_for_layer (crates/qx-metal/src/lib.rs:7959-7983), same
+ * arguments: fp32 q/k/v of one Granite token, sequence 0. */
+QXH_API int32_t qxh_encode_rope_kv_for_layer(qxh_graph* graph, qxh_kv_cache* cache, const float* query,
+                                     const float* key, const float* value, float* query_output,
+                                     uint32_t layer, uint32_t position);
+
+/* encode_qwen_store_kv (crates/qx-metal/src/lib.rs:1968-2018): store K/V rows
+ * without any transform (keys already normalised and rotated). */
+QXH_API int32_t qxh_encode_store_kv(qxh_graph* graph, qxh_kv_cache* cache, uint32_t layer, uint32_t first_sequence,
+                            uint32_t sequences, uint32_t start_position, uint32_t tokens, const void* key,
+                            const void* value, int32_t input_dtype);
+
+/* encode_qwen_qk_norm_rope (crates/qx-metal/src/lib.rs:1918-1966): in-place
+ * per-head RMSNorm + RoPE of one token's q [32][128] and k [4][128]. */
+QXH_API int32_t qxh_encode_qwen_qk_norm_rope(qxh_graph* graph, void* query, void* key, const float* query_norm,
+                                     const float* key_norm, int32_t dtype, uint32_t position);
+
+/* Decode attention: one query token per sequence against positions
+ * [0, length) of each cache (encode_attention_three_stage_for_layer,
+ * crates/qx-metal/src/lib.rs:8341-8382; encode_qwen_gqa_attention :2020-2096).
+ * Split-K online-softmax kernel plus a combine kernel when the context is
+ * split.  `workspace` (>= qxh_attention_workspace_bytes) replaces the
+ * reference's `scores` scratch buffer.  length must not exceed any cursor. */
+QXH_API int32_t qxh_attention_workspace_bytes(const qxh_kv_cache* cache, uint32_t sequences, uint32_t length,
+                                      uint64_t* bytes);
+QXH_API int32_t qxh_encode_attention_for_layer(qxh_graph* graph, qxh_kv_cache* cache, uint32_t layer,
+                                       uint32_t first_sequence, uint32_t sequences, uint32_t length,
+                                       const void* query, int32_t query_dtype, void* output,
+                                       int32_t output_dtype, void* workspace, uint64_t workspace_bytes);
+
+/* Causal prefill attention: query row t of `tokens` (positions
+ * start_position + t) attends to cache positions [0, start_position + t].
+ * The reference runs prompts as repeated decode (crates/qx-runtime/src/lib.rs:1341-1353);
+ * its K-wide verifier attention (encode_attention_batch_with_plan,
+ * crates/qx-metal/src/lib.rs:8206-8267) is the multi-query counterpart.
+ * fp16/bf16 caches run on MFMA with fp32 accumulation. */
+QXH_API int32_t qxh_encode_prefill_attention(qxh_graph* graph, qxh_kv_cache* cache, uint32_t layer, uint32_t sequence,
+                                     uint32_t start_position, uint32_t tokens, const void* query,
+                                     int32_t query_dtype, void* output, int32_t output_dtype);
+
+/* Position-major token rows [count][kv_heads][head_dim] (cache dtypes) out of
+ * the head-major arena, for consumers that read KV by token
+ * (crates/qx-runtime/src/lib.rs:418-430 KvCache::token;
+ * crates/qx-runtime-v2/src/lib.rs:2194-2213; tools/qx-bench/src/main.rs:10994-11025). */
+QXH_API int32_t qxh_encode_kv_gather_token_rows(qxh_graph* graph, const qxh_kv_cache* cache, uint32_t layer,
+                                        uint32_t sequence, uint32_t position_begin, uint32_t count,
+                                        void* keys_out, void* values_out);
+
+/* ---- Granite attention block (attention half of a decoder layer) -----------
+ * GpuRuntimeBuffers::encode_attention_layer_with_plan attention half
+ * (crates/qx-runtime-v2/src/lib.rs:6919-6994) with fp32 dense weights, as the
+ * V1 CPU layer computes it (crates/qx-runtime/src/lib.rs:847-923):
+ * rms_norm -> q/k/v projections -> RoPE + KV append -> attention -> o
+ * projection -> hidden_out = fma(0.22, o, hidden_in). */
+typedef struct {
+    const float* input_norm; /* [1024] */
+    const float* q_proj;     /* [1024][1024] row-major */
+    const float* k_proj;     /* [512][1024] */
+    const float* v_proj;     /* [512][1024] */
+    const float* o_proj;     /* [1024][1024] */
+} qxh_granite_layer_weights;
+
+QXH_API int32_t qxh_granite_block_workspace_bytes(const qxh_kv_cache* cache, uint32_t length, uint64_t* bytes);
+QXH_API int32_t qxh_encode_granite_attention_block(qxh_graph* graph, qxh_kv_cache* cache, uint32_t layer,
+                                           uint32_t position, const qxh_granite_layer_weights* weights,
+                                           const float* hidden_in, float* hidden_out, void* workspace,
+                                           uint64_t workspace_bytes);
+
+/* ---- synthetic data (bench / tests) ------------------------------------------
+ * Counter-based N(0, stddev^2) values (SplitMix64 -> Box-Muller), on device. */
+QXH_API int32_t qxh_encode_fill_normal(qxh_graph* graph, void* data, int32_t dtype, uint64_t count, uint64_t seed,
+                               float stddev);
+/* Fill rows [0, length) of every (layer, sequence, kv_head) cache with
+ * N(0,1) values and set every cursor to `length`. */
+QXH_API int32_t qxh_encode_kv_fill_normal(qxh_graph* graph, qxh_kv_cache* cache, uint64_t seed, uint32_t length);
+
+/* Bit-exactness probe of the device consensus math (the reference's
+ * qx_consensus_math_conformance, kernels/consensus_math.metal:102-112):
+ * for each input x writes bits of exp(x), rsqrt(x), and for
+ * (position, pair) = (inputs_u32[2i], inputs_u32[2i+1]) the RoPE sin/cos. */
+QXH_API int32_t qxh_encode_consensus_conformance(qxh_graph* graph, const float* inputs, const uint32_t* rope_coords,
+                                         uint32_t count, uint32_t* exp_bits, uint32_t* rsqrt_bits,
+                                         uint32_t* sin_bits, uint32_t* cos_bits);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QX_HIP_H */

@@ -1,0 +1,327 @@
+"""ctypes/numpy front end of the CPU oracle (oracle/qx_oracle.c).
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker or the timed CPU baseline,
+never as a product path.  Every function cites the reference source it
+restates; the C file carries the line-by-line citations.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "libqx_oracle.so")
+
+F32, F16, BF16 = 0, 1, 2
+GRANITE_Q_HEADS, GRANITE_KV_HEADS, GRANITE_HEAD_DIM, GRANITE_HIDDEN = 16, 8, 64, 1024
+QWEN_Q_HEADS, QWEN_KV_HEADS, QWEN_HEAD_DIM = 32, 4, 128
+
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc, no contraction)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.qxo_last_error.restype = ctypes.c_char_p
+        L.qxo_f32_to_f16.argtypes = [ctypes.c_float]
+        L.qxo_f32_to_f16.restype = ctypes.c_uint16
+        L.qxo_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.qxo_f16_to_f32.restype = ctypes.c_float
+        L.qxo_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.qxo_f32_to_bf16.restype = ctypes.c_uint16
+        L.qxo_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        L.qxo_bf16_to_f32.restype = ctypes.c_float
+        L.qxo_granite_inverse_frequency_bits.argtypes = [ctypes.c_uint32]
+        L.qxo_granite_inverse_frequency_bits.restype = ctypes.c_uint32
+        L.qxo_exp_f32.argtypes = [ctypes.c_float, _f32p]
+        L.qxo_rsqrt_f32.argtypes = [ctypes.c_float, _f32p]
+        L.qxo_sin_cos_f32.argtypes = [ctypes.c_float, _f32p, _f32p]
+        L.qxo_granite_rope_sin_cos.argtypes = [ctypes.c_uint32, ctypes.c_uint32, _f32p, _f32p]
+        L.qxo_granite_rope_pair.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float,
+                                            ctypes.c_float, _f32p, _f32p]
+        L.qxo_apply_granite_rope.argtypes = [_f32p, _f32p, ctypes.c_uint32]
+        L.qxo_kv_cache_new.argtypes = [ctypes.c_uint32, ctypes.c_int, ctypes.c_int]
+        L.qxo_kv_cache_new.restype = ctypes.c_void_p
+        L.qxo_kv_cache_free.argtypes = [ctypes.c_void_p]
+        L.qxo_kv_cache_free.restype = None
+        L.qxo_kv_cache_len.argtypes = [ctypes.c_void_p]
+        L.qxo_kv_cache_len.restype = ctypes.c_uint32
+        L.qxo_kv_cache_reset.argtypes = [ctypes.c_void_p]
+        L.qxo_kv_cache_reset.restype = None
+        L.qxo_kv_cache_keys.argtypes = [ctypes.c_void_p]
+        L.qxo_kv_cache_keys.restype = _f32p
+        L.qxo_kv_cache_values.argtypes = [ctypes.c_void_p]
+        L.qxo_kv_cache_values.restype = _f32p
+        L.qxo_kv_cache_append.argtypes = [ctypes.c_void_p, ctypes.c_uint32, _f32p, _f32p]
+        L.qxo_kv_cache_extend.argtypes = [ctypes.c_void_p, ctypes.c_uint32, _f32p, _f32p]
+        L.qxo_granite_attend.argtypes = [_f32p, ctypes.c_void_p, ctypes.c_uint32, _f32p]
+        L.qxo_granite_attention_decode.argtypes = [_f32p, _f32p, _f32p, ctypes.c_uint32,
+                                                   ctypes.c_void_p, _f32p]
+        L.qxo_granite_rms_norm.argtypes = [_f32p, _f32p, _f32p]
+        L.qxo_dense_apply.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, _f32p, _f32p]
+        L.qxo_dense_apply.restype = None
+        L.qxo_granite_attention_block.argtypes = [_f32p] * 6 + [ctypes.c_uint32, ctypes.c_void_p, _f32p]
+        L.qxo_qwen_qk_norm_rope.argtypes = [_u16p, _u16p, _f32p, _f32p, ctypes.c_uint32, ctypes.c_int,
+                                            _u16p, _u16p]
+        L.qxo_qwen_qk_norm_rope.restype = None
+        L.qxo_qwen_inverse_frequency.argtypes = [ctypes.c_uint32]
+        L.qxo_qwen_inverse_frequency.restype = ctypes.c_float
+        L.qxo_qwen_gqa_attention.argtypes = [_u16p, _u16p, _u16p, ctypes.c_uint32, ctypes.c_int, _u16p, _f32p]
+        L.qxo_qwen_prefill_rows.argtypes = [_u16p, _u16p, _u16p, ctypes.c_uint32, _u32p, ctypes.c_uint32,
+                                            ctypes.c_int, _u16p, _f32p]
+        L.qxo_granite_prefill_rows.argtypes = [_f32p, ctypes.c_void_p, ctypes.c_uint32, _u32p,
+                                               ctypes.c_uint32, _f32p]
+        _lib = L
+    return _lib
+
+
+class OracleError(RuntimeError):
+    pass
+
+
+def _check(status):
+    if status != 0:
+        raise OracleError(lib().qxo_last_error().decode())
+
+
+def _p(a, ptype=_f32p):
+    return a.ctypes.data_as(ptype)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# --- consensus math (crates/qx-consensus-math/src/lib.rs) --------------------
+
+def exp_f32(x: float):
+    """exp_f32, lib.rs:69-110.  None where the reference returns None."""
+    out = ctypes.c_float()
+    return None if lib().qxo_exp_f32(float(x), ctypes.byref(out)) else out.value
+
+
+def rsqrt_f32(x: float):
+    """rsqrt_f32, lib.rs:113-128."""
+    out = ctypes.c_float()
+    return None if lib().qxo_rsqrt_f32(float(x), ctypes.byref(out)) else out.value
+
+
+def sin_cos_f32(angle: float):
+    """sin_cos_f32, lib.rs:147-189."""
+    s, c = ctypes.c_float(), ctypes.c_float()
+    return None if lib().qxo_sin_cos_f32(float(angle), ctypes.byref(s), ctypes.byref(c)) else (s.value, c.value)
+
+
+def granite_rope_sin_cos(position: int, pair: int):
+    """granite_rope_sin_cos, lib.rs:191-195."""
+    s, c = ctypes.c_float(), ctypes.c_float()
+    r = lib().qxo_granite_rope_sin_cos(position, pair, ctypes.byref(s), ctypes.byref(c))
+    return None if r else (s.value, c.value)
+
+
+def granite_rope_pair(position: int, pair: int, left: float, right: float):
+    """granite_rope_pair, lib.rs:198-207."""
+    f, g = ctypes.c_float(), ctypes.c_float()
+    r = lib().qxo_granite_rope_pair(position, pair, float(left), float(right), ctypes.byref(f), ctypes.byref(g))
+    return None if r else (f.value, g.value)
+
+
+def f32_bits(x) -> int:
+    return int(np.array(x, dtype=np.float32).view(np.uint32))
+
+
+def round_to(a, fmt: int):
+    """Round fp32 values to the storage format (RNE) and back."""
+    a = _f32(a)
+    if fmt == F16:
+        return a.astype(np.float16).astype(np.float32)
+    if fmt == BF16:
+        return bf16_bits_to_f32(f32_to_bf16_bits(a))
+    return a.copy()
+
+
+def f32_to_bf16_bits(a):
+    """Vectorised RNE fp32 -> bfloat16 bits (same rule as qxo_f32_to_bf16)."""
+    x = _f32(a).view(np.uint32).astype(np.uint64)
+    nan = (x & 0x7FFFFFFF) > 0x7F800000
+    r = ((x + 0x7FFF + ((x >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((x[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_bits_to_f32(b):
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def to_bits16(a, fmt: int):
+    return _f32(a).astype(np.float16).view(np.uint16) if fmt == F16 else f32_to_bf16_bits(a)
+
+
+def from_bits16(b, fmt: int):
+    b = np.asarray(b, dtype=np.uint16)
+    return b.view(np.float16).astype(np.float32) if fmt == F16 else bf16_bits_to_f32(b)
+
+
+# --- Granite (crates/qx-runtime/src/lib.rs) ----------------------------------
+
+def apply_granite_rope(query, key, position: int):
+    """apply_granite_rope, lib.rs:434-441.  Returns rotated copies."""
+    q, k = _f32(query).copy(), _f32(key).copy()
+    _check(lib().qxo_apply_granite_rope(_p(q), _p(k), position))
+    return q, k
+
+
+class KvCache:
+    """KvCache, lib.rs:349-431: position-major fp32 rows with a cursor.
+
+    key_format/value_format round values on append (fp16 Metal stores,
+    kernels/v2_decode.metal:445-488); F32 is the reference cache."""
+
+    def __init__(self, capacity: int, key_format: int = F32, value_format: int = F32):
+        self.capacity = capacity
+        self._h = lib().qxo_kv_cache_new(capacity, key_format, value_format)
+        if not self._h:
+            raise MemoryError("oracle KvCache allocation failed")
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.qxo_kv_cache_free(h)
+            self._h = None
+
+    def __len__(self):
+        return lib().qxo_kv_cache_len(self._h)
+
+    def reset(self):
+        lib().qxo_kv_cache_reset(self._h)
+
+    def append(self, position: int, key, value):
+        k, v = _f32(key), _f32(value)
+        _check(lib().qxo_kv_cache_append(self._h, position, _p(k), _p(v)))
+
+    def extend(self, keys, values):
+        """Store pre-rotated position-major rows [n][8][64] at the cursor."""
+        k, v = _f32(keys), _f32(values)
+        n = k.size // (GRANITE_KV_HEADS * GRANITE_HEAD_DIM)
+        _check(lib().qxo_kv_cache_extend(self._h, n, _p(k), _p(v)))
+
+    def keys(self):
+        n = self.capacity * GRANITE_KV_HEADS * GRANITE_HEAD_DIM
+        return np.ctypeslib.as_array(lib().qxo_kv_cache_keys(self._h), shape=(n,)).reshape(
+            self.capacity, GRANITE_KV_HEADS, GRANITE_HEAD_DIM)[: len(self)].copy()
+
+    def values(self):
+        n = self.capacity * GRANITE_KV_HEADS * GRANITE_HEAD_DIM
+        return np.ctypeslib.as_array(lib().qxo_kv_cache_values(self._h), shape=(n,)).reshape(
+            self.capacity, GRANITE_KV_HEADS, GRANITE_HEAD_DIM)[: len(self)].copy()
+
+
+def granite_attention_decode(query, key, value, position: int, cache: KvCache):
+    """granite_attention_decode, lib.rs:444-552 (non-hierarchical)."""
+    q, k, v = _f32(query), _f32(key), _f32(value)
+    out = np.zeros(GRANITE_HIDDEN, np.float32)
+    _check(lib().qxo_granite_attention_decode(_p(q), _p(k), _p(v), position, cache._h, _p(out)))
+    return out
+
+
+def granite_attend(query_rotated, cache: KvCache, length: int):
+    """Attention half of granite_attention_decode (lib.rs:476-549)."""
+    q = _f32(query_rotated)
+    out = np.zeros(GRANITE_HIDDEN, np.float32)
+    _check(lib().qxo_granite_attend(_p(q), cache._h, length, _p(out)))
+    return out
+
+
+def granite_prefill_rows(query_rotated, cache: KvCache, start: int, rows):
+    """Repeated-decode causal prefill (lib.rs:1341-1353): row t attends [0, start+t]."""
+    q = _f32(query_rotated)
+    rows = np.ascontiguousarray(rows, dtype=np.uint32)
+    out = np.zeros((rows.size, GRANITE_HIDDEN), np.float32)
+    _check(lib().qxo_granite_prefill_rows(_p(q), cache._h, start, _p(rows, _u32p), rows.size, _p(out)))
+    return out
+
+
+def granite_rms_norm(hidden, weight):
+    """rms_norm, lib.rs:2406-2414."""
+    h, w = _f32(hidden), _f32(weight)
+    out = np.zeros(GRANITE_HIDDEN, np.float32)
+    _check(lib().qxo_granite_rms_norm(_p(h), _p(w), _p(out)))
+    return out
+
+
+def dense_apply(weight, vector):
+    """DenseMatrix::apply (non-macOS), lib.rs:625-637."""
+    w, x = _f32(weight), _f32(vector)
+    rows, cols = w.shape
+    out = np.zeros(rows, np.float32)
+    lib().qxo_dense_apply(_p(w), rows, cols, _p(x), _p(out))
+    return out
+
+
+def granite_attention_block(hidden, norm_weight, wq, wk, wv, wo, position: int, cache: KvCache):
+    """Attention half of GraniteLayerWeights::decode_with_trace, lib.rs:847-929."""
+    arrs = [_f32(a) for a in (hidden, norm_weight, wq, wk, wv, wo)]
+    out = np.zeros(GRANITE_HIDDEN, np.float32)
+    _check(lib().qxo_granite_attention_block(*[_p(a) for a in arrs], position, cache._h, _p(out)))
+    return out
+
+
+# --- Qwen (tools/qx-qwen-parity/src/main.rs) ---------------------------------
+
+def qwen_qk_norm_rope(query_bits, key_bits, query_norm, key_norm, position: int, fmt: int = F16):
+    """cpu_qk_norm_rope, main.rs:1170-1210 (16-bit I/O in `fmt`)."""
+    q = np.ascontiguousarray(query_bits, dtype=np.uint16)
+    k = np.ascontiguousarray(key_bits, dtype=np.uint16)
+    qn, kn = _f32(query_norm), _f32(key_norm)
+    qo, ko = np.zeros_like(q), np.zeros_like(k)
+    lib().qxo_qwen_qk_norm_rope(_p(q, _u16p), _p(k, _u16p), _p(qn), _p(kn), position, fmt,
+                                _p(qo, _u16p), _p(ko, _u16p))
+    return qo, ko
+
+
+def qwen_inverse_frequencies():
+    return np.array([lib().qxo_qwen_inverse_frequency(i) for i in range(64)], np.float32)
+
+
+def qwen_gqa_attention(query_bits, key_cache_bits, value_cache_bits, fmt: int = F16, want_f32=False):
+    """cpu_gqa_attention, main.rs:1218-1258 (position-major caches)."""
+    q = np.ascontiguousarray(query_bits, dtype=np.uint16)
+    kc = np.ascontiguousarray(key_cache_bits, dtype=np.uint16)
+    vc = np.ascontiguousarray(value_cache_bits, dtype=np.uint16)
+    context = kc.size // (QWEN_KV_HEADS * QWEN_HEAD_DIM)
+    out = np.zeros(QWEN_Q_HEADS * QWEN_HEAD_DIM, np.uint16)
+    of = np.zeros(QWEN_Q_HEADS * QWEN_HEAD_DIM, np.float32)
+    _check(lib().qxo_qwen_gqa_attention(_p(q, _u16p), _p(kc, _u16p), _p(vc, _u16p), context, fmt,
+                                        _p(out, _u16p), _p(of)))
+    return (out, of) if want_f32 else out
+
+
+def qwen_prefill_rows(query_bits, key_cache_bits, value_cache_bits, start: int, rows, fmt: int = F16):
+    """Repeated-decode causal prefill for Qwen; returns (bits, f32) for `rows`."""
+    q = np.ascontiguousarray(query_bits, dtype=np.uint16)
+    kc = np.ascontiguousarray(key_cache_bits, dtype=np.uint16)
+    vc = np.ascontiguousarray(value_cache_bits, dtype=np.uint16)
+    rows = np.ascontiguousarray(rows, dtype=np.uint32)
+    n = QWEN_Q_HEADS * QWEN_HEAD_DIM
+    out = np.zeros((rows.size, n), np.uint16)
+    of = np.zeros((rows.size, n), np.float32)
+    _check(lib().qxo_qwen_prefill_rows(_p(q, _u16p), _p(kc, _u16p), _p(vc, _u16p), start, _p(rows, _u32p),
+                                       rows.size, fmt, _p(out, _u16p), _p(of)))
+    return out, of

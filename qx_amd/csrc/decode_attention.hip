@@ -1,0 +1,324 @@
+// Split-K online-softmax decode attention (flash-decoding) for gfx950.
+//
+// Work decomposition: one workgroup of WAVES wave64s per (context split,
+// kv head, sequence).  The G = q_heads / kv_heads query heads of the group
+// live in registers, so every K and V byte is loaded exactly once per group
+// (the GQA sharing of qx_v2_attention_v_partial_gqa,
+// kernels/v2_decode.metal:1223-1257, extended to QK as well).
+//
+// Lane layout: a K/V row of D elements is LPR lanes x 16 bytes, so one
+// global_load_dwordx4 per lane moves RPW = 64/LPR whole rows per wave.  Each
+// group of LPR lanes owns one row per load; the q.k partial dot of its 16-byte
+// slice is summed across the LPR lanes with DPP, then the lane group keeps a
+// private online-softmax state (m, l, acc[G][16 bytes of dims]) in the log2
+// domain.  After the row loop, row groups merge (xor butterflies), waves merge
+// through LDS, and the workgroup writes either the normalised output (one
+// split) or an (m, l, acc) partial that decode_combine_kernel reduces.
+//
+// The kernel is HBM-bound: the algorithmic traffic per launch is the KV
+// bytes of `length` positions per (sequence, kv head) plus q and the output.
+#include "common.h"
+#include "internal.h"
+
+namespace qxh {
+
+struct DecodeArgs {
+    const void* keys;
+    const void* values;
+    uint64_t head_stride;  // elements
+    uint64_t seq_stride;   // elements
+    const void* query;     // [S][Hq][D]
+    void* out;             // [S][Hq][D]
+    float* ws_ml;          // [S][Hkv][splits][G][2]
+    float* ws_acc;         // [S][Hkv][splits][G][D]
+    uint32_t length;
+    uint32_t chunk;
+    uint32_t splits;
+    int query_dtype;
+    int out_dtype;
+    float qscale;          // softmax scale * log2(e)
+};
+
+constexpr float kNegBig = -1.0e30f;
+
+template <int MASK> __device__ __forceinline__ float xchg(float v) {
+    if constexpr (MASK == 1) return dpp_quad_xor1(v);
+    else if constexpr (MASK == 2) return dpp_quad_xor2(v);
+    else if constexpr (MASK == 8)  // row_ror:8 == xor 8 inside a 16-lane row
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true));
+    else if constexpr (MASK < 32)
+        return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (MASK << 10) | 0x1F));
+    else
+        return bperm_xor(v, MASK);
+}
+
+template <int G, int EPL, int MASK>
+__device__ __forceinline__ void merge_step(float (&m)[G], float (&l)[G], float (&acc)[G][EPL]) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float mo = xchg<MASK>(m[g]);
+        const float lo = xchg<MASK>(l[g]);
+        const float mn = fmaxf(m[g], mo);
+        const float a1 = fast_exp2(m[g] - mn);
+        const float a2 = fast_exp2(mo - mn);
+        l[g] = __builtin_fmaf(l[g], a1, lo * a2);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            const float ao = xchg<MASK>(acc[g][e]);
+            acc[g][e] = __builtin_fmaf(acc[g][e], a1, ao * a2);
+        }
+        m[g] = mn;
+    }
+}
+
+template <int D, int G, int KDT, int WAVES, int UNROLL, bool NT>
+__global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs a) {
+    constexpr int EB = Elem<KDT>::bytes;
+    constexpr int EPL = 16 / EB;
+    constexpr int LPR = D / EPL;
+    constexpr int RPW = 64 / LPR;
+    constexpr int STEP = RPW * UNROLL;
+    static_assert(LPR * EPL == D && RPW * LPR == 64, "row must tile the wave");
+
+    __shared__ float sm_m[WAVES][G];
+    __shared__ float sm_l[WAVES][G];
+    __shared__ float sm_acc[WAVES][G][D];
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int lrow = lane / LPR;
+    const int lcol = (lane % LPR) * EPL;
+    const uint32_t split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    const uint32_t hkv = gridDim.y;
+
+    const uint32_t r0 = split * a.chunk;
+    const uint32_t r1 = min(a.length, r0 + a.chunk);
+    const uint32_t span = r1 > r0 ? r1 - r0 : 0u;
+    const uint32_t wspan = ((span + WAVES - 1) / WAVES + RPW - 1) / RPW * RPW;
+    const uint32_t w0 = r0 + wave * wspan;
+    const uint32_t w1 = min(r1, w0 + wspan);
+
+    const size_t head_off = (size_t)seq * a.seq_stride + (size_t)kvh * a.head_stride;
+    const char* kb = reinterpret_cast<const char*>(a.keys) + head_off * EB;
+    const char* vb = reinterpret_cast<const char*>(a.values) + head_off * EB;
+
+    float q[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e)
+            q[g][e] = load_any(a.query, ((size_t)seq * hkv * G + kvh * G + g) * D + lcol + e, a.query_dtype) *
+                      a.qscale;
+
+    float m[G], l[G], acc[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = kNegBig;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
+    }
+
+    for (uint32_t base = w0; base < w1; base += STEP) {
+        u32x4 kr[UNROLL], vr[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const uint32_t row = base + u * RPW + lrow;
+            const uint32_t rc = row < w1 ? row : w1 - 1;
+            kr[u] = load16<NT>(kb + ((size_t)rc * D + lcol) * EB);
+            vr[u] = load16<NT>(vb + ((size_t)rc * D + lcol) * EB);
+        }
+        float s[UNROLL][G];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            float kf[EPL];
+            Unpack<KDT>::run(kr[u], kf);
+            const bool valid = base + u * RPW + lrow < w1;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) d = __builtin_fmaf(q[g][e], kf[e], d);
+                d = group_sum<LPR>(d);
+                s[u][g] = valid ? d : -INFINITY;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float mb = s[0][g];
+#pragma unroll
+            for (int u = 1; u < UNROLL; ++u) mb = fmaxf(mb, s[u][g]);
+            const float mn = fmaxf(m[g], mb);
+            const float alpha = fast_exp2(m[g] - mn);
+            m[g] = mn;
+            l[g] *= alpha;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            float vf[EPL];
+            Unpack<KDT>::run(vr[u], vf);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float p = fast_exp2(s[u][g] - m[g]);
+                l[g] += p;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[g][e] = __builtin_fmaf(p, vf[e], acc[g][e]);
+            }
+        }
+    }
+
+    // merge the RPW row groups of the wave (lanes sharing lcol)
+    if constexpr (LPR <= 1) merge_step<G, EPL, 1>(m, l, acc);
+    if constexpr (LPR <= 2) merge_step<G, EPL, 2>(m, l, acc);
+    if constexpr (LPR <= 4) merge_step<G, EPL, 4>(m, l, acc);
+    if constexpr (LPR <= 8) merge_step<G, EPL, 8>(m, l, acc);
+    if constexpr (LPR <= 16) merge_step<G, EPL, 16>(m, l, acc);
+    if constexpr (LPR <= 32) merge_step<G, EPL, 32>(m, l, acc);
+
+    if (lrow == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) sm_acc[wave][g][lcol + e] = acc[g][e];
+            if (lcol == 0) {
+                sm_m[wave][g] = m[g];
+                sm_l[wave][g] = l[g];
+            }
+        }
+    }
+    __syncthreads();
+
+    for (int i = threadIdx.x; i < G * D; i += 64 * WAVES) {
+        const int g = i / D, d = i % D;
+        float M = kNegBig;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) M = fmaxf(M, sm_m[w][g]);
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float f = fast_exp2(sm_m[w][g] - M);
+            L = __builtin_fmaf(sm_l[w][g], f, L);
+            A = __builtin_fmaf(sm_acc[w][g][d], f, A);
+        }
+        if (a.splits == 1) {
+            store_any(a.out, ((size_t)seq * hkv * G + kvh * G + g) * D + d, A / L, a.out_dtype);
+        } else {
+            const size_t p = (((size_t)seq * hkv + kvh) * a.splits + split) * G + g;
+            a.ws_acc[p * D + d] = A;
+            if (d == 0) {
+                a.ws_ml[2 * p] = M;
+                a.ws_ml[2 * p + 1] = L;
+            }
+        }
+    }
+}
+
+// Reduce the per-split partials: out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
+// grid (q_heads, sequences), block D.
+template <int D, int G>
+__global__ __launch_bounds__(D) void decode_combine_kernel(DecodeArgs a) {
+    const uint32_t hq = blockIdx.x, seq = blockIdx.y;
+    const uint32_t hkv = gridDim.x / G;
+    const uint32_t kvh = hq / G, g = hq % G;
+    const int d = threadIdx.x;
+    const size_t p0 = ((size_t)seq * hkv + kvh) * a.splits * G + g;
+    float M = kNegBig;
+    for (uint32_t s = 0; s < a.splits; ++s) M = fmaxf(M, a.ws_ml[2 * (p0 + (size_t)s * G)]);
+    float L = 0.0f, A = 0.0f;
+    for (uint32_t s = 0; s < a.splits; ++s) {
+        const size_t p = p0 + (size_t)s * G;
+        const float f = fast_exp2(a.ws_ml[2 * p] - M);
+        L = __builtin_fmaf(a.ws_ml[2 * p + 1], f, L);
+        A = __builtin_fmaf(a.ws_acc[p * D + d], f, A);
+    }
+    store_any(a.out, ((size_t)seq * gridDim.x + hq) * D + d, A / L, a.out_dtype);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+constexpr int kWaves = 4;
+constexpr int kUnroll = 4;
+
+static int rows_per_wave_load(int head_dim, int key_dtype) {
+    const int eb = key_dtype == F32 ? 4 : 2;
+    const int lpr = head_dim * eb / 16;
+    return 64 / lpr;
+}
+
+DecodePlan plan_decode(const ShapeDims& s, int key_dtype, uint32_t sequences, uint32_t length) {
+    DecodePlan p{};
+    p.waves = kWaves;
+    const uint32_t rpw = (uint32_t)rows_per_wave_load(s.head_dim, key_dtype);
+    const uint32_t step = rpw * kUnroll;
+    const uint32_t units = sequences * (uint32_t)s.kv_heads;
+    const uint32_t target_wgs = 2048;
+    // keep the (m, l, acc) partial small next to the KV bytes it summarises
+    uint32_t min_chunk = kWaves * step;
+    if (s.group >= 8 && min_chunk < 256) min_chunk = 256;
+    uint32_t want = (target_wgs + units - 1) / units;
+    uint32_t cap = (length + min_chunk - 1) / min_chunk;
+    uint32_t splits = want < cap ? want : cap;
+    if (splits < 1) splits = 1;
+    const uint32_t gran = kWaves * rpw;
+    uint32_t chunk = (length + splits - 1) / splits;
+    chunk = (chunk + gran - 1) / gran * gran;
+    splits = (length + chunk - 1) / chunk;
+    if (splits < 1) splits = 1;
+    p.splits = splits;
+    p.chunk = chunk;
+    p.workspace_bytes = splits > 1 ? (uint64_t)units * splits * s.group * (s.head_dim + 2) * sizeof(float) : 0;
+    return p;
+}
+
+template <int D, int G, int KDT>
+static void launch_typed(const DecodeArgs& a, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL((decode_attention_kernel<D, G, KDT, kWaves, kUnroll, true>), grid, dim3(64 * kWaves), 0, st,
+                       a);
+}
+
+hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t sequences,
+                                   uint32_t length, const void* query, int query_dtype, void* out, int out_dtype,
+                                   void* workspace, hipStream_t st, int* dispatches) {
+    DecodeArgs a{};
+    a.keys = kv.keys;
+    a.values = kv.values;
+    a.head_stride = kv.head_stride;
+    a.seq_stride = kv.sequence_stride;
+    a.query = query;
+    a.out = out;
+    a.length = length;
+    a.chunk = p.chunk;
+    a.splits = p.splits;
+    a.query_dtype = query_dtype;
+    a.out_dtype = out_dtype;
+    a.qscale = s.scale * kLog2e;
+    if (p.splits > 1) {
+        const uint64_t parts = (uint64_t)sequences * s.kv_heads * p.splits * s.group;
+        a.ws_ml = reinterpret_cast<float*>(workspace);
+        a.ws_acc = a.ws_ml + 2 * parts;
+    }
+    dim3 grid(p.splits, s.kv_heads, sequences);
+    const int kd = kv.key_dtype;
+    if (s.head_dim == 64 && s.group == 2) {
+        if (kd == F32) launch_typed<64, 2, F32>(a, grid, st);
+        else if (kd == F16) launch_typed<64, 2, F16>(a, grid, st);
+        else launch_typed<64, 2, BF16>(a, grid, st);
+        if (p.splits > 1)
+            hipLaunchKernelGGL((decode_combine_kernel<64, 2>), dim3(s.q_heads, sequences), dim3(64), 0, st, a);
+    } else if (s.head_dim == 128 && s.group == 8) {
+        if (kd == F32) launch_typed<128, 8, F32>(a, grid, st);
+        else if (kd == F16) launch_typed<128, 8, F16>(a, grid, st);
+        else launch_typed<128, 8, BF16>(a, grid, st);
+        if (p.splits > 1)
+            hipLaunchKernelGGL((decode_combine_kernel<128, 8>), dim3(s.q_heads, sequences), dim3(128), 0, st, a);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    *dispatches = p.splits > 1 ? 2 : 1;
+    return hipGetLastError();
+}
+
+}  // namespace qxh

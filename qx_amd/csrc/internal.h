@@ -1,0 +1,92 @@
+// Host-side launch interface between the C-ABI layer (runtime.hip) and the
+// kernel translation units.  Launchers validate nothing: runtime.hip checks
+// every shape, pointer and cursor before it calls them.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qxh {
+
+struct ShapeDims {
+    int q_heads;
+    int kv_heads;
+    int head_dim;
+    int group;       // q_heads / kv_heads
+    float scale;     // multiplier on q.k
+    int shape_id;    // QXH_SHAPE_*
+};
+
+// KV arena geometry for one layer: K/V bases already offset to the layer and
+// the first sequence of a launch.
+struct KvLayer {
+    void* keys;
+    void* values;
+    uint64_t head_stride;      // elements between kv heads (capacity * head_dim)
+    uint64_t sequence_stride;  // elements between sequences
+    int key_dtype;
+    int value_dtype;
+    uint32_t capacity;
+};
+
+struct RopeAppendArgs {
+    const void* query;   // [seq][tokens][q_heads][d]
+    const void* key;     // [seq][tokens][kv_heads][d]
+    const void* value;
+    void* query_out;     // may be null (store-only)
+    const float* query_norm;  // Qwen: per-dim weights (null = 1)
+    const float* key_norm;
+    int input_dtype;
+    int output_dtype;
+    uint32_t start_position;
+    uint32_t tokens;
+    uint32_t sequences;
+    int mode;            // 0: Granite RoPE+append, 1: Qwen norm+RoPE+append, 2: store only
+    float qwen_inv_freq[64];
+};
+
+hipError_t launch_rope_append(const ShapeDims& s, const KvLayer& kv, const RopeAppendArgs& a, hipStream_t st);
+hipError_t launch_qwen_qk_norm_rope(void* q, void* k, const float* qn, const float* kn, int dtype, uint32_t position,
+                                    const float* inv_freq64, hipStream_t st);
+hipError_t launch_kv_gather(const ShapeDims& s, const KvLayer& kv, uint32_t pos_begin, uint32_t count, void* keys_out,
+                            void* values_out, hipStream_t st);
+hipError_t launch_fill_normal(void* data, int dtype, uint64_t count, uint64_t seed, float stddev, hipStream_t st);
+hipError_t launch_kv_fill_normal(const ShapeDims& s, const KvLayer& kv_all_layers_seq0, uint32_t layers, uint32_t sequences,
+                                 uint64_t layer_stride, uint32_t length, uint64_t seed, hipStream_t st);
+hipError_t launch_conformance(const float* in, const uint32_t* coords, uint32_t n, uint32_t* e, uint32_t* r, uint32_t* sn,
+                              uint32_t* cs, hipStream_t st);
+
+// Decode attention plan chosen on the host.
+struct DecodePlan {
+    uint32_t splits;        // context splits per (sequence, kv_head)
+    uint32_t chunk;         // positions per split
+    uint64_t workspace_bytes;
+    int waves;              // waves per workgroup
+};
+
+DecodePlan plan_decode(const ShapeDims& s, int key_dtype, uint32_t sequences, uint32_t length);
+hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t sequences,
+                                   uint32_t length, const void* query, int query_dtype, void* out, int out_dtype,
+                                   void* workspace, hipStream_t st, int* dispatches);
+
+hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint32_t start_position, uint32_t tokens,
+                                    const void* query, int query_dtype, void* out, int out_dtype, hipStream_t st,
+                                    int* dispatches);
+
+// Granite attention block (fp32 dense weights).
+struct GraniteBlockArgs {
+    const float* input_norm;
+    const float* wq;
+    const float* wk;
+    const float* wv;
+    const float* wo;
+    const float* hidden_in;
+    float* hidden_out;
+    float* query_rot;   // workspace [1024]
+    float* attention;   // workspace [1024]
+    uint32_t position;
+};
+hipError_t launch_granite_qkv_rope(const ShapeDims& s, const KvLayer& kv, const GraniteBlockArgs& a, hipStream_t st);
+hipError_t launch_granite_out_residual(const GraniteBlockArgs& a, hipStream_t st);
+
+}  // namespace qxh

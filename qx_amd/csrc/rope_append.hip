@@ -1,0 +1,302 @@
+// RoPE + KV append, store-only append, token-row gather, synthetic fills and
+// the consensus-math conformance probe.
+//
+// Granite path (kernels/v2_decode.metal:292-443 counterparts): one thread per
+// rotary pair (i, i+32).  The query pair is rotated into query_out; the key
+// pair is rotated and written straight into its head-major cache slot, and the
+// value pair is copied (rounded to the cache dtype) into the same slot.  The
+// rotation is the reference's fma(-y, s, x*c), fma(y, c, x*s) with consensus
+// sin/cos, so fp32 caches are bit-identical to KvCache::append of the
+// rotated key (crates/qx-runtime/src/lib.rs:464-475).
+//
+// Qwen path (kernels/qwen_attention.metal:62-75, :138-177 counterparts): one
+// wave per head; lane l owns dims l and l+64.  Per-head RMSNorm, rotate-half
+// RoPE with host-provided inverse frequencies, output rounded to the I/O
+// dtype, key written into the cache slot, value copied.
+#include "common.h"
+#include "consensus_math.h"
+#include "internal.h"
+
+namespace qxh {
+
+// ---------------------------------------------------------------------------
+// Granite: consensus RoPE of q and k, K/V append.  grid (tokens, sequences).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void granite_rope_append_kernel(KvLayer kv, RopeAppendArgs a, int q_heads,
+                                                                  int kv_heads) {
+    constexpr int D = 64, P = 32;
+    const uint32_t t = blockIdx.x, s = blockIdx.y;
+    const uint32_t pos = a.start_position + t;
+    const size_t tok = (size_t)s * a.tokens + t;
+    const int pairs = (q_heads + kv_heads) * P;
+    for (int i = threadIdx.x; i < pairs; i += blockDim.x) {
+        const int head = i / P, pair = i % P;
+        float sn, cs;
+        granite_rope_sin_cos(pos, (uint32_t)pair, sn, cs);
+        if (head < q_heads) {
+            if (!a.query_out) continue;
+            const size_t base = (tok * q_heads + head) * D;
+            const float x = load_any(a.query, base + pair, a.input_dtype);
+            const float y = load_any(a.query, base + P + pair, a.input_dtype);
+            store_any(a.query_out, base + pair, __builtin_fmaf(-y, sn, x * cs), a.output_dtype);
+            store_any(a.query_out, base + P + pair, __builtin_fmaf(y, cs, x * sn), a.output_dtype);
+        } else {
+            const int h = head - q_heads;
+            const size_t src = (tok * kv_heads + h) * D;
+            const size_t dst = (size_t)s * kv.sequence_stride + (size_t)h * kv.head_stride + (size_t)pos * D;
+            const float x = load_any(a.key, src + pair, a.input_dtype);
+            const float y = load_any(a.key, src + P + pair, a.input_dtype);
+            store_any(kv.keys, dst + pair, __builtin_fmaf(-y, sn, x * cs), kv.key_dtype);
+            store_any(kv.keys, dst + P + pair, __builtin_fmaf(y, cs, x * sn), kv.key_dtype);
+            store_any(kv.values, dst + pair, load_any(a.value, src + pair, a.input_dtype), kv.value_dtype);
+            store_any(kv.values, dst + P + pair, load_any(a.value, src + P + pair, a.input_dtype), kv.value_dtype);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Qwen: per-head RMSNorm + RoPE.  grid (ceil(heads/4), tokens, sequences),
+// block 256 = 4 waves, one head per wave.  Heads [0, q_heads) are query
+// heads, [q_heads, q_heads + kv_heads) key heads.  With `kv.keys` null the
+// key is rotated in place (the reference's in-place encode_qwen_qk_norm_rope).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void qwen_norm_rope_append_kernel(KvLayer kv, RopeAppendArgs a, int q_heads,
+                                                                    int kv_heads, void* key_inplace) {
+    constexpr int D = 128, P = 64;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int head = blockIdx.x * 4 + wave;
+    if (head >= q_heads + kv_heads) return;
+    const uint32_t t = blockIdx.y, s = blockIdx.z;
+    const uint32_t pos = a.start_position + t;
+    const size_t tok = (size_t)s * a.tokens + t;
+    const bool is_q = head < q_heads;
+    const int h = is_q ? head : head - q_heads;
+    const void* src = is_q ? a.query : a.key;
+    const size_t base = is_q ? (tok * q_heads + h) * D : (tok * kv_heads + h) * D;
+    const float xl = load_any(src, base + lane, a.input_dtype);
+    const float xr = load_any(src, base + P + lane, a.input_dtype);
+    float ss = xl * xl + xr * xr;
+    ss = group_sum<64>(ss);
+    const float inv_rms = 1.0f / __builtin_sqrtf(ss / 128.0f + 1.0e-6f);
+    const float* norm = is_q ? a.query_norm : a.key_norm;
+    const float nl = norm ? norm[lane] : 1.0f;
+    const float nr = norm ? norm[P + lane] : 1.0f;
+    const float left = xl * inv_rms * nl;
+    const float right = xr * inv_rms * nr;
+    const float angle = (float)pos * a.qwen_inv_freq[lane];
+    float sn, cs;
+    sincosf(angle, &sn, &cs);
+    const float o_l = left * cs - right * sn;
+    const float o_r = right * cs + left * sn;
+    if (is_q) {
+        if (a.query_out) {
+            store_any(a.query_out, base + lane, o_l, a.output_dtype);
+            store_any(a.query_out, base + P + lane, o_r, a.output_dtype);
+        }
+        return;
+    }
+    if (key_inplace) {
+        store_any(key_inplace, base + lane, o_l, a.input_dtype);
+        store_any(key_inplace, base + P + lane, o_r, a.input_dtype);
+        return;
+    }
+    const size_t dst = (size_t)s * kv.sequence_stride + (size_t)h * kv.head_stride + (size_t)pos * D;
+    store_any(kv.keys, dst + lane, o_l, kv.key_dtype);
+    store_any(kv.keys, dst + P + lane, o_r, kv.key_dtype);
+    store_any(kv.values, dst + lane, load_any(a.value, base + lane, a.input_dtype), kv.value_dtype);
+    store_any(kv.values, dst + P + lane, load_any(a.value, base + P + lane, a.input_dtype), kv.value_dtype);
+}
+
+// ---------------------------------------------------------------------------
+// Store-only append (encode_qwen_store_kv counterpart).  grid (tokens, sequences).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void store_kv_kernel(KvLayer kv, RopeAppendArgs a, int kv_heads, int head_dim) {
+    const uint32_t t = blockIdx.x, s = blockIdx.y;
+    const uint32_t pos = a.start_position + t;
+    const size_t tok = (size_t)s * a.tokens + t;
+    const int n = kv_heads * head_dim;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int h = i / head_dim, d = i % head_dim;
+        const size_t src = tok * n + i;
+        const size_t dst = (size_t)s * kv.sequence_stride + (size_t)h * kv.head_stride + (size_t)pos * head_dim + d;
+        store_any(kv.keys, dst, load_any(a.key, src, a.input_dtype), kv.key_dtype);
+        store_any(kv.values, dst, load_any(a.value, src, a.input_dtype), kv.value_dtype);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Token-row gather: head-major arena -> position-major [count][kv_heads][d],
+// bit copies in the cache dtypes.  grid (count, kv_heads).
+// ---------------------------------------------------------------------------
+template <typename KT, typename VT>
+__global__ __launch_bounds__(128) void kv_gather_kernel(KvLayer kv, uint32_t pos_begin, int kv_heads, int head_dim,
+                                                        KT* __restrict__ k_out, VT* __restrict__ v_out) {
+    const uint32_t t = blockIdx.x;
+    const int h = blockIdx.y;
+    const size_t src = (size_t)h * kv.head_stride + (size_t)(pos_begin + t) * head_dim;
+    const size_t dst = ((size_t)t * kv_heads + h) * head_dim;
+    const KT* ks = reinterpret_cast<const KT*>(kv.keys);
+    const VT* vs = reinterpret_cast<const VT*>(kv.values);
+    for (int d = threadIdx.x; d < head_dim; d += blockDim.x) {
+        if (k_out) k_out[dst + d] = ks[src + d];
+        if (v_out) v_out[dst + d] = vs[src + d];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic N(0, stddev^2): SplitMix64 counter hash -> Box-Muller.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+__device__ __forceinline__ void normal_pair(uint64_t seed, uint64_t counter, float& z0, float& z1) {
+    const uint64_t h = splitmix64(seed ^ splitmix64(counter));
+    const float u1 = ((float)(h >> 40) + 1.0f) * 5.9604644775390625e-8f;  // (0, 1]
+    const float u2 = (float)((h >> 16) & 0xffffffu) * 5.9604644775390625e-8f;
+    const float r = __builtin_sqrtf(-2.0f * logf(u1));
+    float sn, cs;
+    sincosf(6.283185307179586f * u2, &sn, &cs);
+    z0 = r * cs;
+    z1 = r * sn;
+}
+
+__global__ __launch_bounds__(256) void fill_normal_kernel(void* data, int dtype, uint64_t count, uint64_t seed,
+                                                          float stddev) {
+    const uint64_t pairs = (count + 1) / 2;
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < pairs;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        float z0, z1;
+        normal_pair(seed, i, z0, z1);
+        store_any(data, 2 * i, z0 * stddev, dtype);
+        if (2 * i + 1 < count) store_any(data, 2 * i + 1, z1 * stddev, dtype);
+    }
+}
+
+// Every (layer, sequence, kv head) block of the arena is contiguous in
+// head_stride units, so block index hb = (layer*S + s)*H + h addresses it.
+__global__ __launch_bounds__(256) void kv_fill_normal_kernel(KvLayer kv, uint64_t blocks, int head_dim,
+                                                             uint32_t length, uint64_t seed) {
+    const uint64_t half_d = (uint64_t)head_dim / 2;
+    const uint64_t total = blocks * length * half_d;
+    for (uint64_t e = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; e < total;
+         e += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t pr = e % half_d;
+        const uint64_t row = (e / half_d) % length;
+        const uint64_t hb = e / half_d / length;
+        const size_t off = hb * kv.head_stride + row * head_dim + 2 * pr;
+        const uint64_t ctr = (hb * kv.capacity + row) * half_d + pr;
+        float a, b;
+        normal_pair(seed, ctr, a, b);
+        store_any(kv.keys, off, a, kv.key_dtype);
+        store_any(kv.keys, off + 1, b, kv.key_dtype);
+        normal_pair(seed ^ 0x5DEECE66DA5A5A5Aull, ctr, a, b);
+        store_any(kv.values, off, a, kv.value_dtype);
+        store_any(kv.values, off + 1, b, kv.value_dtype);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Consensus-math conformance (kernels/consensus_math.metal:102-112 counterpart).
+// ---------------------------------------------------------------------------
+__global__ void conformance_kernel(const float* in, const uint32_t* coords, uint32_t n, uint32_t* e, uint32_t* r,
+                                   uint32_t* sn, uint32_t* cs) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    e[i] = __float_as_uint(consensus_exp(in[i]));
+    r[i] = __float_as_uint(consensus_rsqrt(in[i]));
+    float s = __builtin_nanf(""), c = __builtin_nanf("");
+    if (coords[2 * i + 1] < 32) granite_rope_sin_cos(coords[2 * i], coords[2 * i + 1], s, c);
+    sn[i] = __float_as_uint(s);
+    cs[i] = __float_as_uint(c);
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+hipError_t launch_rope_append(const ShapeDims& s, const KvLayer& kv, const RopeAppendArgs& a, hipStream_t st) {
+    if (a.mode == 0) {
+        dim3 grid(a.tokens, a.sequences);
+        hipLaunchKernelGGL(granite_rope_append_kernel, grid, dim3(256), 0, st, kv, a, s.q_heads, s.kv_heads);
+    } else if (a.mode == 1) {
+        dim3 grid((s.q_heads + s.kv_heads + 3) / 4, a.tokens, a.sequences);
+        hipLaunchKernelGGL(qwen_norm_rope_append_kernel, grid, dim3(256), 0, st, kv, a, s.q_heads, s.kv_heads,
+                           (void*)nullptr);
+    } else {
+        dim3 grid(a.tokens, a.sequences);
+        hipLaunchKernelGGL(store_kv_kernel, grid, dim3(256), 0, st, kv, a, s.kv_heads, s.head_dim);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_qwen_qk_norm_rope(void* q, void* k, const float* qn, const float* kn, int dtype, uint32_t position,
+                                    const float* inv_freq64, hipStream_t st) {
+    RopeAppendArgs a{};
+    a.query = q;
+    a.key = k;
+    a.query_out = q;
+    a.query_norm = qn;
+    a.key_norm = kn;
+    a.input_dtype = dtype;
+    a.output_dtype = dtype;
+    a.start_position = position;
+    a.tokens = 1;
+    a.sequences = 1;
+    a.mode = 1;
+    for (int i = 0; i < 64; ++i) a.qwen_inv_freq[i] = inv_freq64[i];
+    KvLayer kv{};
+    hipLaunchKernelGGL(qwen_norm_rope_append_kernel, dim3(9, 1, 1), dim3(256), 0, st, kv, a, 32, 4, k);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_gather(const ShapeDims& s, const KvLayer& kv, uint32_t pos_begin, uint32_t count, void* keys_out,
+                            void* values_out, hipStream_t st) {
+    dim3 grid(count, s.kv_heads);
+    const int kb = kv.key_dtype == F32 ? 4 : 2, vb = kv.value_dtype == F32 ? 4 : 2;
+    if (kb == 4 && vb == 4)
+        hipLaunchKernelGGL((kv_gather_kernel<uint32_t, uint32_t>), grid, dim3(128), 0, st, kv, pos_begin, s.kv_heads,
+                           s.head_dim, (uint32_t*)keys_out, (uint32_t*)values_out);
+    else if (kb == 4)
+        hipLaunchKernelGGL((kv_gather_kernel<uint32_t, uint16_t>), grid, dim3(128), 0, st, kv, pos_begin, s.kv_heads,
+                           s.head_dim, (uint32_t*)keys_out, (uint16_t*)values_out);
+    else if (vb == 4)
+        hipLaunchKernelGGL((kv_gather_kernel<uint16_t, uint32_t>), grid, dim3(128), 0, st, kv, pos_begin, s.kv_heads,
+                           s.head_dim, (uint16_t*)keys_out, (uint32_t*)values_out);
+    else
+        hipLaunchKernelGGL((kv_gather_kernel<uint16_t, uint16_t>), grid, dim3(128), 0, st, kv, pos_begin, s.kv_heads,
+                           s.head_dim, (uint16_t*)keys_out, (uint16_t*)values_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_normal(void* data, int dtype, uint64_t count, uint64_t seed, float stddev, hipStream_t st) {
+    const uint64_t pairs = (count + 1) / 2;
+    uint64_t blocks = (pairs + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks == 0) blocks = 1;
+    hipLaunchKernelGGL(fill_normal_kernel, dim3((unsigned)blocks), dim3(256), 0, st, data, dtype, count, seed, stddev);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_fill_normal(const ShapeDims& s, const KvLayer& kv, uint32_t layers, uint32_t sequences,
+                                 uint64_t layer_stride, uint32_t length, uint64_t seed, hipStream_t st) {
+    (void)layer_stride;
+    const uint64_t blocks_hb = (uint64_t)layers * sequences * s.kv_heads;
+    const uint64_t total = blocks_hb * length * (s.head_dim / 2);
+    uint64_t blocks = (total + 255) / 256;
+    if (blocks > 262144) blocks = 262144;
+    if (blocks == 0) blocks = 1;
+    hipLaunchKernelGGL(kv_fill_normal_kernel, dim3((unsigned)blocks), dim3(256), 0, st, kv, blocks_hb, s.head_dim,
+                       length, seed);
+    return hipGetLastError();
+}
+
+hipError_t launch_conformance(const float* in, const uint32_t* coords, uint32_t n, uint32_t* e, uint32_t* r,
+                              uint32_t* sn, uint32_t* cs, hipStream_t st) {
+    hipLaunchKernelGGL(conformance_kernel, dim3((n + 255) / 256), dim3(256), 0, st, in, coords, n, e, r, sn, cs);
+    return hipGetLastError();
+}
+
+}  // namespace qxh

@@ -1,0 +1,748 @@
+// C-ABI layer of libqx_hip: contexts, graphs (HIP stream + event pair),
+// the head-major KV arena with its cursors, and the validated encoders.
+//
+// Validation mirrors the reference boundary: every encoder checks shapes,
+// sizes and cursors first and returns an error code with a message instead of
+// enqueueing anything (the Err(String) paths of crates/qx-metal/src/lib.rs,
+// e.g. :1927-1935, :1981-1987, :2032-2039, :8124-8132, and KvCache::append,
+// crates/qx-runtime/src/lib.rs:382-405).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/qx_hip.h"
+#include "internal.h"
+
+using namespace qxh;
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+static thread_local std::string g_error;
+
+static int32_t fail(int32_t code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+static int32_t hip_fail(hipError_t e, const char* what) {
+    return fail(QXH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define QXH_REQUIRE(cond, code, ...)          \
+    do {                                      \
+        if (!(cond)) return fail(code, __VA_ARGS__); \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// objects
+// ---------------------------------------------------------------------------
+struct qxh_context {
+    int device;
+    hipStream_t stream;
+    std::mutex mu;
+    qxh_metrics metrics;
+};
+
+struct qxh_graph {
+    qxh_context* ctx;
+    hipStream_t stream;
+    hipEvent_t start;
+    hipEvent_t end;
+    uint32_t dispatches;
+    bool submitted;
+    bool capturing;
+};
+
+struct qxh_replay {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+struct qxh_kv_cache {
+    qxh_context* ctx;
+    qxh_kv_desc desc;
+    ShapeDims dims;
+    char* arena;
+    uint64_t arena_bytes;
+    bool owned;
+    uint64_t head_stride, seq_stride, layer_stride;  // elements
+    uint64_t key_region_bytes;
+    std::vector<uint32_t> cursor;  // [layer][sequence]
+    uint32_t& at(uint32_t layer, uint32_t seq) { return cursor[(size_t)layer * desc.sequences + seq]; }
+};
+
+static bool shape_dims(int32_t shape, ShapeDims* d) {
+    if (shape == QXH_SHAPE_GRANITE) {
+        *d = ShapeDims{16, 8, 64, 2, 0.015625f, QXH_SHAPE_GRANITE};
+        return true;
+    }
+    if (shape == QXH_SHAPE_QWEN3) {
+        *d = ShapeDims{32, 4, 128, 8, 1.0f / std::sqrt(128.0f), QXH_SHAPE_QWEN3};
+        return true;
+    }
+    return false;
+}
+
+static bool valid_dtype(int32_t dt) { return dt == QXH_F32 || dt == QXH_F16 || dt == QXH_BF16; }
+static uint32_t dtype_bytes(int32_t dt) { return dt == QXH_F32 ? 4u : 2u; }
+static uint64_t align256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
+
+// Qwen RoPE inverse frequencies formed exactly as the reference CPU path does,
+// 1e6_f32.powf(-(i as f32) / 64.0) (tools/qx-qwen-parity/src/main.rs:1193).
+static void qwen_inverse_frequencies(float* out) {
+    for (int i = 0; i < 64; ++i) out[i] = powf(1000000.0f, -(float)i / 64.0f);
+}
+
+// ---------------------------------------------------------------------------
+// library
+// ---------------------------------------------------------------------------
+extern "C" int32_t qxh_abi_version(void) { return QXH_ABI_VERSION; }
+
+extern "C" size_t qxh_last_error(char* buffer, size_t capacity) {
+    if (buffer && capacity) {
+        size_t n = g_error.size() < capacity - 1 ? g_error.size() : capacity - 1;
+        memcpy(buffer, g_error.data(), n);
+        buffer[n] = '\0';
+    }
+    return g_error.size();
+}
+
+extern "C" int32_t qxh_shape_query(int32_t shape, qxh_shape_info* out) {
+    QXH_REQUIRE(out, QXH_ERR_INVALID_ARGUMENT, "shape_query: null output");
+    if (shape == QXH_SHAPE_GRANITE) {
+        *out = qxh_shape_info{16, 8, 64, 1024, 0.015625f, 10000.0f, 1e-6f, 0};
+        return QXH_OK;
+    }
+    if (shape == QXH_SHAPE_QWEN3) {
+        *out = qxh_shape_info{32, 4, 128, 2048, 1.0f / std::sqrt(128.0f), 1000000.0f, 1e-6f, 1};
+        return QXH_OK;
+    }
+    return fail(QXH_ERR_INVALID_ARGUMENT, "unknown shape %d", shape);
+}
+
+// ---------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------
+extern "C" int32_t qxh_context_create(int32_t device, qxh_context** out) {
+    QXH_REQUIRE(out, QXH_ERR_INVALID_ARGUMENT, "context_create: null output");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0) return fail(QXH_ERR_NO_DEVICE, "no HIP device available");
+    QXH_REQUIRE(device >= 0 && device < count, QXH_ERR_INVALID_ARGUMENT, "device %d out of range [0, %d)", device,
+                count);
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(QXH_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
+    if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+    qxh_context* c = new qxh_context();
+    c->device = device;
+    c->metrics = qxh_metrics{0, 0, 0.0};
+    if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) {
+        delete c;
+        return hip_fail(e, "hipStreamCreate");
+    }
+    *out = c;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_context_destroy(qxh_context* ctx) {
+    if (!ctx) return QXH_OK;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_context_metrics(const qxh_context* ctx, qxh_metrics* out) {
+    QXH_REQUIRE(ctx && out, QXH_ERR_INVALID_ARGUMENT, "context_metrics: null argument");
+    std::lock_guard<std::mutex> g(const_cast<qxh_context*>(ctx)->mu);
+    *out = ctx->metrics;
+    return QXH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// graph
+// ---------------------------------------------------------------------------
+extern "C" int32_t qxh_graph_begin(qxh_context* ctx, void* stream, qxh_graph** out) {
+    QXH_REQUIRE(ctx && out, QXH_ERR_INVALID_ARGUMENT, "graph_begin: null argument");
+    *out = nullptr;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    qxh_graph* g = new qxh_graph();
+    g->ctx = ctx;
+    g->stream = stream ? (hipStream_t)stream : ctx->stream;
+    g->dispatches = 0;
+    g->submitted = false;
+    g->capturing = false;
+    if ((e = hipEventCreate(&g->start)) != hipSuccess) {
+        delete g;
+        return hip_fail(e, "hipEventCreate");
+    }
+    if ((e = hipEventCreate(&g->end)) != hipSuccess) {
+        (void)hipEventDestroy(g->start);
+        delete g;
+        return hip_fail(e, "hipEventCreate");
+    }
+    if ((e = hipEventRecord(g->start, g->stream)) != hipSuccess) {
+        (void)hipEventDestroy(g->start);
+        (void)hipEventDestroy(g->end);
+        delete g;
+        return hip_fail(e, "hipEventRecord");
+    }
+    *out = g;
+    return QXH_OK;
+}
+
+static void graph_free(qxh_graph* g) {
+    (void)hipEventDestroy(g->start);
+    (void)hipEventDestroy(g->end);
+    delete g;
+}
+
+extern "C" int32_t qxh_graph_submit(qxh_graph* g) {
+    QXH_REQUIRE(g, QXH_ERR_INVALID_ARGUMENT, "graph_submit: null graph");
+    QXH_REQUIRE(!g->submitted, QXH_ERR_INVALID_ARGUMENT, "graph already submitted");
+    QXH_REQUIRE(!g->capturing, QXH_ERR_INVALID_ARGUMENT, "graph is capturing; end the capture first");
+    hipError_t e = hipEventRecord(g->end, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+    g->submitted = true;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_graph_wait(qxh_graph* g, qxh_graph_metrics* metrics) {
+    QXH_REQUIRE(g, QXH_ERR_INVALID_ARGUMENT, "graph_wait: null graph");
+    QXH_REQUIRE(g->submitted, QXH_ERR_INVALID_ARGUMENT, "graph_wait before submit");
+    hipError_t e = hipEventSynchronize(g->end);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, g->start, g->end);
+    if (e == hipSuccess) e = hipGetLastError();
+    const uint32_t dispatches = g->dispatches;
+    qxh_context* ctx = g->ctx;
+    graph_free(g);
+    if (e != hipSuccess) return hip_fail(e, "graph execution");
+    {
+        std::lock_guard<std::mutex> lk(ctx->mu);
+        ctx->metrics.graphs += 1;
+        ctx->metrics.dispatches += dispatches;
+        ctx->metrics.gpu_ms += ms;
+    }
+    if (metrics) *metrics = qxh_graph_metrics{dispatches, ms};
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_graph_finish(qxh_graph* g, qxh_graph_metrics* metrics) {
+    int32_t r = qxh_graph_submit(g);
+    if (r != QXH_OK) return r;
+    return qxh_graph_wait(g, metrics);
+}
+
+extern "C" int32_t qxh_graph_discard(qxh_graph* g) {
+    if (!g) return QXH_OK;
+    if (g->capturing) {
+        hipGraph_t graph = nullptr;
+        (void)hipStreamEndCapture(g->stream, &graph);
+        if (graph) (void)hipGraphDestroy(graph);
+    }
+    graph_free(g);
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_graph_capture_begin(qxh_graph* g) {
+    QXH_REQUIRE(g, QXH_ERR_INVALID_ARGUMENT, "capture_begin: null graph");
+    QXH_REQUIRE(!g->capturing && !g->submitted, QXH_ERR_INVALID_ARGUMENT, "graph cannot start a capture now");
+    hipError_t e = hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamBeginCapture");
+    g->capturing = true;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_graph_capture_end(qxh_graph* g, qxh_replay** out) {
+    QXH_REQUIRE(g && out, QXH_ERR_INVALID_ARGUMENT, "capture_end: null argument");
+    QXH_REQUIRE(g->capturing, QXH_ERR_INVALID_ARGUMENT, "graph is not capturing");
+    *out = nullptr;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(g->stream, &graph);
+    g->capturing = false;
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return hip_fail(e, "hipGraphInstantiate");
+    }
+    *out = new qxh_replay{graph, exec};
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_replay_launch(qxh_replay* r, void* stream) {
+    QXH_REQUIRE(r, QXH_ERR_INVALID_ARGUMENT, "replay_launch: null replay");
+    hipError_t e = hipGraphLaunch(r->exec, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_replay_destroy(qxh_replay* r) {
+    if (!r) return QXH_OK;
+    (void)hipGraphExecDestroy(r->exec);
+    (void)hipGraphDestroy(r->graph);
+    delete r;
+    return QXH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// KV cache
+// ---------------------------------------------------------------------------
+static int32_t check_desc(const qxh_kv_desc* d, ShapeDims* dims) {
+    QXH_REQUIRE(d, QXH_ERR_INVALID_ARGUMENT, "null KV descriptor");
+    QXH_REQUIRE(shape_dims(d->shape, dims), QXH_ERR_INVALID_ARGUMENT, "unknown shape %d", d->shape);
+    QXH_REQUIRE(valid_dtype(d->key_dtype) && valid_dtype(d->value_dtype), QXH_ERR_INVALID_ARGUMENT,
+                "invalid KV dtype (%d, %d)", d->key_dtype, d->value_dtype);
+    QXH_REQUIRE(d->layers > 0 && d->sequences > 0 && d->capacity > 0, QXH_ERR_INVALID_ARGUMENT,
+                "KV layers, sequences and capacity must be positive");
+    return QXH_OK;
+}
+
+static void region_bytes(const qxh_kv_desc* d, const ShapeDims& s, uint64_t* kbytes, uint64_t* vbytes) {
+    const uint64_t elems = (uint64_t)d->layers * d->sequences * s.kv_heads * d->capacity * s.head_dim;
+    *kbytes = align256(elems * dtype_bytes(d->key_dtype));
+    *vbytes = align256(elems * dtype_bytes(d->value_dtype));
+}
+
+extern "C" int32_t qxh_kv_cache_bytes(const qxh_kv_desc* desc, uint64_t* bytes) {
+    ShapeDims s;
+    int32_t r = check_desc(desc, &s);
+    if (r) return r;
+    QXH_REQUIRE(bytes, QXH_ERR_INVALID_ARGUMENT, "null output");
+    uint64_t kb, vb;
+    region_bytes(desc, s, &kb, &vb);
+    *bytes = kb + vb;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_kv_cache_create(qxh_context* ctx, const qxh_kv_desc* desc, void* arena, uint64_t arena_bytes,
+                                       qxh_kv_cache** out) {
+    QXH_REQUIRE(ctx && out, QXH_ERR_INVALID_ARGUMENT, "kv_cache_create: null argument");
+    *out = nullptr;
+    ShapeDims s;
+    int32_t r = check_desc(desc, &s);
+    if (r) return r;
+    uint64_t kb, vb;
+    region_bytes(desc, s, &kb, &vb);
+    const uint64_t need = kb + vb;
+    bool owned = false;
+    if (arena) {
+        QXH_REQUIRE(arena_bytes >= need, QXH_ERR_INVALID_ARGUMENT, "KV arena holds %llu bytes, needs %llu",
+                    (unsigned long long)arena_bytes, (unsigned long long)need);
+        QXH_REQUIRE(((uintptr_t)arena & 255) == 0, QXH_ERR_INVALID_ARGUMENT, "KV arena must be 256-byte aligned");
+    } else {
+        hipError_t e = hipSetDevice(ctx->device);
+        if (e == hipSuccess) e = hipMalloc(&arena, need);
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc(KV arena)");
+        owned = true;
+        arena_bytes = need;
+    }
+    qxh_kv_cache* c = new qxh_kv_cache();
+    c->ctx = ctx;
+    c->desc = *desc;
+    c->dims = s;
+    c->arena = (char*)arena;
+    c->arena_bytes = arena_bytes;
+    c->owned = owned;
+    c->head_stride = (uint64_t)desc->capacity * s.head_dim;
+    c->seq_stride = c->head_stride * s.kv_heads;
+    c->layer_stride = c->seq_stride * desc->sequences;
+    c->key_region_bytes = kb;
+    c->cursor.assign((size_t)desc->layers * desc->sequences, 0u);
+    *out = c;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_kv_cache_destroy(qxh_kv_cache* c) {
+    if (!c) return QXH_OK;
+    if (c->owned) {
+        (void)hipSetDevice(c->ctx->device);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(c->arena);
+    }
+    delete c;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_kv_cache_len(const qxh_kv_cache* c, uint32_t layer, uint32_t seq, uint32_t* length) {
+    QXH_REQUIRE(c && length, QXH_ERR_INVALID_ARGUMENT, "kv_cache_len: null argument");
+    QXH_REQUIRE(layer < c->desc.layers && seq < c->desc.sequences, QXH_ERR_INVALID_ARGUMENT,
+                "layer %u / sequence %u out of range", layer, seq);
+    *length = c->cursor[(size_t)layer * c->desc.sequences + seq];
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_kv_cache_reset(qxh_kv_cache* c) {
+    QXH_REQUIRE(c, QXH_ERR_INVALID_ARGUMENT, "kv_cache_reset: null cache");
+    std::fill(c->cursor.begin(), c->cursor.end(), 0u);
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_kv_cache_rollback(qxh_kv_cache* c, uint32_t seq, uint32_t length) {
+    QXH_REQUIRE(c, QXH_ERR_INVALID_ARGUMENT, "kv_cache_rollback: null cache");
+    QXH_REQUIRE(seq < c->desc.sequences, QXH_ERR_INVALID_ARGUMENT, "sequence %u out of range", seq);
+    for (uint32_t l = 0; l < c->desc.layers; ++l)
+        QXH_REQUIRE(length <= c->at(l, seq), QXH_ERR_KV_POSITION,
+                    "KV rollback checkpoint %u is outside current position %u (layer %u)", length, c->at(l, seq), l);
+    for (uint32_t l = 0; l < c->desc.layers; ++l) c->at(l, seq) = length;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_kv_cache_set_len(qxh_kv_cache* c, uint32_t seq, uint32_t length) {
+    QXH_REQUIRE(c, QXH_ERR_INVALID_ARGUMENT, "kv_cache_set_len: null cache");
+    QXH_REQUIRE(seq == UINT32_MAX || seq < c->desc.sequences, QXH_ERR_INVALID_ARGUMENT, "sequence %u out of range",
+                seq);
+    QXH_REQUIRE(length <= c->desc.capacity, QXH_ERR_KV_POSITION, "KV length %u exceeds context %u", length,
+                c->desc.capacity);
+    for (uint32_t l = 0; l < c->desc.layers; ++l)
+        for (uint32_t s = 0; s < c->desc.sequences; ++s)
+            if (seq == UINT32_MAX || s == seq) c->at(l, s) = length;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_kv_cache_layout(const qxh_kv_cache* c, qxh_kv_layout* out) {
+    QXH_REQUIRE(c && out, QXH_ERR_INVALID_ARGUMENT, "kv_cache_layout: null argument");
+    out->keys = c->arena;
+    out->values = c->arena + c->key_region_bytes;
+    out->head_stride = c->head_stride;
+    out->sequence_stride = c->seq_stride;
+    out->layer_stride = c->layer_stride;
+    out->key_elem_bytes = dtype_bytes(c->desc.key_dtype);
+    out->value_elem_bytes = dtype_bytes(c->desc.value_dtype);
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_kv_cache_desc(const qxh_kv_cache* c, qxh_kv_desc* out) {
+    QXH_REQUIRE(c && out, QXH_ERR_INVALID_ARGUMENT, "kv_cache_desc: null argument");
+    *out = c->desc;
+    return QXH_OK;
+}
+
+static KvLayer kv_layer(const qxh_kv_cache* c, uint32_t layer, uint32_t first_seq) {
+    KvLayer k{};
+    const uint64_t off = (uint64_t)layer * c->layer_stride + (uint64_t)first_seq * c->seq_stride;
+    k.keys = c->arena + off * dtype_bytes(c->desc.key_dtype);
+    k.values = c->arena + c->key_region_bytes + off * dtype_bytes(c->desc.value_dtype);
+    k.head_stride = c->head_stride;
+    k.sequence_stride = c->seq_stride;
+    k.key_dtype = c->desc.key_dtype;
+    k.value_dtype = c->desc.value_dtype;
+    k.capacity = c->desc.capacity;
+    return k;
+}
+
+// ---------------------------------------------------------------------------
+// encoders
+// ---------------------------------------------------------------------------
+static int32_t check_graph(qxh_graph* g) {
+    QXH_REQUIRE(g, QXH_ERR_INVALID_ARGUMENT, "null graph");
+    QXH_REQUIRE(!g->submitted, QXH_ERR_INVALID_ARGUMENT, "graph already submitted");
+    return QXH_OK;
+}
+
+static int32_t check_range(const qxh_kv_cache* c, uint32_t layer, uint32_t first, uint32_t count) {
+    QXH_REQUIRE(c, QXH_ERR_INVALID_ARGUMENT, "null KV cache");
+    QXH_REQUIRE(layer < c->desc.layers, QXH_ERR_INVALID_ARGUMENT, "layer %u out of range (%u layers)", layer,
+                c->desc.layers);
+    QXH_REQUIRE(count > 0 && first < c->desc.sequences && count <= c->desc.sequences - first,
+                QXH_ERR_INVALID_ARGUMENT, "sequences [%u, %u+%u) out of range (%u)", first, first, count,
+                c->desc.sequences);
+    return QXH_OK;
+}
+
+// Shared validation of appends: every cursor equals start_position and
+// start_position + tokens fits the capacity (KvCache::append rules).
+static int32_t check_append(qxh_kv_cache* c, uint32_t layer, uint32_t first, uint32_t count, uint32_t start,
+                            uint32_t tokens) {
+    QXH_REQUIRE(tokens > 0, QXH_ERR_INVALID_ARGUMENT, "append of zero tokens");
+    for (uint32_t s = first; s < first + count; ++s) {
+        const uint32_t len = c->at(layer, s);
+        QXH_REQUIRE(start == len, QXH_ERR_KV_POSITION, "KV position %u does not follow cache length %u (sequence %u)",
+                    start, len, s);
+    }
+    QXH_REQUIRE((uint64_t)start + tokens <= c->desc.capacity, QXH_ERR_KV_POSITION, "KV position %llu exceeds context %u",
+                (unsigned long long)start + tokens - 1, c->desc.capacity);
+    return QXH_OK;
+}
+
+static void advance(qxh_kv_cache* c, uint32_t layer, uint32_t first, uint32_t count, uint32_t tokens) {
+    for (uint32_t s = first; s < first + count; ++s) c->at(layer, s) += tokens;
+}
+
+extern "C" int32_t qxh_encode_rope_kv_batch(qxh_graph* g, qxh_kv_cache* c, uint32_t layer, uint32_t first,
+                                            uint32_t count, uint32_t start, uint32_t tokens, const void* query,
+                                            const void* key, const void* value, int32_t input_dtype,
+                                            const float* query_norm, const float* key_norm, void* query_output,
+                                            int32_t output_dtype) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    if ((r = check_range(c, layer, first, count))) return r;
+    QXH_REQUIRE(key && value, QXH_ERR_INVALID_ARGUMENT, "rope_kv: null key/value");
+    QXH_REQUIRE(!query_output || query, QXH_ERR_INVALID_ARGUMENT, "rope_kv: query_output without query");
+    QXH_REQUIRE(valid_dtype(input_dtype) && valid_dtype(output_dtype), QXH_ERR_INVALID_ARGUMENT,
+                "rope_kv: invalid dtype (%d, %d)", input_dtype, output_dtype);
+    if ((r = check_append(c, layer, first, count, start, tokens))) return r;
+    const bool granite = c->desc.shape == QXH_SHAPE_GRANITE;
+    // Consensus sin/cos is defined for |angle| <= 4096 (lib.rs:149): positions <= 4096.
+    QXH_REQUIRE(!granite || (uint64_t)start + tokens - 1 <= 4096, QXH_ERR_INVALID_ARGUMENT,
+                "unregistered Granite RoPE coordinate: position %llu > 4096",
+                (unsigned long long)start + tokens - 1);
+    RopeAppendArgs a{};
+    a.query = query;
+    a.key = key;
+    a.value = value;
+    a.query_out = query_output;
+    a.query_norm = query_norm;
+    a.key_norm = key_norm;
+    a.input_dtype = input_dtype;
+    a.output_dtype = output_dtype;
+    a.start_position = start;
+    a.tokens = tokens;
+    a.sequences = count;
+    a.mode = granite ? 0 : 1;
+    if (!granite) qwen_inverse_frequencies(a.qwen_inv_freq);
+    hipError_t e = launch_rope_append(c->dims, kv_layer(c, layer, first), a, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "rope_kv launch");
+    g->dispatches += 1;
+    advance(c, layer, first, count, tokens);
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_encode_rope_kv_for_layer(qxh_graph* g, qxh_kv_cache* c, const float* query, const float* key,
+                                                const float* value, float* query_output, uint32_t layer,
+                                                uint32_t position) {
+    QXH_REQUIRE(c, QXH_ERR_INVALID_ARGUMENT, "null KV cache");
+    QXH_REQUIRE(c->desc.shape == QXH_SHAPE_GRANITE, QXH_ERR_INVALID_ARGUMENT,
+                "encode_rope_kv_for_layer is the Granite fp32 entry point");
+    QXH_REQUIRE(query && query_output, QXH_ERR_INVALID_ARGUMENT, "rope_kv: null query");
+    return qxh_encode_rope_kv_batch(g, c, layer, 0, 1, position, 1, query, key, value, QXH_F32, nullptr, nullptr,
+                                    query_output, QXH_F32);
+}
+
+extern "C" int32_t qxh_encode_store_kv(qxh_graph* g, qxh_kv_cache* c, uint32_t layer, uint32_t first, uint32_t count,
+                                       uint32_t start, uint32_t tokens, const void* key, const void* value,
+                                       int32_t input_dtype) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    if ((r = check_range(c, layer, first, count))) return r;
+    QXH_REQUIRE(key && value, QXH_ERR_INVALID_ARGUMENT, "store_kv: null key/value");
+    QXH_REQUIRE(valid_dtype(input_dtype), QXH_ERR_INVALID_ARGUMENT, "store_kv: invalid dtype %d", input_dtype);
+    if ((r = check_append(c, layer, first, count, start, tokens))) return r;
+    RopeAppendArgs a{};
+    a.key = key;
+    a.value = value;
+    a.input_dtype = input_dtype;
+    a.output_dtype = input_dtype;
+    a.start_position = start;
+    a.tokens = tokens;
+    a.sequences = count;
+    a.mode = 2;
+    hipError_t e = launch_rope_append(c->dims, kv_layer(c, layer, first), a, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "store_kv launch");
+    g->dispatches += 1;
+    advance(c, layer, first, count, tokens);
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_encode_qwen_qk_norm_rope(qxh_graph* g, void* query, void* key, const float* query_norm,
+                                                const float* key_norm, int32_t dtype, uint32_t position) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    QXH_REQUIRE(query && key, QXH_ERR_INVALID_ARGUMENT, "qwen_qk_norm_rope: null query/key");
+    QXH_REQUIRE(valid_dtype(dtype), QXH_ERR_INVALID_ARGUMENT, "qwen_qk_norm_rope: invalid dtype %d", dtype);
+    float inv[64];
+    qwen_inverse_frequencies(inv);
+    hipError_t e = launch_qwen_qk_norm_rope(query, key, query_norm, key_norm, dtype, position, inv, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "qwen_qk_norm_rope launch");
+    g->dispatches += 1;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_attention_workspace_bytes(const qxh_kv_cache* c, uint32_t sequences, uint32_t length,
+                                                 uint64_t* bytes) {
+    QXH_REQUIRE(c && bytes, QXH_ERR_INVALID_ARGUMENT, "attention_workspace_bytes: null argument");
+    QXH_REQUIRE(length > 0 && sequences > 0, QXH_ERR_INVALID_ARGUMENT, "empty attention");
+    *bytes = plan_decode(c->dims, c->desc.key_dtype, sequences, length).workspace_bytes;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_encode_attention_for_layer(qxh_graph* g, qxh_kv_cache* c, uint32_t layer, uint32_t first,
+                                                  uint32_t count, uint32_t length, const void* query,
+                                                  int32_t query_dtype, void* output, int32_t output_dtype,
+                                                  void* workspace, uint64_t workspace_bytes) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    if ((r = check_range(c, layer, first, count))) return r;
+    QXH_REQUIRE(query && output, QXH_ERR_INVALID_ARGUMENT, "attention: null query/output");
+    QXH_REQUIRE(valid_dtype(query_dtype) && valid_dtype(output_dtype), QXH_ERR_INVALID_ARGUMENT,
+                "attention: invalid dtype (%d, %d)", query_dtype, output_dtype);
+    QXH_REQUIRE(length > 0, QXH_ERR_INVALID_ARGUMENT, "attention over an empty context");
+    for (uint32_t s = first; s < first + count; ++s)
+        QXH_REQUIRE(length <= c->at(layer, s), QXH_ERR_KV_POSITION,
+                    "attention length %u exceeds committed length %u (sequence %u)", length, c->at(layer, s), s);
+    QXH_REQUIRE(c->desc.key_dtype == c->desc.value_dtype, QXH_ERR_UNSUPPORTED,
+                "decode attention needs equal K and V dtypes (got %d, %d)", c->desc.key_dtype, c->desc.value_dtype);
+    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, count, length);
+    QXH_REQUIRE(workspace_bytes >= p.workspace_bytes && (p.workspace_bytes == 0 || workspace),
+                QXH_ERR_INVALID_ARGUMENT, "attention workspace holds %llu bytes, needs %llu",
+                (unsigned long long)workspace_bytes, (unsigned long long)p.workspace_bytes);
+    int dispatches = 0;
+    hipError_t e = launch_decode_attention(c->dims, kv_layer(c, layer, first), p, count, length, query, query_dtype,
+                                           output, output_dtype, workspace, g->stream, &dispatches);
+    if (e != hipSuccess) return hip_fail(e, "attention launch");
+    g->dispatches += dispatches;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_encode_prefill_attention(qxh_graph* g, qxh_kv_cache* c, uint32_t layer, uint32_t seq,
+                                                uint32_t start, uint32_t tokens, const void* query,
+                                                int32_t query_dtype, void* output, int32_t output_dtype) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    if ((r = check_range(c, layer, seq, 1))) return r;
+    QXH_REQUIRE(query && output, QXH_ERR_INVALID_ARGUMENT, "prefill: null query/output");
+    QXH_REQUIRE(valid_dtype(query_dtype) && valid_dtype(output_dtype), QXH_ERR_INVALID_ARGUMENT,
+                "prefill: invalid dtype (%d, %d)", query_dtype, output_dtype);
+    QXH_REQUIRE(tokens > 0, QXH_ERR_INVALID_ARGUMENT, "prefill of zero tokens");
+    QXH_REQUIRE((uint64_t)start + tokens <= c->at(layer, seq), QXH_ERR_KV_POSITION,
+                "prefill rows end at %llu beyond committed length %u", (unsigned long long)start + tokens,
+                c->at(layer, seq));
+    int dispatches = 0;
+    hipError_t e = launch_prefill_attention(c->dims, kv_layer(c, layer, seq), start, tokens, query, query_dtype,
+                                            output, output_dtype, g->stream, &dispatches);
+    if (e == hipErrorNotSupported)
+        return fail(QXH_ERR_UNSUPPORTED, "prefill: no kernel for this KV dtype / query dtype combination");
+    if (e != hipSuccess) return hip_fail(e, "prefill launch");
+    g->dispatches += dispatches;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_encode_kv_gather_token_rows(qxh_graph* g, const qxh_kv_cache* c, uint32_t layer, uint32_t seq,
+                                                   uint32_t begin, uint32_t count, void* keys_out, void* values_out) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    if ((r = check_range(c, layer, seq, 1))) return r;
+    QXH_REQUIRE(keys_out || values_out, QXH_ERR_INVALID_ARGUMENT, "gather: no output");
+    QXH_REQUIRE(count > 0, QXH_ERR_INVALID_ARGUMENT, "gather of zero rows");
+    const uint32_t len = c->cursor[(size_t)layer * c->desc.sequences + seq];
+    QXH_REQUIRE((uint64_t)begin + count <= len, QXH_ERR_KV_POSITION,
+                "KV position %llu is outside committed length %u", (unsigned long long)begin + count - 1, len);
+    hipError_t e = launch_kv_gather(c->dims, kv_layer(c, layer, seq), begin, count, keys_out, values_out, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "gather launch");
+    g->dispatches += 1;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_granite_block_workspace_bytes(const qxh_kv_cache* c, uint32_t length, uint64_t* bytes) {
+    QXH_REQUIRE(c && bytes, QXH_ERR_INVALID_ARGUMENT, "granite_block_workspace_bytes: null argument");
+    QXH_REQUIRE(c->desc.shape == QXH_SHAPE_GRANITE, QXH_ERR_INVALID_ARGUMENT, "Granite block needs a Granite cache");
+    QXH_REQUIRE(length > 0, QXH_ERR_INVALID_ARGUMENT, "empty attention");
+    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, 1, length);
+    *bytes = 2 * 1024 * sizeof(float) + align256(p.workspace_bytes);
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_encode_granite_attention_block(qxh_graph* g, qxh_kv_cache* c, uint32_t layer, uint32_t position,
+                                                      const qxh_granite_layer_weights* w, const float* hidden_in,
+                                                      float* hidden_out, void* workspace, uint64_t workspace_bytes) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    if ((r = check_range(c, layer, 0, 1))) return r;
+    QXH_REQUIRE(c->desc.shape == QXH_SHAPE_GRANITE, QXH_ERR_INVALID_ARGUMENT, "Granite block needs a Granite cache");
+    QXH_REQUIRE(w && w->input_norm && w->q_proj && w->k_proj && w->v_proj && w->o_proj, QXH_ERR_INVALID_ARGUMENT,
+                "granite block: null weight");
+    QXH_REQUIRE(hidden_in && hidden_out && hidden_in != hidden_out, QXH_ERR_INVALID_ARGUMENT,
+                "granite block: hidden_in and hidden_out must be distinct non-null buffers");
+    QXH_REQUIRE(c->desc.key_dtype == c->desc.value_dtype, QXH_ERR_UNSUPPORTED,
+                "decode attention needs equal K and V dtypes");
+    if ((r = check_append(c, layer, 0, 1, position, 1))) return r;
+    QXH_REQUIRE(position <= 4096, QXH_ERR_INVALID_ARGUMENT, "unregistered Granite RoPE coordinate %u", position);
+    const uint32_t length = position + 1;
+    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, 1, length);
+    const uint64_t need = 2 * 1024 * sizeof(float) + align256(p.workspace_bytes);
+    QXH_REQUIRE(workspace && workspace_bytes >= need, QXH_ERR_INVALID_ARGUMENT,
+                "granite block workspace holds %llu bytes, needs %llu", (unsigned long long)workspace_bytes,
+                (unsigned long long)need);
+    GraniteBlockArgs a{};
+    a.input_norm = w->input_norm;
+    a.wq = w->q_proj;
+    a.wk = w->k_proj;
+    a.wv = w->v_proj;
+    a.wo = w->o_proj;
+    a.hidden_in = hidden_in;
+    a.hidden_out = hidden_out;
+    a.query_rot = reinterpret_cast<float*>(workspace);
+    a.attention = a.query_rot + 1024;
+    a.position = position;
+    void* attn_ws = reinterpret_cast<char*>(workspace) + 2 * 1024 * sizeof(float);
+    const KvLayer kv = kv_layer(c, layer, 0);
+    hipError_t e = launch_granite_qkv_rope(c->dims, kv, a, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "granite qkv launch");
+    int dispatches = 0;
+    e = launch_decode_attention(c->dims, kv, p, 1, length, a.query_rot, QXH_F32, a.attention, QXH_F32, attn_ws,
+                                g->stream, &dispatches);
+    if (e != hipSuccess) return hip_fail(e, "granite attention launch");
+    e = launch_granite_out_residual(a, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "granite output launch");
+    g->dispatches += 2 + dispatches;
+    advance(c, layer, 0, 1, 1);
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_encode_fill_normal(qxh_graph* g, void* data, int32_t dtype, uint64_t count, uint64_t seed,
+                                          float stddev) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    QXH_REQUIRE(data && count > 0, QXH_ERR_INVALID_ARGUMENT, "fill_normal: empty target");
+    QXH_REQUIRE(valid_dtype(dtype), QXH_ERR_INVALID_ARGUMENT, "fill_normal: invalid dtype %d", dtype);
+    hipError_t e = launch_fill_normal(data, dtype, count, seed, stddev, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "fill_normal launch");
+    g->dispatches += 1;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_encode_kv_fill_normal(qxh_graph* g, qxh_kv_cache* c, uint64_t seed, uint32_t length) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    QXH_REQUIRE(c, QXH_ERR_INVALID_ARGUMENT, "kv_fill_normal: null cache");
+    QXH_REQUIRE(length > 0 && length <= c->desc.capacity, QXH_ERR_KV_POSITION, "KV length %u outside (0, %u]", length,
+                c->desc.capacity);
+    hipError_t e = launch_kv_fill_normal(c->dims, kv_layer(c, 0, 0), c->desc.layers, c->desc.sequences,
+                                         c->layer_stride, length, seed, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "kv_fill_normal launch");
+    g->dispatches += 1;
+    std::fill(c->cursor.begin(), c->cursor.end(), length);
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_encode_consensus_conformance(qxh_graph* g, const float* inputs, const uint32_t* coords,
+                                                    uint32_t count, uint32_t* exp_bits, uint32_t* rsqrt_bits,
+                                                    uint32_t* sin_bits, uint32_t* cos_bits) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    QXH_REQUIRE(inputs && coords && exp_bits && rsqrt_bits && sin_bits && cos_bits && count > 0,
+                QXH_ERR_INVALID_ARGUMENT, "conformance: null argument");
+    hipError_t e = launch_conformance(inputs, coords, count, exp_bits, rsqrt_bits, sin_bits, cos_bits, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "conformance launch");
+    g->dispatches += 1;
+    return QXH_OK;
+}

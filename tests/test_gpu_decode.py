@@ -1,0 +1,177 @@
+"""GPU parity: split-K decode attention against the oracle.
+
+Granite fp32 KV: max-abs error <= 1e-5 x output RMS against
+granite_attention_decode (crates/qx-runtime/src/lib.rs:444-552).
+fp16/bf16 KV: <= 2e-3 x RMS against the fp32 oracle on the same (rounded)
+cache contents.  Qwen: against cpu_gqa_attention
+(tools/qx-qwen-parity/src/main.rs:1218-1258).
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from qx_amd import abi, api
+from qx_amd import runtime as rt
+from tests.helpers import TOL_16, TOL_F32, log, rel_err
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "granite_cfg1.npz")
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    return rt.Context(0)
+
+
+def dev(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0").to(dtype)
+
+
+def test_grouped_query_attention_uses_matching_kv_head():
+    # crates/qx-runtime/src/lib.rs:2872-2892, through the reference-shaped API
+    cache = api.KvCache(4)
+    value = np.zeros((8, 64), np.float32)
+    for h in range(8):
+        value[h] = h + 1.0
+    out = api.granite_attention_decode(np.zeros(1024), np.zeros(512), value.ravel(), 0, cache)
+    assert len(cache) == 1
+    for qh in range(16):
+        assert np.all(out[qh * 64:(qh + 1) * 64] == qh // 2 + 1.0)
+
+
+def test_kv_cache_rejects_non_sequential_positions():
+    # crates/qx-runtime/src/lib.rs:2894-2901
+    cache = api.KvCache(2)
+    z = np.zeros(1024)
+    with pytest.raises(abi.QxhError):
+        api.granite_attention_decode(z, z[:512], z[:512], 1, cache)
+
+
+def test_cfg1_positions_0_to_511_fp32(ctx):
+    """Config 1: one Granite layer, positions 0..511 appended one at a time
+    into an fp32 cache of capacity 512; every step's [16,64] output."""
+    log("cfg1 decode 0..511")
+    gold = np.load(GOLDEN)
+    rng = np.random.default_rng(int(gold["seed"]))
+    P = 512
+    q = rng.standard_normal((P, 1024), dtype=np.float32)
+    k = rng.standard_normal((P, 512), dtype=np.float32)
+    v = rng.standard_normal((P, 512), dtype=np.float32)
+    cache = api.KvCache(512)
+    ref = O.KvCache(512)
+    worst = 0.0
+    checkpoints = list(gold["checkpoints"])
+    for p in range(P):
+        out = api.granite_attention_decode(q[p], k[p], v[p], p, cache)
+        r = O.granite_attention_decode(q[p], k[p], v[p], p, ref)
+        e = rel_err(out, r)
+        worst = max(worst, e)
+        assert e <= TOL_F32, (p, e)
+        if p in checkpoints:
+            i = checkpoints.index(p)
+            assert np.array_equal(r, gold["outputs"][i])  # the oracle still reproduces the fixture
+            assert rel_err(out, gold["outputs"][i]) <= TOL_F32
+    log(f"cfg1 worst max-abs/rms = {worst:.3e}")
+    kk, vv = cache.token_rows()
+    assert np.array_equal(kk, ref.keys()) and np.array_equal(vv, ref.values())
+
+
+@pytest.mark.parametrize("kdt,length", [(abi.F32, 1), (abi.F32, 4096), (abi.F16, 37), (abi.F16, 4096),
+                                        (abi.BF16, 2049), (abi.F32, 1000)])
+def test_granite_decode_lengths_and_dtypes(ctx, kdt, length):
+    log("granite decode", kdt, length)
+    rng = np.random.default_rng(100 + length + kdt)
+    S = 3
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 2, S, 4096, kdt)
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=length * 7 + kdt, length=length)
+    q = dev(rng.standard_normal((S, 16, 64), dtype=np.float32))
+    with rt.Graph(ctx) as g:
+        out = rt.attention(g, arena, 1, q, length)
+    tol = TOL_F32 if kdt == abi.F32 else TOL_16
+    for s in range(S):
+        with rt.Graph(ctx) as g:
+            kk, vv = arena.gather(g, 1, s, 0, length)
+        ref_cache = O.KvCache(4096)
+        ref_cache.extend(kk.float().cpu().numpy(), vv.float().cpu().numpy())
+        r = O.granite_attend(q[s].cpu().numpy().ravel(), ref_cache, length)
+        e = rel_err(out[s].cpu().numpy().ravel(), r)
+        assert e <= tol, (s, e)
+
+
+def test_cfg4_batched_fp16_decode_full_size(ctx):
+    """Config 4 shape: 256 sequences x 4096 positions of fp16 KV (one layer here);
+    sampled sequences against the oracle."""
+    log("cfg4 256x4096 fp16")
+    S, L = 256, 4096
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, S, L, abi.F16)
+    q = torch.empty((S, 16, 64), device="cuda:0")
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=4, length=L)
+        rt.fill_normal(g, q, seed=44)
+    with rt.Graph(ctx) as g:
+        out = rt.attention(g, arena, 0, q, L)
+    assert torch.isfinite(out).all()
+    for s in (0, 1, 128, 255):
+        with rt.Graph(ctx) as g:
+            kk, vv = arena.gather(g, 0, s, 0, L)
+        ref_cache = O.KvCache(L)
+        ref_cache.extend(kk.float().cpu().numpy(), vv.float().cpu().numpy())
+        r = O.granite_attend(q[s].cpu().numpy().ravel(), ref_cache, L)
+        assert rel_err(out[s].cpu().numpy().ravel(), r) <= TOL_16
+
+
+def test_split_and_unsplit_agree(ctx):
+    """Size-independent property: the same cache attended as 1 sequence
+    (many splits) and inside a 256-sequence batch (one split) agree."""
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 256, 2048, abi.F32)
+    q = torch.empty((256, 16, 64), device="cuda:0")
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=9, length=2048)
+        rt.fill_normal(g, q, seed=99)
+        batched = rt.attention(g, arena, 0, q, 2048)
+        single = rt.attention(g, arena, 0, q[7:8].contiguous(), 2048, first_sequence=7)
+    assert rt.attention_workspace_bytes(arena, 1, 2048) > 0 == rt.attention_workspace_bytes(arena, 256, 2048)
+    assert rel_err(single[0].cpu().numpy(), batched[7].cpu().numpy()) <= TOL_F32
+
+
+def test_attention_length_beyond_cursor_is_rejected(ctx):
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, 64, abi.F32)
+    arena.set_len(10)
+    q = torch.zeros((1, 16, 64), device="cuda:0")
+    with rt.Graph(ctx) as g:
+        with pytest.raises(abi.QxhError, match="exceeds committed length"):
+            rt.attention(g, arena, 0, q, 11)
+
+
+@pytest.mark.parametrize("fmt,ctxlen", [(abi.F16, 97), (abi.F16, 4096), (abi.BF16, 5000), (abi.BF16, 32768)])
+def test_qwen_decode_matches_cpu_gqa_attention(ctx, fmt, ctxlen):
+    log("qwen decode", fmt, ctxlen)
+    dt = torch.float16 if fmt == abi.F16 else torch.bfloat16
+    ofmt = O.F16 if fmt == abi.F16 else O.BF16
+    arena = rt.KvArena(ctx, abi.SHAPE_QWEN3, 1, 1, ctxlen, fmt)
+    q = torch.empty((1, 32, 128), dtype=dt, device="cuda:0")
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=ctxlen + fmt, length=ctxlen)
+        rt.fill_normal(g, q, seed=3)
+        out = rt.attention(g, arena, 0, q, ctxlen)
+        kk, vv = arena.gather(g, 0, 0, 0, ctxlen)
+    tobits = lambda t: t.contiguous().view(torch.int16).cpu().numpy().ravel().view(np.uint16)
+    _, ref = O.qwen_gqa_attention(tobits(q), tobits(kk), tobits(vv), ofmt, want_f32=True)
+    got = out.float().cpu().numpy().ravel()
+    assert rel_err(got, ref) <= TOL_16
+
+
+def test_run_qwen_gqa_attention_mirror():
+    rng = np.random.default_rng(21)
+    n = 300
+    q = O.to_bits16(rng.standard_normal(4096), O.F16)
+    kc = O.to_bits16(rng.standard_normal(n * 512), O.F16)
+    vc = O.to_bits16(rng.standard_normal(n * 512), O.F16)
+    got = api.run_qwen_gqa_attention(q, kc, vc)
+    _, ref = O.qwen_gqa_attention(q, kc, vc, O.F16, want_f32=True)
+    assert rel_err(O.from_bits16(got, O.F16), ref) <= TOL_16
