@@ -216,24 +216,61 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
 }
 
 // Reduce the per-split partials: out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
-// grid (q_heads, sequences), block D.
+// grid (q_heads, sequences), block D.  The split weights are formed once per
+// block in LDS (parallel over splits), then every thread streams its column
+// of acc with independent loads.
+constexpr int kMaxSplits = 1024;
+
 template <int D, int G>
 __global__ __launch_bounds__(D) void decode_combine_kernel(DecodeArgs a) {
+    __shared__ float sm_f[kMaxSplits];
+    __shared__ float sm_red[D];
     const uint32_t hq = blockIdx.x, seq = blockIdx.y;
     const uint32_t hkv = gridDim.x / G;
     const uint32_t kvh = hq / G, g = hq % G;
-    const int d = threadIdx.x;
-    const size_t p0 = ((size_t)seq * hkv + kvh) * a.splits * G + g;
-    float M = kNegBig;
-    for (uint32_t s = 0; s < a.splits; ++s) M = fmaxf(M, a.ws_ml[2 * (p0 + (size_t)s * G)]);
-    float L = 0.0f, A = 0.0f;
-    for (uint32_t s = 0; s < a.splits; ++s) {
-        const size_t p = p0 + (size_t)s * G;
-        const float f = fast_exp2(a.ws_ml[2 * p] - M);
-        L = __builtin_fmaf(a.ws_ml[2 * p + 1], f, L);
-        A = __builtin_fmaf(a.ws_acc[p * D + d], f, A);
+    const int t = threadIdx.x;
+    const uint32_t S = a.splits;
+    const size_t p0 = ((size_t)seq * hkv + kvh) * S * G + g;
+
+    float mloc = kNegBig;
+    for (uint32_t s = t; s < S; s += D) {
+        const float m = a.ws_ml[2 * (p0 + (size_t)s * G)];
+        sm_f[s] = m;
+        mloc = fmaxf(mloc, m);
     }
-    store_any(a.out, ((size_t)seq * gridDim.x + hq) * D + d, A / L, a.out_dtype);
+    sm_red[t] = mloc;
+    __syncthreads();
+    for (int w = D / 2; w > 0; w >>= 1) {
+        if (t < w) sm_red[t] = fmaxf(sm_red[t], sm_red[t + w]);
+        __syncthreads();
+    }
+    const float M = sm_red[0];
+    __syncthreads();
+    float lloc = 0.0f;
+    for (uint32_t s = t; s < S; s += D) {
+        const float f = fast_exp2(sm_f[s] - M);
+        sm_f[s] = f;
+        lloc = __builtin_fmaf(a.ws_ml[2 * (p0 + (size_t)s * G) + 1], f, lloc);
+    }
+    sm_red[t] = lloc;
+    __syncthreads();
+    for (int w = D / 2; w > 0; w >>= 1) {
+        if (t < w) sm_red[t] += sm_red[t + w];
+        __syncthreads();
+    }
+    const float L = sm_red[0];
+    float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f, A3 = 0.0f;
+    const float* acc = a.ws_acc + p0 * D + t;
+    const size_t stride = (size_t)G * D;
+    uint32_t s = 0;
+    for (; s + 4 <= S; s += 4) {
+        A0 = __builtin_fmaf(acc[(size_t)s * stride], sm_f[s], A0);
+        A1 = __builtin_fmaf(acc[(size_t)(s + 1) * stride], sm_f[s + 1], A1);
+        A2 = __builtin_fmaf(acc[(size_t)(s + 2) * stride], sm_f[s + 2], A2);
+        A3 = __builtin_fmaf(acc[(size_t)(s + 3) * stride], sm_f[s + 3], A3);
+    }
+    for (; s < S; ++s) A0 = __builtin_fmaf(acc[(size_t)s * stride], sm_f[s], A0);
+    store_any(a.out, ((size_t)seq * gridDim.x + hq) * D + t, ((A0 + A1) + (A2 + A3)) / L, a.out_dtype);
 }
 
 // ---------------------------------------------------------------------------
@@ -267,6 +304,11 @@ DecodePlan plan_decode(const ShapeDims& s, int key_dtype, uint32_t sequences, ui
     chunk = (chunk + gran - 1) / gran * gran;
     splits = (length + chunk - 1) / chunk;
     if (splits < 1) splits = 1;
+    if (splits > (uint32_t)kMaxSplits) {
+        chunk = (length + kMaxSplits - 1) / kMaxSplits;
+        chunk = (chunk + gran - 1) / gran * gran;
+        splits = (length + chunk - 1) / chunk;
+    }
     p.splits = splits;
     p.chunk = chunk;
     p.workspace_bytes = splits > 1 ? (uint64_t)units * splits * s.group * (s.head_dim + 2) * sizeof(float) : 0;
