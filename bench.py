@@ -224,6 +224,46 @@ def bench_cfg5a(ctx, steps, warmup):
 
 
 # ---------------------------------------------------------------------------
+# cfg3 / cfg5b: causal prefill (MFMA)
+# ---------------------------------------------------------------------------
+def bench_prefill(ctx, steps, warmup, shape_name):
+    import torch
+    from qx_amd import abi
+    from qx_amd import runtime as rt
+
+    if shape_name == "cfg3":
+        shape, dtype, T = abi.SHAPE_GRANITE, abi.F16, 2048
+    else:
+        shape, dtype, T = abi.SHAPE_QWEN3, abi.BF16, 8192
+    info = rt.shape_info(shape)
+    tdt = rt.torch_dtype(dtype)
+    stream = torch.cuda.current_stream()
+    arena = rt.KvArena(ctx, shape, 1, 1, T, dtype)
+    q = torch.empty((1, T, info.q_heads, info.head_dim), dtype=tdt, device="cuda:0")
+    k = torch.empty((1, T, info.kv_heads, info.head_dim), dtype=tdt, device="cuda:0")
+    v = torch.empty_like(k)
+    qo = torch.empty_like(q)
+    out = torch.empty((T, info.q_heads, info.head_dim), dtype=tdt, device="cuda:0")
+    with rt.Graph(ctx, stream) as g:
+        for i, t in enumerate((q, k, v)):
+            rt.fill_normal(g, t, seed=200 + i)
+        rt.rope_kv_batch(g, arena, 0, 0, q, k, v, query_out=qo)
+    g = rt.Graph(ctx, stream)
+    g.capture_begin()
+    rt.prefill_attention(g, arena, 0, 0, qo[0], out=out)
+    replay = g.capture_end()
+    g.discard()
+    ms = timed(lambda: replay.launch(stream), steps, warmup, stream)
+    flops = 4.0 * info.head_dim * info.q_heads * T * (T + 1) / 2
+    tflops = flops / (ms * 1e-3) / 1e12
+    peak = MFMA_PEAK_TFLOPS["f16" if dtype == abi.F16 else "bf16"]
+    return {"us_per_prefill": ms * 1000.0, "tokens": T, "flop": flops,
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
+                         "frac": round(tflops / peak, 4), "traffic": None},
+            "note": "causal attention only (RoPE/append excluded); flop = 4*D*Hq*T(T+1)/2"}
+
+
+# ---------------------------------------------------------------------------
 # CPU baseline: the oracle's single-threaded Granite attention on a sample
 # ---------------------------------------------------------------------------
 def cpu_baseline(seconds=10.0):
@@ -281,6 +321,8 @@ def main():
     ap.add_argument("--no-detail", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 1 GiB device copy (known bytes) to scale rocprofv3 FETCH/WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -299,13 +341,23 @@ def main():
 def run(ctx, args):
     import torch
 
+    if args.calibrate_copy:
+        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calibration copy: 1073741824 bytes read + 1073741824 bytes written per dispatch")
+        del src, dst
+
     only = set(filter(None, args.only.split(",")))
     detail = {}
     head = bench_cfg4(ctx, args.steps, args.warmup) if (not only or "cfg4" in only) else None
     if head:
         log("cfg4", json.dumps(head))
     if not args.no_detail:
-        for name, fn in (("cfg1", bench_cfg1), ("cfg2", bench_cfg2), ("cfg5a", bench_cfg5a)):
+        for name, fn in (("cfg1", bench_cfg1), ("cfg2", bench_cfg2), ("cfg3", lambda c, k, w: bench_prefill(c, k, w, "cfg3")),
+                         ("cfg5a", bench_cfg5a), ("cfg5b", lambda c, k, w: bench_prefill(c, k, w, "cfg5b"))):
             if only and name not in only:
                 continue
             try:

@@ -105,12 +105,15 @@ QXH_API int32_t qxh_context_create(int32_t device, qxh_context** out);
 QXH_API int32_t qxh_context_destroy(qxh_context* ctx);
 /* MetalContext::metrics, crates/qx-metal/src/lib.rs:9604-9618 */
 QXH_API int32_t qxh_context_metrics(const qxh_context* ctx, qxh_metrics* out);
+/* The context's own non-blocking stream (a hipStream_t). */
+QXH_API int32_t qxh_context_stream(const qxh_context* ctx, void** stream);
 
 /* ---- graph -----------------------------------------------------------------
  * Replaces DecodeGraph / SubmittedDecode (crates/qx-metal/src/lib.rs:9404-9514,
  * begin_decode :9819-9845): ordered work on one HIP stream, bracketed by a
- * pair of events for GPU time.  `stream` is a hipStream_t (NULL: the
- * context's stream).  A graph is single-owner, like &mut DecodeGraph. */
+ * pair of events for GPU time.  `stream` is a hipStream_t; NULL is the HIP
+ * null stream, as everywhere in HIP (qxh_context_stream gives the context's
+ * own stream).  A graph is single-owner, like &mut DecodeGraph. */
 typedef struct qxh_graph qxh_graph;
 
 typedef struct {

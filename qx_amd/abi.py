@@ -66,6 +66,7 @@ SIGNATURES = {
     "qxh_context_create": (c_int32, [c_int32, P(c_void_p)]),
     "qxh_context_destroy": (c_int32, [c_void_p]),
     "qxh_context_metrics": (c_int32, [c_void_p, P(Metrics)]),
+    "qxh_context_stream": (c_int32, [c_void_p, P(c_void_p)]),
     "qxh_graph_begin": (c_int32, [c_void_p, c_void_p, P(c_void_p)]),
     "qxh_graph_submit": (c_int32, [c_void_p]),
     "qxh_graph_wait": (c_int32, [c_void_p, P(GraphMetrics)]),

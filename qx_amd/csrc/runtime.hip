@@ -175,6 +175,12 @@ extern "C" int32_t qxh_context_metrics(const qxh_context* ctx, qxh_metrics* out)
     return QXH_OK;
 }
 
+extern "C" int32_t qxh_context_stream(const qxh_context* ctx, void** stream) {
+    QXH_REQUIRE(ctx && stream, QXH_ERR_INVALID_ARGUMENT, "context_stream: null argument");
+    *stream = (void*)ctx->stream;
+    return QXH_OK;
+}
+
 // ---------------------------------------------------------------------------
 // graph
 // ---------------------------------------------------------------------------
@@ -185,7 +191,7 @@ extern "C" int32_t qxh_graph_begin(qxh_context* ctx, void* stream, qxh_graph** o
     if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
     qxh_graph* g = new qxh_graph();
     g->ctx = ctx;
-    g->stream = stream ? (hipStream_t)stream : ctx->stream;
+    g->stream = (hipStream_t)stream;  // NULL is the HIP null stream
     g->dispatches = 0;
     g->submitted = false;
     g->capturing = false;

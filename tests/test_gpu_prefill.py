@@ -1,0 +1,139 @@
+"""GPU parity: causal MFMA prefill against the oracle's repeated decode.
+
+The reference runs prompts as repeated decode (crates/qx-runtime/src/lib.rs:1341-1353),
+so prompt row t is decode attention at position start + t over [0, start + t].
+Granite (config 3): fp16 q/k/v, RoPE'd by the fused kernel; the oracle runs
+the fp32 path on the upcast inputs.  Qwen (config 5b): bf16, per-head
+RMSNorm + RoPE; the oracle attends with the GPU's own rotated q/k bits so the
+attention arithmetic is compared in isolation (the front end is checked in
+test_gpu_rope_kv.py).  Tolerance: 2e-3 x output RMS on fp32 outputs; sampled
+rows (first, last and seeded random) at full size.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from qx_amd import abi
+from qx_amd import runtime as rt
+from tests.helpers import TOL_16, log, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    return rt.Context(0)
+
+
+def rows_to_check(T, rng, first=32, last=32, rand=32):
+    r = set(range(min(first, T))) | set(range(max(0, T - last), T))
+    if T > first + last:
+        r |= set(int(x) for x in rng.choice(T, size=min(rand, T), replace=False))
+    return np.array(sorted(r), np.uint32)
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("T,start", [(2048, 0), (100, 0), (77, 30), (1, 5), (33, 0)])
+def test_granite_prefill_fp16(ctx, T, start):
+    log("granite prefill", T, start)
+    rng = np.random.default_rng(T * 31 + start)
+    cap = start + T
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, cap, abi.F16)
+    pre_q = rng.standard_normal((start, 16, 64), dtype=np.float32).astype(np.float16)
+    pre_k = rng.standard_normal((start, 8, 64), dtype=np.float32).astype(np.float16)
+    pre_v = rng.standard_normal((start, 8, 64), dtype=np.float32).astype(np.float16)
+    q = rng.standard_normal((T, 16, 64), dtype=np.float32).astype(np.float16)
+    k = rng.standard_normal((T, 8, 64), dtype=np.float32).astype(np.float16)
+    v = rng.standard_normal((T, 8, 64), dtype=np.float32).astype(np.float16)
+    cuda = lambda a: torch.from_numpy(a).cuda()
+    with rt.Graph(ctx) as g:
+        if start:
+            rt.rope_kv_batch(g, arena, 0, 0, cuda(pre_q)[None], cuda(pre_k)[None], cuda(pre_v)[None])
+        qo = torch.empty((1, T, 16, 64), dtype=torch.float16, device="cuda:0")
+        rt.rope_kv_batch(g, arena, 0, start, cuda(q)[None], cuda(k)[None], cuda(v)[None], query_out=qo)
+        out = rt.prefill_attention(g, arena, 0, start, qo[0], out_dtype=torch.float32)
+    # oracle: the fp32 path on upcast inputs (apply_granite_rope + KvCache + attend)
+    ref = O.KvCache(cap)
+    allk = np.concatenate([pre_k, k]).astype(np.float32)
+    allv = np.concatenate([pre_v, v]).astype(np.float32)
+    allq = np.concatenate([pre_q, q]).astype(np.float32)
+    qrot = np.zeros((cap, 1024), np.float32)
+    for p in range(cap):
+        qr, kr = O.apply_granite_rope(allq[p].ravel(), allk[p].ravel(), p)
+        qrot[p] = qr
+        ref.append(p, kr, allv[p].ravel())
+    rows = rows_to_check(T, rng)
+    r = O.granite_prefill_rows(qrot[start:], ref, start, rows)
+    got = out.cpu().numpy().reshape(T, 1024)[rows]
+    e = rel_err(got, r)
+    log(f"granite prefill T={T} start={start}: max-abs/rms {e:.3e} over {rows.size} rows")
+    assert e <= TOL_16
+
+
+@pytest.mark.parametrize("T,start", [(8192, 0), (300, 0), (129, 64)])
+def test_qwen_prefill_bf16(ctx, T, start):
+    log("qwen prefill", T, start)
+    rng = np.random.default_rng(T + 7 * start)
+    cap = start + T
+    dt = torch.bfloat16
+    arena = rt.KvArena(ctx, abi.SHAPE_QWEN3, 1, 1, cap, abi.BF16)
+    qin = torch.empty((1, cap, 32, 128), dtype=dt, device="cuda:0")
+    kin = torch.empty((1, cap, 4, 128), dtype=dt, device="cuda:0")
+    vin = torch.empty((1, cap, 4, 128), dtype=dt, device="cuda:0")
+    qo = torch.empty_like(qin)
+    with rt.Graph(ctx) as g:
+        for i, t in enumerate((qin, kin, vin)):
+            rt.fill_normal(g, t, seed=100 * T + i)
+        if start:
+            rt.rope_kv_batch(g, arena, 0, 0, qin[:, :start].contiguous(), kin[:, :start].contiguous(),
+                             vin[:, :start].contiguous())
+        qtail = qo[:, start:].contiguous()
+        rt.rope_kv_batch(g, arena, 0, start, qin[:, start:].contiguous(), kin[:, start:].contiguous(),
+                         vin[:, start:].contiguous(), query_out=qtail)
+        out = rt.prefill_attention(g, arena, 0, start, qtail[0], out_dtype=torch.float32)
+        out16 = rt.prefill_attention(g, arena, 0, start, qtail[0])
+        kk, vv = arena.gather(g, 0, 0, 0, cap)
+    rows = rows_to_check(T, rng, 24, 24, 24)
+    rb, rf = O.qwen_prefill_rows(bits(qtail[0]), bits(kk), bits(vv), start, rows, O.BF16)
+    got = out.cpu().numpy().reshape(T, 4096)[rows]
+    e = rel_err(got, rf)
+    log(f"qwen prefill T={T} start={start}: max-abs/rms {e:.3e} over {rows.size} rows")
+    assert e <= TOL_16
+    # the bf16 output is the RNE rounding of the fp32 result
+    assert np.array_equal(bits(out16).reshape(T, 4096), O.to_bits16(out.cpu().numpy(), O.BF16).reshape(T, 4096))
+
+
+@pytest.mark.parametrize("shape,dtype", [(abi.SHAPE_GRANITE, abi.F16), (abi.SHAPE_QWEN3, abi.BF16)])
+def test_prefill_last_row_equals_decode(ctx, shape, dtype):
+    """Size-independent property: prefill row t == decode at length start+t+1."""
+    info = rt.shape_info(shape)
+    T = 1000
+    tdt = rt.torch_dtype(dtype)
+    arena = rt.KvArena(ctx, shape, 1, 1, T, dtype)
+    q = torch.empty((T, info.q_heads, info.head_dim), dtype=tdt, device="cuda:0")
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=11, length=T)
+        rt.fill_normal(g, q, seed=12)
+        pre = rt.prefill_attention(g, arena, 0, 0, q, out_dtype=torch.float32)
+        for t in (0, 511, T - 1):
+            dec = rt.attention(g, arena, 0, q[t:t + 1].contiguous(), t + 1, out_dtype=torch.float32)
+            assert rel_err(pre[t].cpu().numpy(), dec[0].cpu().numpy()) <= TOL_16, t
+
+
+def test_prefill_rejects_rows_beyond_cursor_and_fp32(ctx):
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, 64, abi.F16)
+    arena.set_len(10)
+    q = torch.zeros((11, 16, 64), dtype=torch.float16, device="cuda:0")
+    with rt.Graph(ctx) as g:
+        with pytest.raises(abi.QxhError, match="beyond committed length"):
+            rt.prefill_attention(g, arena, 0, 0, q)
+    a32 = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, 64, abi.F32)
+    a32.set_len(10)
+    with rt.Graph(ctx) as g:
+        with pytest.raises(abi.QxhError) as ei:
+            rt.prefill_attention(g, a32, 0, 0, torch.zeros((10, 16, 64), device="cuda:0"))
+        assert ei.value.code == abi.QXH_ERR_UNSUPPORTED
