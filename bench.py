@@ -248,9 +248,10 @@ def bench_prefill(ctx, steps, warmup, shape_name):
         for i, t in enumerate((q, k, v)):
             rt.fill_normal(g, t, seed=200 + i)
         rt.rope_kv_batch(g, arena, 0, 0, q, k, v, query_out=qo)
+    ws = torch.empty(max(rt.prefill_workspace_bytes(arena, T), 1), dtype=torch.uint8, device="cuda:0")
     g = rt.Graph(ctx, stream)
     g.capture_begin()
-    rt.prefill_attention(g, arena, 0, 0, qo[0], out=out)
+    rt.prefill_attention(g, arena, 0, 0, qo[0], out=out, workspace=ws)
     replay = g.capture_end()
     g.discard()
     ms = timed(lambda: replay.launch(stream), steps, warmup, stream)

@@ -245,10 +245,15 @@ QXH_API int32_t qxh_encode_attention_for_layer(qxh_graph* graph, qxh_kv_cache* c
  * The reference runs prompts as repeated decode (crates/qx-runtime/src/lib.rs:1341-1353);
  * its K-wide verifier attention (encode_attention_batch_with_plan,
  * crates/qx-metal/src/lib.rs:8206-8267) is the multi-query counterpart.
- * fp16/bf16 caches run on MFMA with fp32 accumulation. */
+ * fp16/bf16 caches run on MFMA with fp32 accumulation; P.V runs in f16.  For
+ * bf16 caches a workgroup that meets a V value outside the f16 range is
+ * recomputed by an exact bf16 pass; `workspace` (>= qxh_prefill_workspace_bytes,
+ * zero bytes for fp16 caches) holds its per-workgroup flags. */
+QXH_API int32_t qxh_prefill_workspace_bytes(const qxh_kv_cache* cache, uint32_t tokens, uint64_t* bytes);
 QXH_API int32_t qxh_encode_prefill_attention(qxh_graph* graph, qxh_kv_cache* cache, uint32_t layer, uint32_t sequence,
                                      uint32_t start_position, uint32_t tokens, const void* query,
-                                     int32_t query_dtype, void* output, int32_t output_dtype);
+                                     int32_t query_dtype, void* output, int32_t output_dtype, void* workspace,
+                                     uint64_t workspace_bytes);
 
 /* Position-major token rows [count][kv_heads][head_dim] (cache dtypes) out of
  * the head-major arena, for consumers that read KV by token

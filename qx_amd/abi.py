@@ -97,8 +97,9 @@ SIGNATURES = {
     "qxh_attention_workspace_bytes": (c_int32, [c_void_p, c_uint32, c_uint32, P(c_uint64)]),
     "qxh_encode_attention_for_layer": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32,
                                                  c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_uint64]),
+    "qxh_prefill_workspace_bytes": (c_int32, [c_void_p, c_uint32, P(c_uint64)]),
     "qxh_encode_prefill_attention": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32,
-                                               c_void_p, c_int32, c_void_p, c_int32]),
+                                               c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_uint64]),
     "qxh_encode_kv_gather_token_rows": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32,
                                                   c_void_p, c_void_p]),
     "qxh_granite_block_workspace_bytes": (c_int32, [c_void_p, c_uint32, P(c_uint64)]),

@@ -69,9 +69,10 @@ hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const 
                                    uint32_t length, const void* query, int query_dtype, void* out, int out_dtype,
                                    void* workspace, hipStream_t st, int* dispatches);
 
+uint64_t prefill_workspace_bytes(const ShapeDims& s, int kv_dtype, uint32_t tokens);
 hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint32_t start_position, uint32_t tokens,
-                                    const void* query, int query_dtype, void* out, int out_dtype, hipStream_t st,
-                                    int* dispatches);
+                                    const void* query, int query_dtype, void* out, int out_dtype, void* workspace,
+                                    hipStream_t st, int* dispatches);
 
 // Granite attention block (fp32 dense weights).
 struct GraniteBlockArgs {

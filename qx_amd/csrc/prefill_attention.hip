@@ -13,17 +13,22 @@
 // position map is the same for both operands, so the contraction is exact
 // whatever the hardware's internal k order is.
 //
-// Work decomposition: a workgroup of 4 waves shares one K/V head.  Each wave
+// Work decomposition: a workgroup of 8 waves shares one K/V head.  Each wave
 // owns 32 queries (two 16-column blocks) of one query head; the workgroup
-// covers HW heads of the GQA group x QW query blocks.  K/V tiles of 32
-// positions are staged through double-buffered LDS by all 256 threads while
-// the previous tile is consumed.  Tiles above the causal diagonal are never
+// covers HW heads of the GQA group x QW query blocks (Qwen: the 8 heads of a
+// group; Granite: 2 heads x 4 query blocks).  K/V tiles of 64 positions are
+// staged through double-buffered, padded LDS by all 512 threads, with the
+// global loads of tile t+2 in flight while tile t is consumed.  Tiles above the causal diagonal are never
 // loaded; the diagonal tile is masked per element.  Query blocks are issued
 // last-first so the longest rows start first.
 //
-// bf16 operands: rounding the probabilities P to bf16 would cost ~7e-3 of
-// output RMS, so P is split into bf16 hi + lo parts and the P.V product runs
-// twice (error ~2^-16).  f16 P needs no split.
+// Precision of P.V: rounding the probabilities to bf16 would cost ~7e-3 of
+// output RMS, so P.V always runs in f16 (P to f16 costs ~8e-4).  bf16 value
+// tiles are converted to f16 while they are staged into LDS (exact inside the
+// f16 range).  A tile holding any value outside that range is voted at the
+// staging barrier; such a workgroup records a flag and leaves its rows to a
+// second, exact kernel (EXACT = true) that keeps V in bf16 and splits P into
+// bf16 hi + lo parts.  The exact kernel's other workgroups exit at once.
 #include "common.h"
 #include "internal.h"
 
@@ -46,6 +51,7 @@ struct PrefillArgs {
     int group;
     int out_dtype;
     float scale_log2;      // softmax scale * log2(e)
+    uint32_t* flags;       // per-workgroup "V outside the f16 range" votes (bf16 caches)
 };
 
 template <int DT> struct MfmaT;
@@ -61,28 +67,54 @@ template <> struct MfmaT<BF16> {
     __device__ __forceinline__ static f32x4 mma(const vec& a, const vec& b, const f32x4& c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
     }
-    __device__ __forceinline__ static __bf16 cvt(float x) {
-        return __builtin_bit_cast(__bf16, f32_to_bf16_bits(x));
-    }
+    __device__ __forceinline__ static __bf16 cvt(float x) { return (__bf16)x; }
 };
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-template <int D, int DT, int HW, int QW, bool PSPLIT>
-__global__ __launch_bounds__(256, 2) void prefill_attention_kernel(PrefillArgs a) {
-    using M = MfmaT<DT>;
+// Convert 8 packed bf16 to 8 packed f16 (RNE; exact for |v| in the f16 normal
+// range).  Sets `ovf` when a value is not representable as a finite f16.
+__device__ __forceinline__ u32x4 bf16x8_to_f16x8(const u32x4& v, bool& ovf) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float lo = __uint_as_float(v[i] << 16);
+        const float hi = __uint_as_float(v[i] & 0xffff0000u);
+        ovf |= !(__builtin_fabsf(lo) <= 65504.0f) || !(__builtin_fabsf(hi) <= 65504.0f);
+        const _Float16 a = (_Float16)lo, b = (_Float16)hi;
+        r[i] = (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+    }
+    return r;
+}
+
+template <int D, int DT, int HW, int QW, bool EXACT>
+__global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a) {
+    using M = MfmaT<DT>;             // Q.K operands (the cache dtype)
+    using MH = MfmaT<F16>;           // P.V operands: f16 probabilities and f16 values
     using vec = typename M::vec;
+    using hvec = typename MH::vec;
+    constexpr int WAVES = 8;
     constexpr int KSTEPS = D / 32;      // 32-dim k-steps of Q.K
     constexpr int DTILES = D / 16;      // 16-dim output tiles
-    constexpr int BN = 32;              // positions per tile
-    constexpr int ROWB = D * 2 + 16;    // padded LDS row (bytes)
-    constexpr int TILEB = BN * ROWB;
-    constexpr int CHUNKS = BN * D * 2 / 16;   // 16-byte chunks per K (or V) tile
-    constexpr int CPT = (2 * CHUNKS) / 256;    // chunks per thread (K and V)
-    static_assert(HW * QW == 4, "4 waves per workgroup");
-    static_assert(CPT >= 1 && CPT * 256 == 2 * CHUNKS, "tile staging must divide evenly");
+    constexpr int BN = 64;              // positions per tile
+    constexpr int MT = BN / 16;         // 16-position blocks per tile
+    constexpr int KROWB = D * 2 + 16;   // padded K row: 16 lanes reading 16 rows hit distinct banks
+    constexpr int VROWB = D * 2 + 32;   // padded V row: the 4 rows of a transposed read hit distinct banks
+    constexpr int KTILEB = BN * KROWB;
+    constexpr int VTILEB = BN * VROWB;
+    constexpr int CHUNKS = BN * D * 2 / 16;            // 16-byte chunks per K (or V) tile
+    constexpr int CPT = (2 * CHUNKS) / (64 * WAVES);   // chunks per thread (K and V)
+    static_assert(HW * QW == WAVES, "one wave per (head, 32-query block)");
+    static_assert(CPT >= 1 && CPT * 64 * WAVES == 2 * CHUNKS, "tile staging must divide evenly");
 
-    __shared__ __attribute__((aligned(16))) char lds[2][2][TILEB];  // [buffer][K, V]
+    __shared__ __attribute__((aligned(16))) char lds_k[2][KTILEB];
+    __shared__ __attribute__((aligned(16))) char lds_v[2][VTILEB];  // f16 (fast) or the cache dtype (exact)
+
+    const uint32_t wg_id = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    if constexpr (EXACT) {
+        // only workgroups whose fast pass met a V value outside the f16 range
+        if (a.flags[wg_id] == 0) return;
+    }
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -100,6 +132,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(PrefillArgs a
     const bool wave_live = q0 < T;
     const uint32_t wave_kv = wave_live ? a.start + min(T - 1, q0 + 31) + 1 : 0;
     const uint32_t wave_tiles = (wave_kv + BN - 1) / BN;
+    const float c = a.scale_log2;
 
     const char* kbase = reinterpret_cast<const char*>(a.keys) + (size_t)kvh * a.head_stride * 2;
     const char* vbase = reinterpret_cast<const char*>(a.values) + (size_t)kvh * a.head_stride * 2;
@@ -120,127 +153,194 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(PrefillArgs a
     for (int dt = 0; dt < DTILES; ++dt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float mrun[2] = {-1.0e30f, -1.0e30f};
+    float mrun[2] = {-1.0e30f, -1.0e30f};  // running max of raw q.k (unscaled)
     float lrun[2] = {0.f, 0.f};
 
-    // staging: thread moves CPT 16-byte chunks of the K and V tiles
-    u32x4 stage[CPT];
-    auto load_tile = [&](uint32_t t) {
+    // staging: each thread moves CPT 16-byte chunks of the K and V tiles
+    auto load_tile = [&](uint32_t t, u32x4 (&st)[CPT]) {
 #pragma unroll
-        for (int c = 0; c < CPT; ++c) {
-            const int idx = tid + c * 256;            // [0, 2*CHUNKS)
+        for (int cc = 0; cc < CPT; ++cc) {
+            const int idx = tid + cc * 64 * WAVES;    // [0, 2*CHUNKS)
             const int which = idx / CHUNKS;           // 0 = K, 1 = V
             const int rem = idx % CHUNKS;
             const int row = rem / (D / 8), col = rem % (D / 8);
             const uint32_t pos = t * BN + row;
             if (pos < kv_len) {
                 const char* src = (which ? vbase : kbase) + ((size_t)pos * D + col * 8) * 2;
-                stage[c] = *reinterpret_cast<const u32x4*>(src);
+                st[cc] = *reinterpret_cast<const u32x4*>(src);
             } else {
-                stage[c] = u32x4{0u, 0u, 0u, 0u};
+                st[cc] = u32x4{0u, 0u, 0u, 0u};
             }
         }
     };
-    auto store_tile = [&](int buf) {
+    // returns true when some V value of this thread's chunks is not a finite f16
+    auto store_tile = [&](int buf, const u32x4 (&st)[CPT]) -> bool {
+        bool ovf = false;
 #pragma unroll
-        for (int c = 0; c < CPT; ++c) {
-            const int idx = tid + c * 256;
+        for (int cc = 0; cc < CPT; ++cc) {
+            const int idx = tid + cc * 64 * WAVES;
             const int which = idx / CHUNKS;
             const int rem = idx % CHUNKS;
             const int row = rem / (D / 8), col = rem % (D / 8);
-            *reinterpret_cast<u32x4*>(&lds[buf][which][row * ROWB + col * 16]) = stage[c];
+            if (which == 0) {
+                *reinterpret_cast<u32x4*>(&lds_k[buf][row * KROWB + col * 16]) = st[cc];
+            } else {
+                u32x4 h = st[cc];
+                if constexpr (DT == BF16 && !EXACT) h = bf16x8_to_f16x8(st[cc], ovf);
+                *reinterpret_cast<u32x4*>(&lds_v[buf][row * VROWB + col * 16]) = h;
+            }
         }
+        return ovf;
     };
-
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
 
     const uint32_t qpos_base = a.start + q0;  // position of this wave's first query row
 
-    for (uint32_t t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
-        if (t + 1 < ntiles) load_tile(t + 1);
-        if (t < wave_tiles) {
-            const char* kl = lds[buf][0];
-            const char* vl = lds[buf][1];
-            // ---- S^T = K . Q^T --------------------------------------------------
-            f32x4 sacc[2][2];
+    auto compute = [&](uint32_t t, int buf) {
+        const char* kl = lds_k[buf];
+        const char* vl = lds_v[buf];
+        // ---- S^T = K . Q^T ------------------------------------------------------
+        f32x4 sacc[MT][2];
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) sacc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int nt = 0; nt < 2; ++nt) sacc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < KSTEPS; ++ks) {
+        for (int ks = 0; ks < KSTEPS; ++ks) {
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt) {
-                    const vec kop = __builtin_bit_cast(
-                        vec, *reinterpret_cast<const u32x4*>(kl + (mt * 16 + li) * ROWB + (32 * ks + 8 * lg) * 2));
+            for (int mt = 0; mt < MT; ++mt) {
+                const vec kop = __builtin_bit_cast(
+                    vec, *reinterpret_cast<const u32x4*>(kl + (mt * 16 + li) * KROWB + (32 * ks + 8 * lg) * 2));
 #pragma unroll
-                    for (int nt = 0; nt < 2; ++nt) sacc[mt][nt] = M::mma(kop, qop[nt][ks], sacc[mt][nt]);
-                }
-            }
-            // ---- online softmax per query column -----------------------------------
-            const uint32_t tpos = t * BN;
-            const bool need_mask = tpos + BN - 1 > qpos_base;
-            vec pop[2];
-            vec plo[2];
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const uint32_t qpos = qpos_base + 16 * nt + li;
-                float s[2][4];
-                float tmax = -INFINITY;
-#pragma unroll
-                for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        float v = sacc[mt][nt][j] * a.scale_log2;
-                        if (need_mask && tpos + mt * 16 + 4 * lg + j > qpos) v = -INFINITY;
-                        s[mt][j] = v;
-                        tmax = fmaxf(tmax, v);
-                    }
-                tmax = fmaxf(tmax, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(tmax), 0x401F)));
-                tmax = fmaxf(tmax, bperm_xor(tmax, 32));
-                const float mnew = fmaxf(mrun[nt], tmax);
-                const float alpha = fast_exp2(mrun[nt] - mnew);
-                mrun[nt] = mnew;
-                float psum = 0.f;
-#pragma unroll
-                for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const float p = fast_exp2(s[mt][j] - mnew);
-                        psum += p;
-                        const auto ph = M::cvt(p);
-                        pop[nt][mt * 4 + j] = ph;
-                        if constexpr (PSPLIT) plo[nt][mt * 4 + j] = M::cvt(p - (float)ph);
-                    }
-                lrun[nt] = __builtin_fmaf(lrun[nt], alpha, psum);
-#pragma unroll
-                for (int dt = 0; dt < DTILES; ++dt) oacc[dt][nt] *= alpha;
-            }
-            // ---- O^T += V^T . P^T -------------------------------------------------
-#pragma unroll
-            for (int dt = 0; dt < DTILES; ++dt) {
-                // lane (lg, li) addresses row base + li/4, dims 16*dt + 4*(li%4): after the
-                // transpose it holds V[base + j][16*dt + li] for j = 0..3
-                const int coloff = (16 * dt + 4 * (li & 3)) * 2;
-                const lds_i16x4* p0 = (const lds_i16x4*)(vl + (4 * lg + (li >> 2)) * ROWB + coloff);
-                const lds_i16x4* p1 = (const lds_i16x4*)(vl + (16 + 4 * lg + (li >> 2)) * ROWB + coloff);
-                const i16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p0));
-                const i16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p1));
-                typedef short i16x8 __attribute__((ext_vector_type(8)));
-                const i16x8 vv = __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
-                const vec vop = __builtin_bit_cast(vec, vv);
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
-                    oacc[dt][nt] = M::mma(vop, pop[nt], oacc[dt][nt]);
-                    if constexpr (PSPLIT) oacc[dt][nt] = M::mma(vop, plo[nt], oacc[dt][nt]);
-                }
+                for (int nt = 0; nt < 2; ++nt) sacc[mt][nt] = M::mma(kop, qop[nt][ks], sacc[mt][nt]);
             }
         }
-        if (t + 1 < ntiles) store_tile((t + 1) & 1);
-        __syncthreads();
+        // ---- online softmax per query column (log2 domain, scale folded into fma) ----
+        const uint32_t tpos = t * BN;
+        const bool need_mask = tpos + BN - 1 > qpos_base;
+        float prob[MT][2][4];
+        bool rescale = false;
+        float alpha[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const uint32_t qpos = qpos_base + 16 * nt + li;
+            if (need_mask) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (tpos + mt * 16 + 4 * lg + j > qpos) sacc[mt][nt][j] = -INFINITY;
+            }
+            float tmax = sacc[0][nt][0];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, sacc[mt][nt][j]);
+            tmax = fmaxf(tmax, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(tmax), 0x401F)));
+            tmax = fmaxf(tmax, bperm_xor(tmax, 32));
+            const float mnew = fmaxf(mrun[nt], tmax);
+            alpha[nt] = fast_exp2((mrun[nt] - mnew) * c);
+            rescale |= mnew != mrun[nt];
+            mrun[nt] = mnew;
+            const float moff = -mnew * c;
+            float psum = 0.f;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float p = fast_exp2(__builtin_fmaf(sacc[mt][nt][j], c, moff));
+                    psum += p;
+                    prob[mt][nt][j] = p;
+                }
+            lrun[nt] = __builtin_fmaf(lrun[nt], alpha[nt], psum);
+        }
+        if (__any(rescale)) {
+#pragma unroll
+            for (int dt = 0; dt < DTILES; ++dt)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] *= alpha[nt];
+        }
+        // ---- O^T += V^T . P^T (two 32-position k-steps) ------------------------------
+        // lane (lg, li) addresses row base + li/4, dims 16*dt + 4*(li%4); after the
+        // transpose it holds V[base + j][16*dt + li] for j = 0..3
+        auto vt_operand = [&](int kp, int dt) {
+            const int coloff = (16 * dt + 4 * (li & 3)) * 2;
+            const int rbase = 32 * kp + 4 * lg + (li >> 2);
+            const lds_i16x4* p0 = (const lds_i16x4*)(vl + rbase * VROWB + coloff);
+            const lds_i16x4* p1 = (const lds_i16x4*)(vl + (rbase + 16) * VROWB + coloff);
+            const i16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p0));
+            const i16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p1));
+            return __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
+        };
+        if constexpr (!EXACT) {
+            // f16 probabilities against the f16 V tile: one MFMA per (dt, nt, k-step)
+            hvec pop[MT / 2][2];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) pop[mt / 2][nt][(mt & 1) * 4 + j] = (_Float16)prob[mt][nt][j];
+#pragma unroll
+            for (int kp = 0; kp < MT / 2; ++kp)
+#pragma unroll
+                for (int dt = 0; dt < DTILES; ++dt) {
+                    const hvec vop = __builtin_bit_cast(hvec, vt_operand(kp, dt));
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = MH::mma(vop, pop[kp][nt], oacc[dt][nt]);
+                }
+        } else {
+            // exact: cache-dtype values, probabilities split into hi + lo parts of that dtype
+            vec phi[MT / 2][2], plo[MT / 2][2];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const auto h = M::cvt(prob[mt][nt][j]);
+                        phi[mt / 2][nt][(mt & 1) * 4 + j] = h;
+                        plo[mt / 2][nt][(mt & 1) * 4 + j] = M::cvt(prob[mt][nt][j] - (float)h);
+                    }
+#pragma unroll
+            for (int kp = 0; kp < MT / 2; ++kp)
+#pragma unroll
+                for (int dt = 0; dt < DTILES; ++dt) {
+                    const vec vop = __builtin_bit_cast(vec, vt_operand(kp, dt));
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) {
+                        oacc[dt][nt] = M::mma(vop, phi[kp][nt], oacc[dt][nt]);
+                        oacc[dt][nt] = M::mma(vop, plo[kp][nt], oacc[dt][nt]);
+                    }
+                }
+        }
+    };
+
+    // Two register stages: the loads of tile t+2 are in flight while tile t is
+    // consumed and tile t+1 (loaded one iteration earlier) is written to LDS.
+    // The barrier after each LDS write also votes whether that tile holds V
+    // values outside the f16 range.
+    u32x4 st0[CPT], st1[CPT];
+    load_tile(0, st0);
+    bool any_ovf = __syncthreads_or(store_tile(0, st0));
+    if (ntiles > 1) load_tile(1, st1);
+    for (uint32_t t = 0; t < ntiles; t += 2) {
+        // even tile t in buffer 0; st1 holds tile t+1
+        if (t + 2 < ntiles) load_tile(t + 2, st0);
+        if (t < wave_tiles) compute(t, 0);
+        bool f = false;
+        if (t + 1 < ntiles) f = store_tile(1, st1);
+        any_ovf |= __syncthreads_or(f);
+        if (t + 1 >= ntiles) break;
+        // odd tile t+1 in buffer 1; st0 holds tile t+2
+        if (t + 3 < ntiles) load_tile(t + 3, st1);
+        if (t + 1 < wave_tiles) compute(t + 1, 1);
+        f = false;
+        if (t + 2 < ntiles) f = store_tile(0, st0);
+        any_ovf |= __syncthreads_or(f);
+    }
+    if constexpr (!EXACT) {
+        if (a.flags && tid == 0) a.flags[wg_id] = any_ovf ? 1u : 0u;
+        if (any_ovf) return;  // the exact pass owns this workgroup's rows
     }
 
     if (!wave_live) return;
@@ -261,9 +361,15 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(PrefillArgs a
     }
 }
 
+uint64_t prefill_workspace_bytes(const ShapeDims& s, int kv_dtype, uint32_t tokens) {
+    if (kv_dtype != BF16) return 0;
+    const uint32_t qb = s.head_dim == 64 ? (tokens + 127) / 128 : (tokens + 31) / 32;
+    return (uint64_t)qb * s.kv_heads * sizeof(uint32_t);
+}
+
 hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint32_t start_position, uint32_t tokens,
-                                    const void* query, int query_dtype, void* out, int out_dtype, hipStream_t st,
-                                    int* dispatches) {
+                                    const void* query, int query_dtype, void* out, int out_dtype, void* workspace,
+                                    hipStream_t st, int* dispatches) {
     *dispatches = 0;
     if (kv.key_dtype != kv.value_dtype || kv.key_dtype != query_dtype || kv.key_dtype == F32)
         return hipErrorNotSupported;
@@ -279,22 +385,28 @@ hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint3
     a.group = s.group;
     a.out_dtype = out_dtype;
     a.scale_log2 = s.scale * kLog2e;
+    a.flags = reinterpret_cast<uint32_t*>(workspace);
+    const bool bf = query_dtype == BF16;
     if (s.head_dim == 64 && s.group == 2) {
-        dim3 grid((tokens + 63) / 64, s.kv_heads, 1);
-        if (query_dtype == F16)
-            hipLaunchKernelGGL((prefill_attention_kernel<64, F16, 2, 2, false>), grid, dim3(256), 0, st, a);
-        else
-            hipLaunchKernelGGL((prefill_attention_kernel<64, BF16, 2, 2, true>), grid, dim3(256), 0, st, a);
+        dim3 grid((tokens + 127) / 128, s.kv_heads, 1);
+        if (!bf) {
+            hipLaunchKernelGGL((prefill_attention_kernel<64, F16, 2, 4, false>), grid, dim3(512), 0, st, a);
+        } else {
+            hipLaunchKernelGGL((prefill_attention_kernel<64, BF16, 2, 4, false>), grid, dim3(512), 0, st, a);
+            hipLaunchKernelGGL((prefill_attention_kernel<64, BF16, 2, 4, true>), grid, dim3(512), 0, st, a);
+        }
     } else if (s.head_dim == 128 && s.group == 8) {
-        dim3 grid((tokens + 31) / 32, s.kv_heads, 2);
-        if (query_dtype == F16)
-            hipLaunchKernelGGL((prefill_attention_kernel<128, F16, 4, 1, false>), grid, dim3(256), 0, st, a);
-        else
-            hipLaunchKernelGGL((prefill_attention_kernel<128, BF16, 4, 1, true>), grid, dim3(256), 0, st, a);
+        dim3 grid((tokens + 31) / 32, s.kv_heads, 1);
+        if (!bf) {
+            hipLaunchKernelGGL((prefill_attention_kernel<128, F16, 8, 1, false>), grid, dim3(512), 0, st, a);
+        } else {
+            hipLaunchKernelGGL((prefill_attention_kernel<128, BF16, 8, 1, false>), grid, dim3(512), 0, st, a);
+            hipLaunchKernelGGL((prefill_attention_kernel<128, BF16, 8, 1, true>), grid, dim3(512), 0, st, a);
+        }
     } else {
         return hipErrorNotSupported;
     }
-    *dispatches = 1;
+    *dispatches = bf ? 2 : 1;
     return hipGetLastError();
 }
 

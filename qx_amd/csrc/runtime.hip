@@ -619,9 +619,17 @@ extern "C" int32_t qxh_encode_attention_for_layer(qxh_graph* g, qxh_kv_cache* c,
     return QXH_OK;
 }
 
+extern "C" int32_t qxh_prefill_workspace_bytes(const qxh_kv_cache* c, uint32_t tokens, uint64_t* bytes) {
+    QXH_REQUIRE(c && bytes, QXH_ERR_INVALID_ARGUMENT, "prefill_workspace_bytes: null argument");
+    QXH_REQUIRE(tokens > 0, QXH_ERR_INVALID_ARGUMENT, "prefill of zero tokens");
+    *bytes = prefill_workspace_bytes(c->dims, c->desc.key_dtype, tokens);
+    return QXH_OK;
+}
+
 extern "C" int32_t qxh_encode_prefill_attention(qxh_graph* g, qxh_kv_cache* c, uint32_t layer, uint32_t seq,
                                                 uint32_t start, uint32_t tokens, const void* query,
-                                                int32_t query_dtype, void* output, int32_t output_dtype) {
+                                                int32_t query_dtype, void* output, int32_t output_dtype,
+                                                void* workspace, uint64_t workspace_bytes) {
     int32_t r = check_graph(g);
     if (r) return r;
     if ((r = check_range(c, layer, seq, 1))) return r;
@@ -632,9 +640,13 @@ extern "C" int32_t qxh_encode_prefill_attention(qxh_graph* g, qxh_kv_cache* c, u
     QXH_REQUIRE((uint64_t)start + tokens <= c->at(layer, seq), QXH_ERR_KV_POSITION,
                 "prefill rows end at %llu beyond committed length %u", (unsigned long long)start + tokens,
                 c->at(layer, seq));
+    const uint64_t need = prefill_workspace_bytes(c->dims, c->desc.key_dtype, tokens);
+    QXH_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), QXH_ERR_INVALID_ARGUMENT,
+                "prefill workspace holds %llu bytes, needs %llu", (unsigned long long)workspace_bytes,
+                (unsigned long long)need);
     int dispatches = 0;
     hipError_t e = launch_prefill_attention(c->dims, kv_layer(c, layer, seq), start, tokens, query, query_dtype,
-                                            output, output_dtype, g->stream, &dispatches);
+                                            output, output_dtype, need ? workspace : nullptr, g->stream, &dispatches);
     if (e == hipErrorNotSupported)
         return fail(QXH_ERR_UNSUPPORTED, "prefill: no kernel for this KV dtype / query dtype combination");
     if (e != hipSuccess) return hip_fail(e, "prefill launch");

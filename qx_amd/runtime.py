@@ -285,14 +285,25 @@ def attention(graph: Graph, cache: KvArena, layer: int, query, length: int, out=
     return out
 
 
+def prefill_workspace_bytes(cache: KvArena, tokens: int) -> int:
+    n = ctypes.c_uint64()
+    check(lib().qxh_prefill_workspace_bytes(cache.handle, tokens, ctypes.byref(n)))
+    return n.value
+
+
 def prefill_attention(graph: Graph, cache: KvArena, layer: int, start_position: int, query, out=None, out_dtype=None,
-                      sequence: int = 0):
+                      sequence: int = 0, workspace=None):
     """Causal prefill: query [tokens][q_heads][d]; row t attends [0, start+t]."""
     tokens = query.shape[0]
     if out is None:
         out = torch.empty(query.shape, dtype=out_dtype or query.dtype, device=query.device)
+    need = prefill_workspace_bytes(cache, tokens)
+    if workspace is None and need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=query.device)
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     check(lib().qxh_encode_prefill_attention(graph.handle, cache.handle, layer, sequence, start_position, tokens,
-                                             _ptr(query), qxh_dtype(query), _ptr(out), qxh_dtype(out)))
+                                             _ptr(query), qxh_dtype(query), _ptr(out), qxh_dtype(out),
+                                             _ptr(workspace), ws_bytes))
     return out
 
 

@@ -124,6 +124,44 @@ def test_prefill_last_row_equals_decode(ctx, shape, dtype):
             assert rel_err(pre[t].cpu().numpy(), dec[0].cpu().numpy()) <= TOL_16, t
 
 
+@pytest.mark.parametrize("shape", [abi.SHAPE_GRANITE, abi.SHAPE_QWEN3])
+def test_bf16_values_outside_f16_range_take_the_exact_pass(ctx, shape):
+    """bf16 V tiles are multiplied in f16; a value beyond the f16 range must
+    route its workgroup to the exact bf16 pass and still match the oracle."""
+    log("prefill overflow path", shape)
+    info = rt.shape_info(shape)
+    T = 300
+    rng = np.random.default_rng(77)
+    arena = rt.KvArena(ctx, shape, 1, 1, T, abi.BF16)
+    q = torch.empty((T, info.q_heads, info.head_dim), dtype=torch.bfloat16, device="cuda:0")
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=21, length=T)
+        rt.fill_normal(g, q, seed=22)
+    # plant a few huge values (finite in bf16, beyond f16) into V rows 5 and 250
+    vptr = arena.layout.values
+    nbytes = T * info.kv_heads * info.head_dim * 2
+    off = vptr - arena.arena.data_ptr()
+    vview = arena.arena[off:off + nbytes].view(torch.bfloat16).view(info.kv_heads, T, info.head_dim)
+    vview[0, 5, 3] = 3.0e5
+    vview[info.kv_heads - 1, 250, 7] = -1.0e9
+    torch.cuda.synchronize()
+    with rt.Graph(ctx) as g:
+        out = rt.prefill_attention(g, arena, 0, 0, q, out_dtype=torch.float32)
+        kk, vv = arena.gather(g, 0, 0, 0, T)
+    rows = np.array([0, 4, 5, 6, 100, 249, 250, 251, 299], np.uint32)
+    if shape == abi.SHAPE_QWEN3:
+        _, ref = O.qwen_prefill_rows(bits(q), bits(kk), bits(vv), 0, rows, O.BF16)
+    else:
+        c = O.KvCache(T)
+        c.extend(kk.float().cpu().numpy(), vv.float().cpu().numpy())
+        ref = O.granite_prefill_rows(q.float().cpu().numpy().reshape(T, -1), c, 0, rows)
+    got = out.cpu().numpy().reshape(T, -1)[rows]
+    assert np.all(np.isfinite(got))
+    e = rel_err(got, ref)
+    log(f"overflow path max-abs/rms {e:.3e}")
+    assert e <= TOL_16
+
+
 def test_prefill_rejects_rows_beyond_cursor_and_fp32(ctx):
     arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, 64, abi.F16)
     arena.set_len(10)
