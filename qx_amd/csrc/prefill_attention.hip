@@ -29,6 +29,8 @@
 // staging barrier; such a workgroup records a flag and leaves its rows to a
 // second, exact kernel (EXACT = true) that keeps V in bf16 and splits P into
 // bf16 hi + lo parts.  The exact kernel's other workgroups exit at once.
+#include <type_traits>
+
 #include "common.h"
 #include "internal.h"
 
@@ -52,6 +54,9 @@ struct PrefillArgs {
     int out_dtype;
     float scale_log2;      // softmax scale * log2(e)
     uint32_t* flags;       // per-workgroup "V outside the f16 range" votes (bf16 caches)
+    uint32_t qblocks;      // query blocks per head
+    uint32_t kv_heads;
+    uint32_t xcd_map;      // 1: XCD-aware block -> (head, query block) mapping
 };
 
 template <int DT> struct MfmaT;
@@ -71,6 +76,42 @@ template <> struct MfmaT<BF16> {
 };
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// Reductions across the four 16-lane groups (which hold the same query column
+// at different positions).  v_permlane{16,32}_swap exchange lane halves on
+// the VALU; with both operands equal, op(result[0], result[1]) is
+// op(v, v from lane ^ 16) (resp. ^ 32) on every lane.
+__device__ __forceinline__ float max_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Scheduling hint: interleave one MFMA with `valu` VALU instructions, n times.
+template <int N, int VALU>
+__device__ __forceinline__ void interleave_mfma_valu() {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, VALU, 0);
+    }
+}
+
+// A running max may lag the true max by up to this many binary orders of
+// magnitude before the accumulators are rescaled; probabilities then stay
+// below 2^8, well inside the f16 range.
+constexpr float kLazyRescale = 8.0f;
 
 // Convert 8 packed bf16 to 8 packed f16 (RNE; exact for |v| in the f16 normal
 // range).  Sets `ovf` when a value is not representable as a finite f16.
@@ -93,6 +134,8 @@ __global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a
     using MH = MfmaT<F16>;           // P.V operands: f16 probabilities and f16 values
     using vec = typename M::vec;
     using hvec = typename MH::vec;
+    // probability operand: f16 on the fast pass, the cache dtype on the exact pass
+    using pvec = typename std::conditional<EXACT, vec, hvec>::type;
     constexpr int WAVES = 8;
     constexpr int KSTEPS = D / 32;      // 32-dim k-steps of Q.K
     constexpr int DTILES = D / 16;      // 16-dim output tiles
@@ -110,7 +153,7 @@ __global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a
     __shared__ __attribute__((aligned(16))) char lds_k[2][KTILEB];
     __shared__ __attribute__((aligned(16))) char lds_v[2][VTILEB];  // f16 (fast) or the cache dtype (exact)
 
-    const uint32_t wg_id = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const uint32_t wg_id = blockIdx.x + gridDim.x * blockIdx.z;
     if constexpr (EXACT) {
         // only workgroups whose fast pass met a V value outside the f16 range
         if (a.flags[wg_id] == 0) return;
@@ -119,10 +162,29 @@ __global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int lg = lane >> 4, li = lane & 15;
-    const int kvh = blockIdx.y;
+    // XCD-aware block mapping: workgroups are dispatched round-robin over the
+    // 8 XCDs (each with its own L2), so block b runs on XCD b % 8.  Give each
+    // XCD the query blocks of one K/V head (or of a fixed share of heads) so
+    // that head's K/V stays resident in that XCD's L2.  Within an XCD, query
+    // blocks go longest-first.
+    const uint32_t nqb = a.qblocks;
+    uint32_t kvh_u, qidx;
+    {
+        const uint32_t lin = blockIdx.x;
+        if (a.xcd_map) {
+            const uint32_t xcd = lin & 7, slot = lin >> 3;
+            const uint32_t per = 8 / a.kv_heads;        // XCDs serving one head
+            kvh_u = xcd / per;
+            qidx = slot * per + (xcd % per);
+        } else {
+            kvh_u = lin / nqb;
+            qidx = lin % nqb;
+        }
+    }
+    const int kvh = (int)kvh_u;
     const int head = kvh * a.group + blockIdx.z * HW + (wave % HW);
     const int qsub = wave / HW;
-    const uint32_t qblock = gridDim.x - 1 - blockIdx.x;  // longest rows first
+    const uint32_t qblock = nqb - 1 - qidx;  // longest rows first
     const uint32_t T = a.tokens;
     const uint32_t wg_q0 = qblock * (32 * QW);
     const uint32_t wg_qlast = min(T, wg_q0 + 32 * QW) - 1;
@@ -195,124 +257,144 @@ __global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a
 
     const uint32_t qpos_base = a.start + q0;  // position of this wave's first query row
 
-    auto compute = [&](uint32_t t, int buf) {
-        const char* kl = lds_k[buf];
-        const char* vl = lds_v[buf];
-        // ---- S^T = K . Q^T ------------------------------------------------------
-        f32x4 sacc[MT][2];
+    // One 64-position tile = two 32-position sub-tiles.  Per sub-tile: S^T by
+    // 16 MFMAs, online softmax, P.V by 16 MFMAs.  Both sub-tiles' Q.K products
+    // are issued first, so the softmax of sub-tile 0 runs on the VALU while
+    // the MFMA pipe still works on sub-tile 1, and the softmax of sub-tile 1
+    // overlaps the P.V of sub-tile 0.
+    auto qk = [&](const char* kl, int sub, f32x4 (&S)[2][2]) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) sacc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int nt = 0; nt < 2; ++nt) S[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
+            for (int mt = 0; mt < 2; ++mt) {
                 const vec kop = __builtin_bit_cast(
-                    vec, *reinterpret_cast<const u32x4*>(kl + (mt * 16 + li) * KROWB + (32 * ks + 8 * lg) * 2));
+                    vec, *reinterpret_cast<const u32x4*>(kl + (sub * 32 + mt * 16 + li) * KROWB + (32 * ks + 8 * lg) * 2));
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) sacc[mt][nt] = M::mma(kop, qop[nt][ks], sacc[mt][nt]);
+                for (int nt = 0; nt < 2; ++nt) S[mt][nt] = M::mma(kop, qop[nt][ks], S[mt][nt]);
             }
         }
-        // ---- online softmax per query column (log2 domain, scale folded into fma) ----
-        const uint32_t tpos = t * BN;
-        const bool need_mask = tpos + BN - 1 > qpos_base;
-        float prob[MT][2][4];
-        bool rescale = false;
-        float alpha[2];
+    };
+    // Online softmax of one 32-position sub-tile.  The running max is lazy: it
+    // moves (and the accumulators are rescaled) only when some query's tile
+    // max exceeds it by more than 2^kLazyRescale.  Probabilities are produced
+    // packed for the P.V operand; their sum comes from v_dot2 on the packed
+    // values, so l and the P.V product see the same rounded probabilities.
+    auto softmax = [&](uint32_t spos, f32x4 (&S)[2][2], pvec (&P)[2], vec (&Plo)[2]) {
+        if (spos + 31 > qpos_base) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            const uint32_t qpos = qpos_base + 16 * nt + li;
-            if (need_mask) {
+            for (int nt = 0; nt < 2; ++nt) {
+                const uint32_t qpos = qpos_base + 16 * nt + li;
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
+                for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        if (tpos + mt * 16 + 4 * lg + j > qpos) sacc[mt][nt][j] = -INFINITY;
+                        if (spos + mt * 16 + 4 * lg + j > qpos) S[mt][nt][j] = -INFINITY;
             }
-            float tmax = sacc[0][nt][0];
+        }
+        float tmax[2];
+        bool need = false;
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
+        for (int nt = 0; nt < 2; ++nt) {
+            float m = fmaxf(fmaxf(fmaxf(S[0][nt][0], S[0][nt][1]), fmaxf(S[0][nt][2], S[0][nt][3])),
+                            fmaxf(fmaxf(S[1][nt][0], S[1][nt][1]), fmaxf(S[1][nt][2], S[1][nt][3])));
+            m = max_xor16(m);
+            tmax[nt] = max_xor32(m);
+            need |= (tmax[nt] - mrun[nt]) * c > kLazyRescale;
+        }
+        if (__any(need)) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, sacc[mt][nt][j]);
-            tmax = fmaxf(tmax, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(tmax), 0x401F)));
-            tmax = fmaxf(tmax, bperm_xor(tmax, 32));
-            const float mnew = fmaxf(mrun[nt], tmax);
-            alpha[nt] = fast_exp2((mrun[nt] - mnew) * c);
-            rescale |= mnew != mrun[nt];
-            mrun[nt] = mnew;
-            const float moff = -mnew * c;
-            float psum = 0.f;
+            for (int nt = 0; nt < 2; ++nt) {
+                const float mnew = fmaxf(mrun[nt], tmax[nt]);
+                const float alpha = fast_exp2((mrun[nt] - mnew) * c);
+                mrun[nt] = mnew;
+                lrun[nt] *= alpha;
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
+                for (int dt = 0; dt < DTILES; ++dt) oacc[dt][nt] *= alpha;
+            }
+        }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float p = fast_exp2(__builtin_fmaf(sacc[mt][nt][j], c, moff));
-                    psum += p;
-                    prob[mt][nt][j] = p;
+        for (int nt = 0; nt < 2; ++nt) {
+            const float moff = -mrun[nt] * c;
+            float p[8];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) p[mt * 4 + j] = fast_exp2(__builtin_fmaf(S[mt][nt][j], c, moff));
+            if constexpr (!EXACT) {
+                typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                float l = lrun[nt];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const h2 pr = {(_Float16)p[2 * k], (_Float16)p[2 * k + 1]};
+                    P[nt][2 * k] = pr[0];
+                    P[nt][2 * k + 1] = pr[1];
+                    l = __builtin_amdgcn_fdot2(pr, h2{(_Float16)1.0f, (_Float16)1.0f}, l, false);
                 }
-            lrun[nt] = __builtin_fmaf(lrun[nt], alpha[nt], psum);
-        }
-        if (__any(rescale)) {
+                lrun[nt] = l;
+            } else {
+                // exact pass: cache-dtype hi + lo parts reproduce p to ~2^-16
+                float l = lrun[nt];
 #pragma unroll
-            for (int dt = 0; dt < DTILES; ++dt)
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] *= alpha[nt];
+                for (int k = 0; k < 8; ++k) {
+                    const auto h = M::cvt(p[k]);
+                    P[nt][k] = h;
+                    Plo[nt][k] = M::cvt(p[k] - (float)h);
+                    l += p[k];
+                }
+                lrun[nt] = l;
+            }
         }
-        // ---- O^T += V^T . P^T (two 32-position k-steps) ------------------------------
-        // lane (lg, li) addresses row base + li/4, dims 16*dt + 4*(li%4); after the
-        // transpose it holds V[base + j][16*dt + li] for j = 0..3
-        auto vt_operand = [&](int kp, int dt) {
-            const int coloff = (16 * dt + 4 * (li & 3)) * 2;
-            const int rbase = 32 * kp + 4 * lg + (li >> 2);
-            const lds_i16x4* p0 = (const lds_i16x4*)(vl + rbase * VROWB + coloff);
-            const lds_i16x4* p1 = (const lds_i16x4*)(vl + (rbase + 16) * VROWB + coloff);
-            const i16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p0));
-            const i16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p1));
-            return __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
-        };
+    };
+    // lane (lg, li) addresses row base + li/4, dims 16*dt + 4*(li%4); after the
+    // transpose it holds V[base + j][16*dt + li] for j = 0..3
+    auto vt_operand = [&](const char* vl, int sub, int dt) {
+        const int coloff = (16 * dt + 4 * (li & 3)) * 2;
+        const int rbase = 32 * sub + 4 * lg + (li >> 2);
+        const lds_i16x4* p0 = (const lds_i16x4*)(vl + rbase * VROWB + coloff);
+        const lds_i16x4* p1 = (const lds_i16x4*)(vl + (rbase + 16) * VROWB + coloff);
+        const i16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p0));
+        const i16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p1));
+        return __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+    auto pv = [&](const char* vl, int sub, const pvec (&P)[2], const vec (&Plo)[2]) {
         if constexpr (!EXACT) {
-            // f16 probabilities against the f16 V tile: one MFMA per (dt, nt, k-step)
-            hvec pop[MT / 2][2];
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
+            for (int dt = 0; dt < DTILES; ++dt) {
+                const hvec vop = __builtin_bit_cast(hvec, vt_operand(vl, sub, dt));
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) pop[mt / 2][nt][(mt & 1) * 4 + j] = (_Float16)prob[mt][nt][j];
-#pragma unroll
-            for (int kp = 0; kp < MT / 2; ++kp)
-#pragma unroll
-                for (int dt = 0; dt < DTILES; ++dt) {
-                    const hvec vop = __builtin_bit_cast(hvec, vt_operand(kp, dt));
-#pragma unroll
-                    for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = MH::mma(vop, pop[kp][nt], oacc[dt][nt]);
-                }
+                for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = MH::mma(vop, P[nt], oacc[dt][nt]);
+            }
         } else {
-            // exact: cache-dtype values, probabilities split into hi + lo parts of that dtype
-            vec phi[MT / 2][2], plo[MT / 2][2];
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
+            for (int dt = 0; dt < DTILES; ++dt) {
+                const vec vop = __builtin_bit_cast(vec, vt_operand(vl, sub, dt));
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const auto h = M::cvt(prob[mt][nt][j]);
-                        phi[mt / 2][nt][(mt & 1) * 4 + j] = h;
-                        plo[mt / 2][nt][(mt & 1) * 4 + j] = M::cvt(prob[mt][nt][j] - (float)h);
-                    }
-#pragma unroll
-            for (int kp = 0; kp < MT / 2; ++kp)
-#pragma unroll
-                for (int dt = 0; dt < DTILES; ++dt) {
-                    const vec vop = __builtin_bit_cast(vec, vt_operand(kp, dt));
-#pragma unroll
-                    for (int nt = 0; nt < 2; ++nt) {
-                        oacc[dt][nt] = M::mma(vop, phi[kp][nt], oacc[dt][nt]);
-                        oacc[dt][nt] = M::mma(vop, plo[kp][nt], oacc[dt][nt]);
-                    }
+                for (int nt = 0; nt < 2; ++nt) {
+                    oacc[dt][nt] = M::mma(vop, P[nt], oacc[dt][nt]);
+                    oacc[dt][nt] = M::mma(vop, Plo[nt], oacc[dt][nt]);
                 }
+            }
         }
+    };
+    auto compute = [&](uint32_t t, int buf) {
+        const char* kl = lds_k[buf];
+        const char* vl = lds_v[buf];
+        const uint32_t tpos = t * BN;
+        f32x4 s0[2][2], s1[2][2];
+        pvec P0[2], P1[2];
+        vec L0[2], L1[2];
+        qk(kl, 0, s0);
+        qk(kl, 1, s1);
+        softmax(tpos, s0, P0, L0);
+        interleave_mfma_valu<8 * KSTEPS / 2, 6>();
+        pv(vl, 0, P0, L0);
+        softmax(tpos + 32, s1, P1, L1);
+        interleave_mfma_valu<DTILES * 2, 6>();
+        pv(vl, 1, P1, L1);
     };
 
     // Two register stages: the loads of tile t+2 are in flight while tile t is
@@ -348,8 +430,8 @@ __global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         float l = lrun[nt];
-        l += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(l), 0x401F));
-        l += bperm_xor(l, 32);
+        l = sum_xor16(l);
+        l = sum_xor32(l);
         const uint32_t qr = q0 + 16 * nt + li;
         if (qr >= T) continue;
         const float inv = 1.0f / l;
@@ -386,9 +468,12 @@ hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint3
     a.out_dtype = out_dtype;
     a.scale_log2 = s.scale * kLog2e;
     a.flags = reinterpret_cast<uint32_t*>(workspace);
+    a.kv_heads = s.kv_heads;
     const bool bf = query_dtype == BF16;
     if (s.head_dim == 64 && s.group == 2) {
-        dim3 grid((tokens + 127) / 128, s.kv_heads, 1);
+        a.qblocks = (tokens + 127) / 128;
+        a.xcd_map = (8 % s.kv_heads == 0) && ((uint64_t)a.qblocks * s.kv_heads) % 8 == 0;
+        dim3 grid(a.qblocks * s.kv_heads, 1, 1);
         if (!bf) {
             hipLaunchKernelGGL((prefill_attention_kernel<64, F16, 2, 4, false>), grid, dim3(512), 0, st, a);
         } else {
@@ -396,7 +481,9 @@ hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint3
             hipLaunchKernelGGL((prefill_attention_kernel<64, BF16, 2, 4, true>), grid, dim3(512), 0, st, a);
         }
     } else if (s.head_dim == 128 && s.group == 8) {
-        dim3 grid((tokens + 31) / 32, s.kv_heads, 1);
+        a.qblocks = (tokens + 31) / 32;
+        a.xcd_map = (8 % s.kv_heads == 0) && ((uint64_t)a.qblocks * s.kv_heads) % 8 == 0;
+        dim3 grid(a.qblocks * s.kv_heads, 1, 1);
         if (!bf) {
             hipLaunchKernelGGL((prefill_attention_kernel<128, F16, 8, 1, false>), grid, dim3(512), 0, st, a);
         } else {
