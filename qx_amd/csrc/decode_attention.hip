@@ -19,6 +19,7 @@
 // bytes of `length` positions per (sequence, kv head) plus q and the output.
 #include "common.h"
 #include "internal.h"
+#include "mfma.h"
 
 namespace qxh {
 
@@ -215,62 +216,247 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
     }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA decode for 16-bit caches.  The G query heads of a group are the columns
+// of S^T = K . Q^T (v_mfma_f32_16x16x32, 16 - G padding columns), so one
+// 16-position K block costs one MFMA per 32 dims instead of G x D VALU FMAs.
+// Per wave and 32-position tile: K comes straight from memory in A-operand
+// layout (lane (g, i): position i, dims 32ks + 8g..+8), V goes through a
+// wave-private LDS tile and returns transposed (ds_read_b64_tr_b16) as the
+// V^T operand of O^T = V^T . P^T.  P.V runs in the cache dtype; bf16 splits P
+// into hi + lo parts (two MFMAs, exact to ~2^-16), which costs nothing in a
+// bandwidth-bound kernel.  Lane (g, i) keeps the softmax state of head i, so
+// rescaling the O^T accumulators is lane-local.
+// ---------------------------------------------------------------------------
+template <int D, int G, int KDT, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
+    using M = MfmaT<KDT>;
+    using vec = typename M::vec;
+    constexpr int KSTEPS = D / 32;
+    constexpr int DTILES = D / 16;
+    constexpr int VROWB = D * 2 + 32;            // padded V row for conflict-light transposed reads
+    constexpr int VCH = 32 * D * 2 / 16 / 64;    // 16-byte V chunks per lane per tile
+    static_assert(G <= 16, "query heads of a group must fit the 16 MFMA columns");
+
+    __shared__ __attribute__((aligned(16))) char vtile[WAVES][32 * VROWB];
+    __shared__ float sm_m[WAVES][G];
+    __shared__ float sm_l[WAVES][G];
+    __shared__ float sm_acc[WAVES][G][D];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int lg = lane >> 4, li = lane & 15;
+    const uint32_t split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    const uint32_t hkv = gridDim.y;
+    const uint32_t r0 = split * a.chunk;
+    const uint32_t r1 = min(a.length, r0 + a.chunk);
+    const uint32_t span = r1 > r0 ? r1 - r0 : 0u;
+    const uint32_t wspan = ((span + WAVES - 1) / WAVES + 31) / 32 * 32;
+    const uint32_t w0 = r0 + wave * wspan;
+    const uint32_t w1 = min(r1, w0 + wspan);
+    const float c = a.qscale;  // softmax scale * log2(e), applied to q.k in fp32
+
+    const size_t head_off = (size_t)seq * a.seq_stride + (size_t)kvh * a.head_stride;
+    const char* kb = reinterpret_cast<const char*>(a.keys) + head_off * 2;
+    const char* vb = reinterpret_cast<const char*>(a.values) + head_off * 2;
+    char* vl = vtile[wave];
+
+    // Q^T operand: lane (g, i) supplies head i (zero for i >= G), dims 32ks + 8g..
+    vec qop[KSTEPS];
+    {
+        const size_t qrow = ((size_t)seq * hkv * G + kvh * G + (li < G ? li : 0)) * D;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            if (a.query_dtype == KDT) {
+                const u32x4 raw = *reinterpret_cast<const u32x4*>(
+                    reinterpret_cast<const char*>(a.query) + (qrow + 32 * ks + 8 * lg) * 2);
+                qop[ks] = li < G ? __builtin_bit_cast(vec, raw) : __builtin_bit_cast(vec, u32x4{0u, 0u, 0u, 0u});
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    qop[ks][j] = M::cvt(li < G ? load_any(a.query, qrow + 32 * ks + 8 * lg + j, a.query_dtype) : 0.0f);
+            }
+        }
+    }
+
+    f32x4 oacc[DTILES];
+#pragma unroll
+    for (int dt = 0; dt < DTILES; ++dt) oacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float mrun = kNegBig, lrun = 0.f;
+
+    for (uint32_t base = w0; base < w1; base += 32) {
+        // K in A-operand layout, V row-major chunks (rows past the range are clamped; masked below)
+        u32x4 kr[2][KSTEPS], vr[VCH];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const uint32_t row = min(base + 16 * mt + li, w1 - 1);
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks)
+                kr[mt][ks] = load16<true>(kb + ((size_t)row * D + 32 * ks + 8 * lg) * 2);
+        }
+#pragma unroll
+        for (int cc = 0; cc < VCH; ++cc) {
+            const int chunk = lane + 64 * cc;
+            const int row = chunk / (D / 8), col = chunk % (D / 8);
+            const uint32_t pos = min(base + row, w1 - 1);
+            vr[cc] = load16<true>(vb + ((size_t)pos * D + col * 8) * 2);
+        }
+        // S^T = K . Q^T
+        f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks)
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) sacc[mt] = M::mma(__builtin_bit_cast(vec, kr[mt][ks]), qop[ks], sacc[mt]);
+        // V tile into this wave's LDS slot
+#pragma unroll
+        for (int cc = 0; cc < VCH; ++cc) {
+            const int chunk = lane + 64 * cc;
+            const int row = chunk / (D / 8), col = chunk % (D / 8);
+            *reinterpret_cast<u32x4*>(vl + row * VROWB + col * 16) = vr[cc];
+        }
+        // online softmax of head `li` over this tile's 32 positions
+        float sv[8];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t pos = base + 16 * mt + 4 * lg + j;
+                const float v = pos < w1 ? sacc[mt][j] * c : -INFINITY;
+                sv[mt * 4 + j] = v;
+                tmax = fmaxf(tmax, v);
+            }
+        tmax = max_xor32(max_xor16(tmax));
+        const float mnew = fmaxf(mrun, tmax);
+        const float alpha = fast_exp2(mrun - mnew);
+        mrun = mnew;
+        vec phi, plo;
+        float psum = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float p = fast_exp2(sv[k] - mnew);
+            psum += p;
+            const auto h = M::cvt(p);
+            phi[k] = h;
+            if constexpr (KDT == BF16) plo[k] = M::cvt(p - (float)h);
+        }
+        lrun = __builtin_fmaf(lrun, alpha, psum);
+#pragma unroll
+        for (int dt = 0; dt < DTILES; ++dt) oacc[dt] *= alpha;
+        // O^T += V^T . P^T
+#pragma unroll
+        for (int dt = 0; dt < DTILES; ++dt) {
+            const vec vop = __builtin_bit_cast(vec, vt_operand_rows32<VROWB>(vl, 0, 16 * dt, lg, li));
+            oacc[dt] = M::mma(vop, phi, oacc[dt]);
+            if constexpr (KDT == BF16) oacc[dt] = M::mma(vop, plo, oacc[dt]);
+        }
+    }
+
+    // the four 16-lane groups hold disjoint positions of head li: total l
+    lrun = sum_xor32(sum_xor16(lrun));
+    if (li < G) {
+#pragma unroll
+        for (int dt = 0; dt < DTILES; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sm_acc[wave][li][16 * dt + 4 * lg + j] = oacc[dt][j];
+        if (lg == 0) {
+            sm_m[wave][li] = mrun;
+            sm_l[wave][li] = lrun;
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * D; i += 64 * WAVES) {
+        const int g = i / D, d = i % D;
+        float Mx = kNegBig;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) Mx = fmaxf(Mx, sm_m[w][g]);
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float f = fast_exp2(sm_m[w][g] - Mx);
+            L = __builtin_fmaf(sm_l[w][g], f, L);
+            A = __builtin_fmaf(sm_acc[w][g][d], f, A);
+        }
+        if (a.splits == 1) {
+            store_any(a.out, ((size_t)seq * hkv * G + kvh * G + g) * D + d, A / L, a.out_dtype);
+        } else {
+            const size_t pidx = (((size_t)seq * hkv + kvh) * a.splits + split) * G + g;
+            a.ws_acc[pidx * D + d] = A;
+            if (d == 0) {
+                a.ws_ml[2 * pidx] = Mx;
+                a.ws_ml[2 * pidx + 1] = L;
+            }
+        }
+    }
+}
+
 // Reduce the per-split partials: out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
-// grid (q_heads, sequences), block D.  The split weights are formed once per
-// block in LDS (parallel over splits), then every thread streams its column
-// of acc with independent loads.
+// grid (q_heads, sequences), block 1024.  The reduction is latency-bound (a
+// few hundred KB per launch), so it is organised as two rounds of independent
+// loads: every thread loads at most one (m, l) pair to form M, L and the split
+// weights in LDS, then thread (subset, d4) accumulates float4 columns of acc
+// for splits subset, subset + NSUB, ... (all loads issued together), and the
+// NSUB partial sums are added through LDS.
 constexpr int kMaxSplits = 1024;
+constexpr int kCombineThreads = 1024;
 
 template <int D, int G>
-__global__ __launch_bounds__(D) void decode_combine_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeArgs a) {
+    constexpr int D4 = D / 4;
+    constexpr int NSUB = kCombineThreads / D4;
     __shared__ float sm_f[kMaxSplits];
-    __shared__ float sm_red[D];
+    __shared__ float sm_red[kCombineThreads / 64];
+    __shared__ f32x4 sm_acc[NSUB][D4];
     const uint32_t hq = blockIdx.x, seq = blockIdx.y;
     const uint32_t hkv = gridDim.x / G;
     const uint32_t kvh = hq / G, g = hq % G;
-    const int t = threadIdx.x;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t S = a.splits;
     const size_t p0 = ((size_t)seq * hkv + kvh) * S * G + g;
 
-    float mloc = kNegBig;
-    for (uint32_t s = t; s < S; s += D) {
-        const float m = a.ws_ml[2 * (p0 + (size_t)s * G)];
-        sm_f[s] = m;
-        mloc = fmaxf(mloc, m);
+    // round 1: M = max m_s, L = sum l_s 2^(m_s - M), f_s = 2^(m_s - M)
+    float m = kNegBig, l = 0.0f;
+    if ((uint32_t)t < S) {
+        m = a.ws_ml[2 * (p0 + (size_t)t * G)];
+        l = a.ws_ml[2 * (p0 + (size_t)t * G) + 1];
     }
-    sm_red[t] = mloc;
+    float wm = m;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) wm = fmaxf(wm, __shfl_xor(wm, o));
+    if (lane == 0) sm_red[wave] = wm;
     __syncthreads();
-    for (int w = D / 2; w > 0; w >>= 1) {
-        if (t < w) sm_red[t] = fmaxf(sm_red[t], sm_red[t + w]);
-        __syncthreads();
-    }
-    const float M = sm_red[0];
+    float M = kNegBig;
+#pragma unroll
+    for (int w = 0; w < kCombineThreads / 64; ++w) M = fmaxf(M, sm_red[w]);
+    const float f = fast_exp2(m - M);
+    if ((uint32_t)t < S) sm_f[t] = f;
+    float wl = (uint32_t)t < S ? l * f : 0.0f;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) wl += __shfl_xor(wl, o);
     __syncthreads();
-    float lloc = 0.0f;
-    for (uint32_t s = t; s < S; s += D) {
-        const float f = fast_exp2(sm_f[s] - M);
-        sm_f[s] = f;
-        lloc = __builtin_fmaf(a.ws_ml[2 * (p0 + (size_t)s * G) + 1], f, lloc);
-    }
-    sm_red[t] = lloc;
+    if (lane == 0) sm_red[wave] = wl;
     __syncthreads();
-    for (int w = D / 2; w > 0; w >>= 1) {
-        if (t < w) sm_red[t] += sm_red[t + w];
-        __syncthreads();
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kCombineThreads / 64; ++w) L += sm_red[w];
+
+    // round 2: column sums
+    const int d4 = t % D4, sub = t / D4;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t sp = sub; sp < S; sp += NSUB) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(a.ws_acc + (p0 + (size_t)sp * G) * D + 4 * d4);
+        acc += v * sm_f[sp];
     }
-    const float L = sm_red[0];
-    float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f, A3 = 0.0f;
-    const float* acc = a.ws_acc + p0 * D + t;
-    const size_t stride = (size_t)G * D;
-    uint32_t s = 0;
-    for (; s + 4 <= S; s += 4) {
-        A0 = __builtin_fmaf(acc[(size_t)s * stride], sm_f[s], A0);
-        A1 = __builtin_fmaf(acc[(size_t)(s + 1) * stride], sm_f[s + 1], A1);
-        A2 = __builtin_fmaf(acc[(size_t)(s + 2) * stride], sm_f[s + 2], A2);
-        A3 = __builtin_fmaf(acc[(size_t)(s + 3) * stride], sm_f[s + 3], A3);
+    sm_acc[sub][d4] = acc;
+    __syncthreads();
+    if (t < D4) {
+        f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+        for (int k = 0; k < NSUB; ++k) tot += sm_acc[k][t];
+        const float inv = 1.0f / L;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            store_any(a.out, ((size_t)seq * gridDim.x + hq) * D + 4 * t + j, tot[j] * inv, a.out_dtype);
     }
-    for (; s < S; ++s) A0 = __builtin_fmaf(acc[(size_t)s * stride], sm_f[s], A0);
-    store_any(a.out, ((size_t)seq * gridDim.x + hq) * D + t, ((A0 + A1) + (A2 + A3)) / L, a.out_dtype);
 }
 
 // ---------------------------------------------------------------------------
@@ -293,13 +479,15 @@ DecodePlan plan_decode(const ShapeDims& s, int key_dtype, uint32_t sequences, ui
     const uint32_t units = sequences * (uint32_t)s.kv_heads;
     const uint32_t target_wgs = 2048;
     // keep the (m, l, acc) partial small next to the KV bytes it summarises
-    uint32_t min_chunk = kWaves * step;
+    // VALU kernel (fp32): keep the (m, l, acc) partial small next to the KV
+    // bytes it summarises; MFMA kernel (16-bit): one 32-position tile per wave
+    uint32_t min_chunk = key_dtype == F32 ? kWaves * step : kWaves * 32;
     if (s.group >= 8 && min_chunk < 256) min_chunk = 256;
     uint32_t want = (target_wgs + units - 1) / units;
     uint32_t cap = (length + min_chunk - 1) / min_chunk;
     uint32_t splits = want < cap ? want : cap;
     if (splits < 1) splits = 1;
-    const uint32_t gran = kWaves * rpw;
+    const uint32_t gran = key_dtype == F32 ? kWaves * rpw : kWaves * 32;
     uint32_t chunk = (length + splits - 1) / splits;
     chunk = (chunk + gran - 1) / gran * gran;
     splits = (length + chunk - 1) / chunk;
@@ -344,18 +532,19 @@ hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const 
     }
     dim3 grid(p.splits, s.kv_heads, sequences);
     const int kd = kv.key_dtype;
+    const dim3 block(64 * kWaves);
     if (s.head_dim == 64 && s.group == 2) {
         if (kd == F32) launch_typed<64, 2, F32>(a, grid, st);
-        else if (kd == F16) launch_typed<64, 2, F16>(a, grid, st);
-        else launch_typed<64, 2, BF16>(a, grid, st);
+        else if (kd == F16) hipLaunchKernelGGL((decode_mfma_kernel<64, 2, F16, kWaves>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((decode_mfma_kernel<64, 2, BF16, kWaves>), grid, block, 0, st, a);
         if (p.splits > 1)
-            hipLaunchKernelGGL((decode_combine_kernel<64, 2>), dim3(s.q_heads, sequences), dim3(64), 0, st, a);
+            hipLaunchKernelGGL((decode_combine_kernel<64, 2>), dim3(s.q_heads, sequences), dim3(kCombineThreads), 0, st, a);
     } else if (s.head_dim == 128 && s.group == 8) {
         if (kd == F32) launch_typed<128, 8, F32>(a, grid, st);
-        else if (kd == F16) launch_typed<128, 8, F16>(a, grid, st);
-        else launch_typed<128, 8, BF16>(a, grid, st);
+        else if (kd == F16) hipLaunchKernelGGL((decode_mfma_kernel<128, 8, F16, kWaves>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((decode_mfma_kernel<128, 8, BF16, kWaves>), grid, block, 0, st, a);
         if (p.splits > 1)
-            hipLaunchKernelGGL((decode_combine_kernel<128, 8>), dim3(s.q_heads, sequences), dim3(128), 0, st, a);
+            hipLaunchKernelGGL((decode_combine_kernel<128, 8>), dim3(s.q_heads, sequences), dim3(kCombineThreads), 0, st, a);
     } else {
         return hipErrorInvalidValue;
     }

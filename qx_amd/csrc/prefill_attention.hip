@@ -33,13 +33,9 @@
 
 #include "common.h"
 #include "internal.h"
+#include "mfma.h"
 
 namespace qxh {
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 struct PrefillArgs {
     const void* query;   // [T][Hq][D]
@@ -58,45 +54,6 @@ struct PrefillArgs {
     uint32_t kv_heads;
     uint32_t xcd_map;      // 1: XCD-aware block -> (head, query block) mapping
 };
-
-template <int DT> struct MfmaT;
-template <> struct MfmaT<F16> {
-    typedef f16x8 vec;
-    __device__ __forceinline__ static f32x4 mma(const vec& a, const vec& b, const f32x4& c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-    }
-    __device__ __forceinline__ static _Float16 cvt(float x) { return (_Float16)x; }
-};
-template <> struct MfmaT<BF16> {
-    typedef bf16x8 vec;
-    __device__ __forceinline__ static f32x4 mma(const vec& a, const vec& b, const f32x4& c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-    }
-    __device__ __forceinline__ static __bf16 cvt(float x) { return (__bf16)x; }
-};
-
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-
-// Reductions across the four 16-lane groups (which hold the same query column
-// at different positions).  v_permlane{16,32}_swap exchange lane halves on
-// the VALU; with both operands equal, op(result[0], result[1]) is
-// op(v, v from lane ^ 16) (resp. ^ 32) on every lane.
-__device__ __forceinline__ float max_xor16(float v) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float max_xor32(float v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float sum_xor16(float v) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float sum_xor32(float v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
 
 // Scheduling hint: interleave one MFMA with `valu` VALU instructions, n times.
 template <int N, int VALU>
@@ -140,7 +97,6 @@ __global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a
     constexpr int KSTEPS = D / 32;      // 32-dim k-steps of Q.K
     constexpr int DTILES = D / 16;      // 16-dim output tiles
     constexpr int BN = 64;              // positions per tile
-    constexpr int MT = BN / 16;         // 16-position blocks per tile
     constexpr int KROWB = D * 2 + 16;   // padded K row: 16 lanes reading 16 rows hit distinct banks
     constexpr int VROWB = D * 2 + 32;   // padded V row: the 4 rows of a transposed read hit distinct banks
     constexpr int KTILEB = BN * KROWB;
