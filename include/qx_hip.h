@@ -211,7 +211,10 @@ QXH_API int32_t qxh_encode_rope_kv_batch(qxh_graph* graph, qxh_kv_cache* cache, 
                                  void* query_output, int32_t output_dtype);
 
 /* encode_rope_kv_for_layer (crates/qx-metal/src/lib.rs:7959-7983), same
- * arguments: fp32 q/k/v of one Granite token, sequence 0. */
+ * arguments: fp32 q/k/v of one Granite token, sequence 0.  query_output may
+ * equal query (in-place rotation, as crates/qx-runtime-v2/src/lib.rs:6942-6952
+ * calls it); in qxh_encode_rope_kv_batch the same holds when input_dtype ==
+ * output_dtype. */
 QXH_API int32_t qxh_encode_rope_kv_for_layer(qxh_graph* graph, qxh_kv_cache* cache, const float* query,
                                      const float* key, const float* value, float* query_output,
                                      uint32_t layer, uint32_t position);

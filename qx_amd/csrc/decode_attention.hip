@@ -284,14 +284,17 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
     float mrun = kNegBig, lrun = 0.f;
 
     for (uint32_t base = w0; base < w1; base += 32) {
-        // K in A-operand layout, V row-major chunks (rows past the range are clamped; masked below)
+        // K in A-operand layout, V row-major chunks (rows past the range are clamped; masked below).
+        // One K load covers 64 of each row's 2D bytes, so the rest of the line is read by the next
+        // instruction: K uses ordinary (temporal) loads so the line survives in L2 until then
+        // (nontemporal K loads measured 8% extra HBM fetch); V loads read whole rows.
         u32x4 kr[2][KSTEPS], vr[VCH];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
             const uint32_t row = min(base + 16 * mt + li, w1 - 1);
 #pragma unroll
             for (int ks = 0; ks < KSTEPS; ++ks)
-                kr[mt][ks] = load16<true>(kb + ((size_t)row * D + 32 * ks + 8 * lg) * 2);
+                kr[mt][ks] = load16<false>(kb + ((size_t)row * D + 32 * ks + 8 * lg) * 2);
         }
 #pragma unroll
         for (int cc = 0; cc < VCH; ++cc) {
@@ -478,7 +481,6 @@ DecodePlan plan_decode(const ShapeDims& s, int key_dtype, uint32_t sequences, ui
     const uint32_t step = rpw * kUnroll;
     const uint32_t units = sequences * (uint32_t)s.kv_heads;
     const uint32_t target_wgs = 2048;
-    // keep the (m, l, acc) partial small next to the KV bytes it summarises
     // VALU kernel (fp32): keep the (m, l, acc) partial small next to the KV
     // bytes it summarises; MFMA kernel (16-bit): one 32-position tile per wave
     uint32_t min_chunk = key_dtype == F32 ? kWaves * step : kWaves * 32;

@@ -84,6 +84,33 @@ def test_granite_rope_append_matches_oracle_bits(ctx, kdt):
     assert np.array_equal(vv.float().cpu().numpy(), ref.values())
 
 
+def test_rope_kv_for_layer_in_place_like_the_reference_call_site(ctx):
+    """GpuRuntimeBuffers::encode_attention_layer_with_plan passes `query` as
+    both input and query_output (crates/qx-runtime-v2/src/lib.rs:6942-6952);
+    the single-token C entry point must rotate in place and append layer 2."""
+    log("rope_kv_for_layer in place")
+    rng = np.random.default_rng(9)
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 3, 1, 32, abi.F32)
+    ref = O.KvCache(32)
+    for p in range(6):
+        q = rng.standard_normal(1024).astype(np.float32)
+        k = rng.standard_normal(512).astype(np.float32)
+        v = rng.standard_normal(512).astype(np.float32)
+        qd, kd, vd = dev(q), dev(k), dev(v)
+        with rt.Graph(ctx) as g:
+            abi.check(abi.lib().qxh_encode_rope_kv_for_layer(g.handle, arena.handle, qd.data_ptr(), kd.data_ptr(),
+                                                             vd.data_ptr(), qd.data_ptr(), 2, p))
+        qr, kr = O.apply_granite_rope(q, k, p)
+        ref.append(p, kr, v)
+        assert np.array_equal(qd.cpu().numpy().view(np.uint32), qr.view(np.uint32)), p
+        assert np.array_equal(kd.cpu().numpy(), k)  # the key input is left untouched
+    assert arena.len(2, 0) == 6 and arena.len(0, 0) == 0
+    with rt.Graph(ctx) as g:
+        kk, vv = arena.gather(g, 2, 0, 0, 6)
+    assert np.array_equal(kk.cpu().numpy(), ref.keys())
+    assert np.array_equal(vv.cpu().numpy(), ref.values())
+
+
 def test_batched_multi_token_append_and_cursors(ctx):
     log("batched append")
     rng = np.random.default_rng(5)
