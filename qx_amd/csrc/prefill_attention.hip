@@ -53,6 +53,10 @@ struct PrefillArgs {
     uint32_t qblocks;      // query blocks per head
     uint32_t kv_heads;
     uint32_t xcd_map;      // 1: XCD-aware block -> (head, query block) mapping
+    // exact pass after the pipelined kernel: per-(kv head, 64-position tile)
+    // flags of the V^T pre-pass replace the per-workgroup votes
+    const uint32_t* tile_flags;
+    uint32_t tile_flag_stride;  // tiles per kv head
 };
 
 // Scheduling hint: interleave one MFMA with `valu` VALU instructions, n times.
@@ -112,7 +116,7 @@ __global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a
     const uint32_t wg_id = blockIdx.x + gridDim.x * blockIdx.z;
     if constexpr (EXACT) {
         // only workgroups whose fast pass met a V value outside the f16 range
-        if (a.flags[wg_id] == 0) return;
+        if (!a.tile_flags && a.flags[wg_id] == 0) return;
     }
 
     const int tid = threadIdx.x;
@@ -151,6 +155,17 @@ __global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a
     const uint32_t wave_kv = wave_live ? a.start + min(T - 1, q0 + 31) + 1 : 0;
     const uint32_t wave_tiles = (wave_kv + BN - 1) / BN;
     const float c = a.scale_log2;
+
+    if constexpr (EXACT) {
+        if (a.tile_flags) {
+            // rows of this workgroup reach tiles [0, ntiles); the pipelined
+            // kernel left them here iff one of those tiles is flagged
+            const uint32_t* f = a.tile_flags + (size_t)kvh * a.tile_flag_stride;
+            bool bad = false;
+            for (uint32_t i = lane; i < ntiles; i += 64) bad |= f[i] != 0;
+            if (!__syncthreads_or(bad)) return;
+        }
+    }
 
     const char* kbase = reinterpret_cast<const char*>(a.keys) + (size_t)kvh * a.head_stride * 2;
     const char* vbase = reinterpret_cast<const char*>(a.values) + (size_t)kvh * a.head_stride * 2;
@@ -399,7 +414,9 @@ __global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a
     }
 }
 
-uint64_t prefill_workspace_bytes(const ShapeDims& s, int kv_dtype, uint32_t tokens) {
+uint64_t prefill_workspace_bytes(const ShapeDims& s, int kv_dtype, uint32_t capacity, uint32_t tokens) {
+    if (kv_dtype == F32) return 0;
+    if (prefill_pipe_supported(s, tokens)) return prefill_pipe_workspace_bytes(s, capacity);
     if (kv_dtype != BF16) return 0;
     const uint32_t qb = s.head_dim == 64 ? (tokens + 127) / 128 : (tokens + 31) / 32;
     return (uint64_t)qb * s.kv_heads * sizeof(uint32_t);
@@ -411,6 +428,12 @@ hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint3
     *dispatches = 0;
     if (kv.key_dtype != kv.value_dtype || kv.key_dtype != query_dtype || kv.key_dtype == F32)
         return hipErrorNotSupported;
+    const bool pp = prefill_pipe_supported(s, tokens);
+    if (pp) {
+        hipError_t e = launch_prefill_pipe(s, kv, start_position, tokens, query, query_dtype, out, out_dtype, workspace,
+                                         st, dispatches);
+        if (e != hipSuccess || query_dtype != BF16) return e;
+    }
     PrefillArgs a{};
     a.query = query;
     a.keys = kv.keys;
@@ -425,6 +448,11 @@ hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint3
     a.scale_log2 = s.scale * kLog2e;
     a.flags = reinterpret_cast<uint32_t*>(workspace);
     a.kv_heads = s.kv_heads;
+    if (pp) {
+        // exact pass only, for the rows the pipelined kernel left behind
+        a.tile_flags = reinterpret_cast<const uint32_t*>(workspace);
+        a.tile_flag_stride = prefill_pipe_vt_tiles(kv.capacity);
+    }
     const bool bf = query_dtype == BF16;
     if (s.head_dim == 64 && s.group == 2) {
         a.qblocks = (tokens + 127) / 128;
@@ -433,7 +461,7 @@ hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint3
         if (!bf) {
             hipLaunchKernelGGL((prefill_attention_kernel<64, F16, 2, 4, false>), grid, dim3(512), 0, st, a);
         } else {
-            hipLaunchKernelGGL((prefill_attention_kernel<64, BF16, 2, 4, false>), grid, dim3(512), 0, st, a);
+            if (!pp) hipLaunchKernelGGL((prefill_attention_kernel<64, BF16, 2, 4, false>), grid, dim3(512), 0, st, a);
             hipLaunchKernelGGL((prefill_attention_kernel<64, BF16, 2, 4, true>), grid, dim3(512), 0, st, a);
         }
     } else if (s.head_dim == 128 && s.group == 8) {
@@ -443,13 +471,13 @@ hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint3
         if (!bf) {
             hipLaunchKernelGGL((prefill_attention_kernel<128, F16, 8, 1, false>), grid, dim3(512), 0, st, a);
         } else {
-            hipLaunchKernelGGL((prefill_attention_kernel<128, BF16, 8, 1, false>), grid, dim3(512), 0, st, a);
+            if (!pp) hipLaunchKernelGGL((prefill_attention_kernel<128, BF16, 8, 1, false>), grid, dim3(512), 0, st, a);
             hipLaunchKernelGGL((prefill_attention_kernel<128, BF16, 8, 1, true>), grid, dim3(512), 0, st, a);
         }
     } else {
         return hipErrorNotSupported;
     }
-    *dispatches = bf ? 2 : 1;
+    *dispatches += bf ? (pp ? 1 : 2) : 1;
     return hipGetLastError();
 }
 

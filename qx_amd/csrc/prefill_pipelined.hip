@@ -1,0 +1,564 @@
+// Causal prefill attention, pipelined (gfx950 MFMA, fp32 accumulate).
+//
+// Two kernels per call:
+//
+// 1. prefill_vt_kernel: the layer's V rows [0, kv_len) of each kv head are
+//    rewritten once into an f16 V^T scratch, [kv_head][tile][d][64], so that
+//    the P.V operand of a lane (16 contiguous bytes) is one ds_read_b128
+//    instead of two transposed 8-byte reads.  Within each 32-position half of
+//    a 64-position tile the slots are permuted the way the Q.K accumulator
+//    leaves probabilities in lanes: slot 8g+j (j < 4) holds position 4g+j and
+//    slot 8g+4+j holds position 16+4g+j.  bf16 values are rounded to f16
+//    (exact inside the f16 range); a tile holding a value outside the finite
+//    f16 range gets a flag, and the query rows that reach such a tile are
+//    left to the exact bf16 kernel (prefill_attention.hip).
+//
+// 2. prefill_pipe_kernel: 8 waves share one K/V head.  K and V^T tiles are
+//    copied HBM -> LDS by buffer_load_dwordx4 ... lds (no VGPR staging),
+//    three stages deep, with XOR swizzles that keep the 16-lane operand
+//    reads free of bank conflicts.  Each round is an MFMA phase (O^T +=
+//    V^T.P^T for tile r-1, S^T = K.Q^T for tile r, operand reads software-
+//    pipelined ahead of the MFMAs) and a softmax phase, with one workgroup
+//    barrier between them.  All waves run the phases in step: on gfx950 the
+//    softmax VALU work slows the LDS operand stream it would overlap with,
+//    and a measured ping-pong arrangement (the two waves of a SIMD half a
+//    round apart) was 5% slower than this.
+//
+// Stage r (K tile r, V^T tile r-1) is read only in the MFMA phase of round
+// r; its loads are issued at the start of round r-2 into the slot that
+// round r-3 used, and each wave waits for its own loads of stage r+1 before
+// the barrier of round r.
+#include <type_traits>
+
+#include "common.h"
+#include "internal.h"
+#include "mfma.h"
+
+namespace qxh {
+
+namespace {
+
+constexpr int kTile = 64;          // positions per K/V tile
+constexpr float kLazyBits = 8.0f;  // rescale when a max grows by more than 2^8
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 16-byte-per-lane copy HBM -> LDS (buffer_load_dwordx4 ... lds): lane l of
+// the wave lands at lds_dst + 16*l.  The MUBUF form is used rather than
+// global_load_lds: the compiler then counts these loads in vmcnt only and
+// keeps exact lgkmcnt waits for the operand reads of the MFMA phase.
+// Buffer resource: raw, no stride, num_records bounds every access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t offset, char* lds_dst) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds_dst, 16, (int)offset, 0, 0, 0);
+}
+
+// Workgroup barrier without the memory fence of __syncthreads(): that fence
+// would drain the direct-to-LDS loads of later stages.  The asm memory
+// clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void phase_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// pre-pass: V -> f16 V^T tiles
+// ---------------------------------------------------------------------------
+struct VtArgs {
+    const void* values;    // [Hkv][cap][D] (cache dtype)
+    uint16_t* vt;          // [Hkv][vt_tiles][D][64] f16
+    uint32_t* flags;       // [Hkv][vt_tiles]
+    uint64_t head_stride;  // V elements between kv heads
+    uint32_t vt_tiles;
+    uint32_t kv_len;
+};
+
+template <int D, int DT>
+__global__ __launch_bounds__(256) void prefill_vt_kernel(VtArgs a) {
+    constexpr int RB = D * 2 + 16;  // padded LDS row (bytes)
+    __shared__ __attribute__((aligned(16))) char tile[kTile * RB];
+    const uint32_t t = blockIdx.x, h = blockIdx.y;
+    const char* vbase = reinterpret_cast<const char*>(a.values) + (size_t)h * a.head_stride * 2;
+    bool ovf = false;
+    constexpr int CH = kTile * D / 8;
+#pragma unroll
+    for (int c = threadIdx.x; c < CH; c += 256) {
+        const int row = c / (D / 8), col = c % (D / 8);
+        const uint32_t pos = t * kTile + row;
+        const uint32_t src = min(pos, a.kv_len - 1);
+        u32x4 v = *reinterpret_cast<const u32x4*>(vbase + ((size_t)src * D + col * 8) * 2);
+        if constexpr (DT == BF16) {
+            // bf16 -> f32 is exact; |x| >= 65520 (or inf / nan) has no finite f16
+            u32x4 hv;
+            uint32_t big = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float lo = __uint_as_float(v[i] << 16);
+                const float hi = __uint_as_float(v[i] & 0xffff0000u);
+                big |= (uint32_t)!(__builtin_fabsf(lo) < 65520.0f) | (uint32_t)!(__builtin_fabsf(hi) < 65520.0f);
+                const _Float16 l16 = (_Float16)lo, h16 = (_Float16)hi;
+                hv[i] = (uint32_t)__builtin_bit_cast(uint16_t, l16) | ((uint32_t)__builtin_bit_cast(uint16_t, h16) << 16);
+            }
+            ovf |= (big != 0) && pos < a.kv_len;
+            v = hv;
+        }
+        *reinterpret_cast<u32x4*>(&tile[row * RB + col * 16]) = v;
+    }
+    ovf = __syncthreads_or(ovf);
+    if (threadIdx.x == 0) a.flags[(size_t)h * a.vt_tiles + t] = ovf ? 1u : 0u;
+    uint16_t* dst = a.vt + ((size_t)h * a.vt_tiles + t) * D * kTile;
+#pragma unroll
+    for (int c = threadIdx.x; c < D * 8; c += 256) {
+        const int d = c >> 3, ch = c & 7;
+        const int sub = ch >> 2, g = ch & 3;
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; j += 2) {
+            const int r0 = 32 * sub + 4 * g + j;
+            const uint16_t e0 = *reinterpret_cast<const uint16_t*>(&tile[r0 * RB + d * 2]);
+            const uint16_t e1 = *reinterpret_cast<const uint16_t*>(&tile[(r0 + 1) * RB + d * 2]);
+            const uint16_t f0 = *reinterpret_cast<const uint16_t*>(&tile[(r0 + 16) * RB + d * 2]);
+            const uint16_t f1 = *reinterpret_cast<const uint16_t*>(&tile[(r0 + 17) * RB + d * 2]);
+            w[j / 2] = (uint32_t)e0 | ((uint32_t)e1 << 16);
+            w[2 + j / 2] = (uint32_t)f0 | ((uint32_t)f1 << 16);
+        }
+        *reinterpret_cast<u32x4*>(dst + (size_t)d * kTile + ch * 8) = u32x4{w[0], w[1], w[2], w[3]};
+    }
+}
+
+// ---------------------------------------------------------------------------
+// pipelined prefill
+// ---------------------------------------------------------------------------
+struct PrefillPipeArgs {
+    const void* query;       // [T][Hq][D]
+    const void* keys;        // [Hkv][cap][D] of this layer and sequence
+    const uint16_t* vt;      // [Hkv][vt_tiles][D][64] f16
+    const uint32_t* flags;   // [Hkv][vt_tiles] or null (f16 caches)
+    void* out;               // [T][Hq][D]
+    uint64_t head_stride;    // K elements between kv heads
+    uint32_t vt_tiles;
+    uint32_t start;
+    uint32_t tokens;
+    int q_heads;
+    int group;
+    int out_dtype;
+    float scale_log2;
+    uint32_t qblocks;
+    uint32_t kv_heads;
+    uint32_t xcd_map;
+};
+
+// Column layout: every wave owns 32 query columns, two 16-column MFMA blocks
+// (nt = 0, 1).  HEADS_PER_WAVE = 1 (Qwen, group 8): wave w is head w of the
+// group, nt selects tokens 16*nt .. of the workgroup's 32 tokens.
+// HEADS_PER_WAVE = 2 (Granite, group 2): nt selects the head, wave w covers
+// 16 tokens of the workgroup's 128 (waves w and w+4 take adjacent blocks).
+template <int D, int DT, int HEADS_PER_WAVE>
+__global__ __launch_bounds__(512, 1) void prefill_pipe_kernel(PrefillPipeArgs a) {
+    using M = MfmaT<DT>;
+    using MH = MfmaT<F16>;
+    using vec = typename M::vec;
+    using hvec = typename MH::vec;
+    constexpr int KSTEPS = D / 32;
+    constexpr int DTILES = D / 16;
+    constexpr int KROWB = D * 2;                 // K tile row bytes (swizzled, unpadded)
+    constexpr int KTILEB = kTile * KROWB;
+    constexpr int VTILEB = D * kTile * 2;         // V^T tile: D rows of 128 bytes
+    constexpr int STAGEB = KTILEB + VTILEB;
+    constexpr int KI = KTILEB / 1024;             // 1 KB direct loads per K tile
+    constexpr int VI = VTILEB / 1024;
+    constexpr int LPW = (KI + VI) / 8;            // loads per wave per stage
+    constexpr int KCH = D / 8;                    // 16-byte chunks per K row
+    constexpr int TOKW = HEADS_PER_WAVE == 1 ? 32 : 16;   // tokens per wave
+    constexpr int WGT = HEADS_PER_WAVE == 1 ? 32 : 128;   // tokens per workgroup
+    static_assert(LPW * 8 == KI + VI, "stage loads must split evenly over 8 waves");
+
+    __shared__ __attribute__((aligned(1024))) char lds[3 * STAGEB];
+
+    const int tid = threadIdx.x;
+    // readfirstlane: the compiler then knows the wave index (and every branch
+    // on it) is uniform, so those branches stay scalar
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int lg = lane >> 4, li = lane & 15;
+
+    // block -> (kv head, query block); each XCD serves one kv head (or a
+    // fixed share of heads) so the head's K/V stays in that XCD's L2
+    const uint32_t nqb = a.qblocks;
+    uint32_t kvh, qidx;
+    if (a.xcd_map) {
+        const uint32_t lin = blockIdx.x, xcd = lin & 7, slot = lin >> 3;
+        const uint32_t per = 8 / a.kv_heads;
+        kvh = xcd / per;
+        qidx = slot * per + (xcd % per);
+    } else {
+        kvh = blockIdx.x / nqb;
+        qidx = blockIdx.x % nqb;
+    }
+    const uint32_t qblock = nqb - 1 - qidx;  // longest rows first
+    const uint32_t T = a.tokens;
+    const uint32_t wg_t0 = qblock * WGT;
+    const uint32_t kv_len = a.start + min(T, wg_t0 + WGT);
+    const uint32_t n = (kv_len + kTile - 1) / kTile;
+
+    // this wave's columns
+    const int wslot = HEADS_PER_WAVE == 1 ? 0 : 2 * (wave & 3) + (wave >> 2);
+    const uint32_t w_t0 = wg_t0 + wslot * TOKW;  // first token of the wave
+    int col_head[2];
+    uint32_t col_tok[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        if constexpr (HEADS_PER_WAVE == 1) {
+            col_head[nt] = (int)kvh * a.group + wave;
+            col_tok[nt] = w_t0 + 16 * nt + li;
+        } else {
+            col_head[nt] = (int)kvh * a.group + nt;
+            col_tok[nt] = w_t0 + li;
+        }
+    }
+    const bool wave_live = w_t0 < T;
+    const uint32_t w_last = min(T - 1, w_t0 + TOKW - 1);
+    const uint32_t wave_n = wave_live ? (a.start + w_last) / kTile + 1 : 0;
+    const uint32_t w_qpos_min = a.start + w_t0;
+
+    // bf16 caches: rows that reach a tile with V outside the f16 range belong
+    // to the exact pass
+    if (a.flags) {
+        const uint32_t* f = a.flags + (size_t)kvh * a.vt_tiles;
+        bool bad = false;
+        for (uint32_t i = lane; i < n; i += 64) bad |= f[i] != 0;
+        if (__any(bad)) return;  // uniform over the workgroup (same tiles)
+    }
+
+    const char* kbase = reinterpret_cast<const char*>(a.keys) + (size_t)kvh * a.head_stride * 2;
+    const char* vtbase = reinterpret_cast<const char*>(a.vt) + (size_t)kvh * a.vt_tiles * VTILEB;
+
+    // Direct loads: stage load j (1 KB) is issued by wave j / LPW.  Loads
+    // j < KI copy RPI rows of the K tile, the rest copy 8 rows (d) of the V^T
+    // tile.  The per-lane part of each source address is fixed: the row in
+    // the tile and the (swizzled) 16-byte chunk.
+    constexpr int RPI = 1024 / KROWB;
+    int ld_row[LPW];       // K: row in the tile
+    uint32_t ld_off[LPW];  // K: chunk byte offset in the row; V^T: byte offset in the tile
+#pragma unroll
+    for (int k = 0; k < LPW; ++k) {
+        const int j = wave * LPW + k;
+        if (j < KI) {
+            const int row = j * RPI + lane / KCH;
+            const int swz = D == 128 ? (row & 15) : ((row >> 1) & 7);
+            ld_row[k] = row;
+            ld_off[k] = (uint32_t)(((lane % KCH) ^ swz) * 16);
+        } else {
+            const int d = (j - KI) * 8 + (lane >> 3);
+            ld_row[k] = 0;
+            ld_off[k] = (uint32_t)(d * 128 + ((lane & 7) ^ ((d >> 1) & 7)) * 16);
+        }
+    }
+    // resources over exactly the rows this workgroup may read
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, kv_len * KROWB);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vtbase, n * VTILEB);
+    auto issue_stage = [&](uint32_t r) {
+        char* sb = lds + (r % 3) * STAGEB;
+        const uint32_t kt = min(r, n - 1);
+        const uint32_t vtile = r == 0 ? 0u : min(r - 1, n - 1);
+#pragma unroll
+        for (int k = 0; k < LPW; ++k) {
+            const int j = wave * LPW + k;
+            if (j < KI) {
+                const uint32_t pos = min(kt * kTile + ld_row[k], kv_len - 1);
+                lds_dma16(krs, pos * KROWB + ld_off[k], sb + j * 1024);
+            } else {
+                lds_dma16(vrs, vtile * VTILEB + ld_off[k], sb + KTILEB + (j - KI) * 1024);
+            }
+        }
+    };
+    auto kswz = [](int row) { return D == 128 ? (row & 15) : ((row >> 1) & 7); };
+
+    // Q^T operands: lane supplies column li of block nt, dims 32*ks + 8*lg ..
+    vec qop[2][KSTEPS];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const uint32_t qr = min(col_tok[nt], T - 1);
+        const char* qp = reinterpret_cast<const char*>(a.query) + (((size_t)qr * a.q_heads + col_head[nt]) * D) * 2;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks)
+            qop[nt][ks] = __builtin_bit_cast(vec, *reinterpret_cast<const u32x4*>(qp + (32 * ks + 8 * lg) * 2));
+    }
+
+    f32x4 oacc[DTILES][2];
+#pragma unroll
+    for (int dt = 0; dt < DTILES; ++dt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const float c = a.scale_log2;
+    const float lazy_raw = kLazyBits / c;       // threshold in raw q.k units
+    float mrun[2] = {-1.0e30f, -1.0e30f};       // running max of raw q.k
+    float thr[2] = {-1.0e30f, -1.0e30f};        // rescale when a score exceeds this
+    // Row sums ride on the matrix core: lacc[nt] += ones . P^T gives every
+    // lane the full column sum (all four entries equal), so the sum sees the
+    // same f16 probabilities as P.V and needs no VALU adds or lane reduction.
+    f32x4 lacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const hvec ones = hvec{(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
+                           (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
+    f32x4 S[4][2];                               // scores of one tile: positions 16*mt + 4*lg + j
+    hvec P[2][2];                                // probabilities of one tile: [half][nt]
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) P[h][nt] = hvec{};
+
+    // MFMA phase of round r: O^T += V^T.P^T for tile r-1 (PV) and S^T = K.Q^T
+    // for tile r (QK), as one sequence of 16-byte LDS operand reads, each
+    // feeding two MFMAs (the two column blocks).  Reads run PREF operands
+    // ahead of their MFMAs; sched_group_barrier keeps that interleave (one
+    // read per two MFMAs) so the LDS latency hides behind the matrix core.
+    constexpr int NPV = 2 * DTILES;      // V^T operands of one tile
+    constexpr int NQK = 4 * KSTEPS;      // K operands of one tile
+    constexpr int PREF = 6;
+    auto mfma_phase = [&](uint32_t r, auto pv_on, auto qk_on) {
+        constexpr bool DO_PV = decltype(pv_on)::value;
+        constexpr bool DO_QK = decltype(qk_on)::value;
+        constexpr int B0 = DO_PV ? 0 : NPV;          // first operand index
+        constexpr int B1 = DO_QK ? NPV + NQK : NPV;  // one past the last
+        constexpr int N = B1 - B0;
+        const char* st = lds + (r % 3) * STAGEB;
+        // operand i: PV (i < NPV): half = i / DTILES, dt = i % DTILES;
+        //            QK: ks = (i - NPV) / 4, mt = (i - NPV) % 4
+        auto read = [&](int i) -> u32x4 {
+            if (i < NPV) {
+                const int half = i / DTILES, dt = i % DTILES;
+                const int d = 16 * dt + li;
+                const int ch = (4 * half + lg) ^ ((d >> 1) & 7);
+                return *reinterpret_cast<const u32x4*>(st + KTILEB + d * 128 + ch * 16);
+            }
+            const int ks = (i - NPV) / 4, mt = (i - NPV) % 4;
+            const int row = 16 * mt + li;
+            const int ch = (4 * ks + lg) ^ kswz(row);
+            return *reinterpret_cast<const u32x4*>(st + row * KROWB + ch * 16);
+        };
+        auto use = [&](int i, const u32x4& op) {
+            if (i < NPV) {
+                const int half = i / DTILES, dt = i % DTILES;
+                const hvec vop = __builtin_bit_cast(hvec, op);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = MH::mma(vop, P[half][nt], oacc[dt][nt]);
+                if (dt == DTILES - 1) {
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) lacc[nt] = MH::mma(ones, P[half][nt], lacc[nt]);
+                }
+            } else {
+                const int ks = (i - NPV) / 4, mt = (i - NPV) % 4;
+                const vec kop = __builtin_bit_cast(vec, op);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+                    S[mt][nt] = M::mma(kop, qop[nt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : S[mt][nt]);
+            }
+        };
+        u32x4 buf[PREF];
+#pragma unroll
+        for (int i = 0; i < PREF; ++i) buf[i] = read(B0 + i);
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const u32x4 op = buf[i % PREF];
+            if (i + PREF < N) buf[i % PREF] = read(B0 + i + PREF);
+            use(B0 + i, op);
+        }
+        // keep the order: PREF reads, then (read, MFMAs of one operand) pairs,
+        // then the tail.  Operand i feeds 2 MFMAs, or 4 for the last V^T
+        // operand of each half (the row-sum MFMAs ride along).
+        constexpr auto nmfma = [](int i) constexpr { return (i < NPV && i % DTILES == DTILES - 1) ? 4 : 2; };
+        constexpr int TAIL = [&]() constexpr {
+            int t = 0;
+            for (int i = N - PREF; i < N; ++i) t += nmfma(B0 + i);
+            return t;
+        }();
+        __builtin_amdgcn_sched_group_barrier(0x100, PREF, 0);
+#pragma unroll
+        for (int i = 0; i < N - PREF; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (nmfma(B0 + i) == 4) __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            else __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, TAIL, 0);
+    };
+    // softmax of tile t (scores in S) -> probabilities in P
+    auto softmax = [&](uint32_t t) {
+        if (t * kTile + kTile - 1 > w_qpos_min) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const uint32_t qpos = a.start + col_tok[nt];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (t * kTile + 16 * mt + 4 * lg + j > qpos) S[mt][nt][j] = -INFINITY;
+            }
+        }
+        float lm[2];
+        bool need = false;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const float a0 = max3f(S[0][nt][0], S[0][nt][1], S[0][nt][2]);
+            const float a1 = max3f(S[0][nt][3], S[1][nt][0], S[1][nt][1]);
+            const float a2 = max3f(S[1][nt][2], S[1][nt][3], S[2][nt][0]);
+            const float a3 = max3f(S[2][nt][1], S[2][nt][2], S[2][nt][3]);
+            const float a4 = max3f(S[3][nt][0], S[3][nt][1], S[3][nt][2]);
+            lm[nt] = fmaxf(max3f(a0, a1, a2), max3f(a3, a4, S[3][nt][3]));
+            need |= lm[nt] > thr[nt];
+        }
+        if (__any(need)) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const float m = max_xor32(max_xor16(lm[nt]));
+                const float mnew = fmaxf(mrun[nt], m);
+                const float alpha = fast_exp2((mrun[nt] - mnew) * c);
+                mrun[nt] = mnew;
+                thr[nt] = mnew + lazy_raw;
+                lacc[nt] *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < DTILES; ++dt) oacc[dt][nt] *= alpha;
+            }
+        }
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const float moff = -mrun[nt] * c;
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const int mt = 2 * half + (k >> 2), j = k & 3;
+                    P[half][nt][k] = (_Float16)fast_exp2(__builtin_fmaf(S[mt][nt][j], c, moff));
+                }
+            }
+        }
+    };
+
+    // prologue: stages 0 and 1 in flight, stage 0 complete
+    issue_stage(0);
+    issue_stage(1);
+    wait_vmcnt<LPW>();
+    phase_barrier();
+
+    for (uint32_t r = 0; r <= n; ++r) {
+        const bool more = r + 2 <= n;
+        if (more) issue_stage(r + 2);
+        // MFMA phase: P.V of tile r-1, then S = Q.K of tile r.  Round 0 runs
+        // P.V with P = 0, and round wave_n computes a Q.K that no softmax
+        // reads: one code path for every round the wave takes part in.  A
+        // wave that runs ahead into this phase while its SIMD partner is
+        // still in softmax takes issue priority.
+        __builtin_amdgcn_s_setprio(1);
+        if (r <= wave_n) mfma_phase(r, std::true_type{}, std::true_type{});
+        __builtin_amdgcn_s_setprio(0);
+        // stage r+1 complete; stage r+2 (issued above) may still be in flight
+        if (more) wait_vmcnt<LPW>();
+        else wait_vmcnt<0>();
+        phase_barrier();
+        // softmax phase of tile r (no LDS access: the next round's MFMA phase
+        // needs no second barrier)
+        if (r < wave_n) softmax(r);
+    }
+
+    if (!wave_live) return;
+    // lane holds dims 16*dt + 4*lg + j of column li: one 4-element vector store per dt
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const float l = lacc[nt][0];
+        const uint32_t qr = col_tok[nt];
+        if (qr >= T) continue;
+        const float inv = 1.0f / l;
+        char* orow = reinterpret_cast<char*>(a.out) + ((size_t)qr * a.q_heads + col_head[nt]) * D * (a.out_dtype == F32 ? 4 : 2);
+#pragma unroll
+        for (int dt = 0; dt < DTILES; ++dt) {
+            const f32x4 v = oacc[dt][nt] * inv;
+            const int e = 16 * dt + 4 * lg;
+            if (a.out_dtype == F32) {
+                *reinterpret_cast<f32x4*>(orow + e * 4) = v;
+            } else if (a.out_dtype == F16) {
+                typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                const h4 hv = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+                *reinterpret_cast<h4*>(orow + e * 2) = hv;
+            } else {
+                const uint32_t w0 = (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
+                const uint32_t w1 = (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
+                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                *reinterpret_cast<u32x2*>(orow + e * 2) = u32x2{w0, w1};
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+uint32_t prefill_pipe_vt_tiles(uint32_t capacity) { return (capacity + kTile - 1) / kTile; }
+
+uint64_t prefill_pipe_workspace_bytes(const ShapeDims& s, uint32_t capacity) {
+    const uint64_t tiles = prefill_pipe_vt_tiles(capacity);
+    const uint64_t flags = ((uint64_t)s.kv_heads * tiles * 4 + 255) / 256 * 256;
+    return flags + (uint64_t)s.kv_heads * tiles * s.head_dim * kTile * 2;
+}
+
+bool prefill_pipe_supported(const ShapeDims& s, uint32_t tokens) {
+    return tokens >= kTile && ((s.head_dim == 128 && s.group == 8) || (s.head_dim == 64 && s.group == 2));
+}
+
+hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t start, uint32_t tokens, const void* query,
+                             int dtype, void* out, int out_dtype, void* workspace, hipStream_t st, int* dispatches) {
+    *dispatches = 0;
+    const uint32_t vt_tiles = prefill_pipe_vt_tiles(kv.capacity);
+    const uint32_t kv_len = start + tokens;
+    const uint32_t tiles = (kv_len + kTile - 1) / kTile;
+    uint32_t* flags = reinterpret_cast<uint32_t*>(workspace);
+    const uint64_t flag_bytes = ((uint64_t)s.kv_heads * vt_tiles * 4 + 255) / 256 * 256;
+    uint16_t* vt = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(workspace) + flag_bytes);
+
+    VtArgs va{kv.values, vt, flags, kv.head_stride, vt_tiles, kv_len};
+    dim3 vgrid(tiles, s.kv_heads);
+    const bool bf = dtype == BF16;
+    if (s.head_dim == 128) {
+        if (bf) hipLaunchKernelGGL((prefill_vt_kernel<128, BF16>), vgrid, dim3(256), 0, st, va);
+        else hipLaunchKernelGGL((prefill_vt_kernel<128, F16>), vgrid, dim3(256), 0, st, va);
+    } else {
+        if (bf) hipLaunchKernelGGL((prefill_vt_kernel<64, BF16>), vgrid, dim3(256), 0, st, va);
+        else hipLaunchKernelGGL((prefill_vt_kernel<64, F16>), vgrid, dim3(256), 0, st, va);
+    }
+
+    PrefillPipeArgs a{};
+    a.query = query;
+    a.keys = kv.keys;
+    a.vt = vt;
+    a.flags = bf ? flags : nullptr;
+    a.out = out;
+    a.head_stride = kv.head_stride;
+    a.vt_tiles = vt_tiles;
+    a.start = start;
+    a.tokens = tokens;
+    a.q_heads = s.q_heads;
+    a.group = s.group;
+    a.out_dtype = out_dtype;
+    a.scale_log2 = s.scale * kLog2e;
+    a.kv_heads = s.kv_heads;
+    const uint32_t wgt = s.head_dim == 128 ? 32 : 128;
+    a.qblocks = (tokens + wgt - 1) / wgt;
+    a.xcd_map = (8 % s.kv_heads == 0) && ((uint64_t)a.qblocks * s.kv_heads) % 8 == 0;
+    dim3 grid(a.qblocks * s.kv_heads);
+    if (s.head_dim == 128) {
+        if (bf) hipLaunchKernelGGL((prefill_pipe_kernel<128, BF16, 1>), grid, dim3(512), 0, st, a);
+        else hipLaunchKernelGGL((prefill_pipe_kernel<128, F16, 1>), grid, dim3(512), 0, st, a);
+    } else {
+        if (bf) hipLaunchKernelGGL((prefill_pipe_kernel<64, BF16, 2>), grid, dim3(512), 0, st, a);
+        else hipLaunchKernelGGL((prefill_pipe_kernel<64, F16, 2>), grid, dim3(512), 0, st, a);
+    }
+    *dispatches = 2;
+    return hipGetLastError();
+}
+
+}  // namespace qxh

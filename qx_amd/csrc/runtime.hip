@@ -622,7 +622,7 @@ extern "C" int32_t qxh_encode_attention_for_layer(qxh_graph* g, qxh_kv_cache* c,
 extern "C" int32_t qxh_prefill_workspace_bytes(const qxh_kv_cache* c, uint32_t tokens, uint64_t* bytes) {
     QXH_REQUIRE(c && bytes, QXH_ERR_INVALID_ARGUMENT, "prefill_workspace_bytes: null argument");
     QXH_REQUIRE(tokens > 0, QXH_ERR_INVALID_ARGUMENT, "prefill of zero tokens");
-    *bytes = prefill_workspace_bytes(c->dims, c->desc.key_dtype, tokens);
+    *bytes = prefill_workspace_bytes(c->dims, c->desc.key_dtype, c->desc.capacity, tokens);
     return QXH_OK;
 }
 
@@ -640,7 +640,7 @@ extern "C" int32_t qxh_encode_prefill_attention(qxh_graph* g, qxh_kv_cache* c, u
     QXH_REQUIRE((uint64_t)start + tokens <= c->at(layer, seq), QXH_ERR_KV_POSITION,
                 "prefill rows end at %llu beyond committed length %u", (unsigned long long)start + tokens,
                 c->at(layer, seq));
-    const uint64_t need = prefill_workspace_bytes(c->dims, c->desc.key_dtype, tokens);
+    const uint64_t need = prefill_workspace_bytes(c->dims, c->desc.key_dtype, c->desc.capacity, tokens);
     QXH_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), QXH_ERR_INVALID_ARGUMENT,
                 "prefill workspace holds %llu bytes, needs %llu", (unsigned long long)workspace_bytes,
                 (unsigned long long)need);
