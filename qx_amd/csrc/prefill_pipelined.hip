@@ -426,18 +426,29 @@ __global__ __launch_bounds__(512, 1) void prefill_pipe_kernel(PrefillPipeArgs a)
                 for (int dt = 0; dt < DTILES; ++dt) oacc[dt][nt] *= alpha;
             }
         }
+        // Three batches (scale/shift, exp2, f16 packing), kept apart so that
+        // no exp2 waits on the fma issued right before it.
+        const float moff[2] = {-mrun[0] * c, -mrun[1] * c};
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            const float moff = -mrun[nt] * c;
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
+            for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const int mt = 2 * half + (k >> 2), j = k & 3;
-                    P[half][nt][k] = (_Float16)fast_exp2(__builtin_fmaf(S[mt][nt][j], c, moff));
-                }
-            }
-        }
+                for (int j = 0; j < 4; ++j) S[mt][nt][j] = __builtin_fmaf(S[mt][nt][j], c, moff[nt]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) S[mt][nt][j] = fast_exp2(S[mt][nt][j]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int half = 0; half < 2; ++half)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) P[half][nt][k] = (_Float16)S[2 * half + (k >> 2)][nt][k & 3];
     };
 
     // prologue: stages 0 and 1 in flight, stage 0 complete
