@@ -283,12 +283,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
     for (int dt = 0; dt < DTILES; ++dt) oacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float mrun = kNegBig, lrun = 0.f;
 
-    for (uint32_t base = w0; base < w1; base += 32) {
-        // K in A-operand layout, V row-major chunks (rows past the range are clamped; masked below).
-        // One K load covers 64 of each row's 2D bytes, so the rest of the line is read by the next
-        // instruction: K uses ordinary (temporal) loads so the line survives in L2 until then
-        // (nontemporal K loads measured 8% extra HBM fetch); V loads read whole rows.
-        u32x4 kr[2][KSTEPS], vr[VCH];
+    // K in A-operand layout, V row-major chunks (rows past the range are clamped; masked below).
+    // One K load covers 64 of each row's 2D bytes, so the rest of the line is read by the next
+    // instruction: K uses ordinary (temporal) loads so the line survives in L2 until then
+    // (nontemporal K loads measured 8% extra HBM fetch); V loads read whole rows.
+    auto load_tile = [&](uint32_t base, u32x4 (&kr)[2][KSTEPS], u32x4 (&vr)[VCH]) {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
             const uint32_t row = min(base + 16 * mt + li, w1 - 1);
@@ -303,6 +302,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
             const uint32_t pos = min(base + row, w1 - 1);
             vr[cc] = load16<true>(vb + ((size_t)pos * D + col * 8) * 2);
         }
+    };
+    for (uint32_t base = w0; base < w1; base += 32) {
+        u32x4 kr[2][KSTEPS], vr[VCH];
+        load_tile(base, kr, vr);
         // S^T = K . Q^T
         f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -393,72 +396,103 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
 }
 
 // Reduce the per-split partials: out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
-// grid (q_heads, sequences), block 1024.  The reduction is latency-bound (a
-// few hundred KB per launch), so it is organised as two rounds of independent
-// loads: every thread loads at most one (m, l) pair to form M, L and the split
-// weights in LDS, then thread (subset, d4) accumulates float4 columns of acc
-// for splits subset, subset + NSUB, ... (all loads issued together), and the
-// NSUB partial sums are added through LDS.
+// grid (q_heads x D/32, sequences), block 1024: one workgroup per 32 dims of
+// a head.  The reduction is latency-bound (a
+// few hundred KB per launch), so every partial a thread needs is requested in
+// one round: thread (sub, d4) loads (m, l) and the float4 column d4 of acc for
+// splits sub, sub + NSUB, ... (up to kBatch at a time), folds them into a
+// running (m, l, acc) of its own, and the NSUB running states of a column are
+// then merged through LDS with the same rule.
 constexpr int kMaxSplits = 1024;
 constexpr int kCombineThreads = 1024;
 
+constexpr int kCombineDims = 32;  // dims of one head per combine workgroup
+
 template <int D, int G>
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeArgs a) {
-    constexpr int D4 = D / 4;
+    constexpr int D4 = kCombineDims / 4;
     constexpr int NSUB = kCombineThreads / D4;
-    __shared__ float sm_f[kMaxSplits];
-    __shared__ float sm_red[kCombineThreads / 64];
+    constexpr int kBatch = 4;
+    constexpr int DSPLIT = D / kCombineDims;
+    __shared__ float sm_m[NSUB], sm_l[NSUB];
     __shared__ f32x4 sm_acc[NSUB][D4];
-    const uint32_t hq = blockIdx.x, seq = blockIdx.y;
-    const uint32_t hkv = gridDim.x / G;
+    const uint32_t hq = blockIdx.x / DSPLIT, dpart = blockIdx.x % DSPLIT, seq = blockIdx.y;
+    const uint32_t q_heads = gridDim.x / DSPLIT;
+    const uint32_t hkv = q_heads / G;
     const uint32_t kvh = hq / G, g = hq % G;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int t = threadIdx.x;
+    const int d4 = (int)dpart * D4 + t % D4, sub = t / D4;
     const uint32_t S = a.splits;
     const size_t p0 = ((size_t)seq * hkv + kvh) * S * G + g;
 
-    // round 1: M = max m_s, L = sum l_s 2^(m_s - M), f_s = 2^(m_s - M)
-    float m = kNegBig, l = 0.0f;
-    if ((uint32_t)t < S) {
-        m = a.ws_ml[2 * (p0 + (size_t)t * G)];
-        l = a.ws_ml[2 * (p0 + (size_t)t * G) + 1];
+    float M = kNegBig, L = 0.0f;
+    f32x4 A = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t s0 = sub; s0 < S; s0 += NSUB * kBatch) {
+        float m[kBatch], l[kBatch];
+        f32x4 v[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const uint32_t sp = s0 + (uint32_t)b * NSUB;
+            const size_t pi = p0 + (size_t)sp * G;
+            m[b] = kNegBig;
+            l[b] = 0.0f;
+            v[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (sp < S) {  // predicated: no request for splits past the end
+                m[b] = a.ws_ml[2 * pi];
+                l[b] = a.ws_ml[2 * pi + 1];
+                v[b] = *reinterpret_cast<const f32x4*>(a.ws_acc + pi * D + 4 * d4);
+            }
+        }
+        float mb = M;
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) mb = fmaxf(mb, m[b]);
+        const float r = fast_exp2(M - mb);
+        L *= r;
+        A *= r;
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const float f = fast_exp2(m[b] - mb);  // 0 for the padding entries
+            L = __builtin_fmaf(l[b], f, L);
+            A += v[b] * f;
+        }
+        M = mb;
     }
-    float wm = m;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) wm = fmaxf(wm, __shfl_xor(wm, o));
-    if (lane == 0) sm_red[wave] = wm;
+    // tree merge of the NSUB states of each column: log2(NSUB) steps
+    const int c4 = t % D4;  // column slot in LDS
+    sm_m[sub] = M;  // every column of a sub holds the same (M, L)
+    sm_l[sub] = L;
+    sm_acc[sub][c4] = A;
     __syncthreads();
-    float M = kNegBig;
 #pragma unroll
-    for (int w = 0; w < kCombineThreads / 64; ++w) M = fmaxf(M, sm_red[w]);
-    const float f = fast_exp2(m - M);
-    if ((uint32_t)t < S) sm_f[t] = f;
-    float wl = (uint32_t)t < S ? l * f : 0.0f;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) wl += __shfl_xor(wl, o);
-    __syncthreads();
-    if (lane == 0) sm_red[wave] = wl;
-    __syncthreads();
-    float L = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kCombineThreads / 64; ++w) L += sm_red[w];
-
-    // round 2: column sums
-    const int d4 = t % D4, sub = t / D4;
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t sp = sub; sp < S; sp += NSUB) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(a.ws_acc + (p0 + (size_t)sp * G) * D + 4 * d4);
-        acc += v * sm_f[sp];
+    for (int half = NSUB / 2; half >= 1; half >>= 1) {
+        float Mo = 0.f, Lo = 0.f;
+        f32x4 Ao = f32x4{0.f, 0.f, 0.f, 0.f};
+        const bool act = sub < half;
+        if (act) {
+            Mo = sm_m[sub + half];
+            Lo = sm_l[sub + half];
+            Ao = sm_acc[sub + half][c4];
+        }
+        __syncthreads();
+        if (act) {
+            const float mn = fmaxf(M, Mo);
+            const float f0 = fast_exp2(M - mn), f1 = fast_exp2(Mo - mn);
+            L = __builtin_fmaf(L, f0, Lo * f1);
+            A = A * f0 + Ao * f1;
+            M = mn;
+            sm_acc[sub][c4] = A;
+            if (c4 == 0) {
+                sm_m[sub] = M;
+                sm_l[sub] = L;
+            }
+        }
+        __syncthreads();
     }
-    sm_acc[sub][d4] = acc;
-    __syncthreads();
-    if (t < D4) {
-        f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-        for (int k = 0; k < NSUB; ++k) tot += sm_acc[k][t];
+    if (sub == 0) {
         const float inv = 1.0f / L;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            store_any(a.out, ((size_t)seq * gridDim.x + hq) * D + 4 * t + j, tot[j] * inv, a.out_dtype);
+            store_any(a.out, ((size_t)seq * q_heads + hq) * D + 4 * d4 + j, A[j] * inv, a.out_dtype);
     }
 }
 
@@ -540,13 +574,13 @@ hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const 
         else if (kd == F16) hipLaunchKernelGGL((decode_mfma_kernel<64, 2, F16, kWaves>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((decode_mfma_kernel<64, 2, BF16, kWaves>), grid, block, 0, st, a);
         if (p.splits > 1)
-            hipLaunchKernelGGL((decode_combine_kernel<64, 2>), dim3(s.q_heads, sequences), dim3(kCombineThreads), 0, st, a);
+            hipLaunchKernelGGL((decode_combine_kernel<64, 2>), dim3(s.q_heads * (64 / kCombineDims), sequences), dim3(kCombineThreads), 0, st, a);
     } else if (s.head_dim == 128 && s.group == 8) {
         if (kd == F32) launch_typed<128, 8, F32>(a, grid, st);
         else if (kd == F16) hipLaunchKernelGGL((decode_mfma_kernel<128, 8, F16, kWaves>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((decode_mfma_kernel<128, 8, BF16, kWaves>), grid, block, 0, st, a);
         if (p.splits > 1)
-            hipLaunchKernelGGL((decode_combine_kernel<128, 8>), dim3(s.q_heads, sequences), dim3(kCombineThreads), 0, st, a);
+            hipLaunchKernelGGL((decode_combine_kernel<128, 8>), dim3(s.q_heads * (128 / kCombineDims), sequences), dim3(kCombineThreads), 0, st, a);
     } else {
         return hipErrorInvalidValue;
     }
