@@ -73,7 +73,7 @@ uint64_t prefill_workspace_bytes(const ShapeDims& s, int kv_dtype, uint32_t capa
 // pipelined path (prefill_pipelined.hip): V^T pre-pass + pipelined MFMA kernel
 bool prefill_pipe_supported(const ShapeDims& s, uint32_t tokens);
 uint32_t prefill_pipe_vt_tiles(uint32_t capacity);
-uint64_t prefill_pipe_workspace_bytes(const ShapeDims& s, uint32_t capacity);
+uint64_t prefill_pipe_workspace_bytes(const ShapeDims& s, uint32_t capacity, uint32_t tokens);
 hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t start, uint32_t tokens, const void* query,
                              int dtype, void* out, int out_dtype, void* workspace, hipStream_t st, int* dispatches);
 hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint32_t start_position, uint32_t tokens,

@@ -416,7 +416,7 @@ __global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a
 
 uint64_t prefill_workspace_bytes(const ShapeDims& s, int kv_dtype, uint32_t capacity, uint32_t tokens) {
     if (kv_dtype == F32) return 0;
-    if (prefill_pipe_supported(s, tokens)) return prefill_pipe_workspace_bytes(s, capacity);
+    if (prefill_pipe_supported(s, tokens)) return prefill_pipe_workspace_bytes(s, capacity, tokens);
     if (kv_dtype != BF16) return 0;
     const uint32_t qb = s.head_dim == 64 ? (tokens + 127) / 128 : (tokens + 31) / 32;
     return (uint64_t)qb * s.kv_heads * sizeof(uint32_t);

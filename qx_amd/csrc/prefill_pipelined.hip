@@ -153,15 +153,41 @@ struct PrefillPipeArgs {
     uint32_t qblocks;
     uint32_t kv_heads;
     uint32_t xcd_map;
+    // Split KV (few workgroups): blockIdx.y = chunk of chunk_tiles tiles of the
+    // block's KV range; a block with more than one chunk writes per-column
+    // partials (m * c, l, unnormalised O) that prefill_combine_kernel merges.
+    uint32_t chunk_tiles;  // 0: one chunk per block
+    uint32_t max_chunks;   // partial slots per block
+    float* part_ml;        // [Hkv][qblocks][max_chunks][columns][2]
+    float* part_o;         // [Hkv][qblocks][max_chunks][columns][D]
 };
 
+// Column c (0 .. 32 NW - 1) of a workgroup: wave c / 32, block nt =
+// (c / 16) % 2, lane column li = c % 16, mapped to (token, head) as the
+// kernel lays them out (see prefill_pipe_kernel).
+template <int HEADS_PER_WAVE, int NW>
+__device__ __forceinline__ void pipe_column(int col, uint32_t wg_t0, uint32_t kvh, int group, uint32_t& tok,
+                                            int& head) {
+    const int wave = col >> 5, nt = (col >> 4) & 1, li = col & 15;
+    if constexpr (HEADS_PER_WAVE == 1) {
+        head = (int)kvh * group + wave;
+        tok = wg_t0 + 16 * nt + li;
+    } else {
+        const int wslot = NW == 8 ? 2 * (wave & 3) + (wave >> 2) : wave;
+        head = (int)kvh * group + nt;
+        tok = wg_t0 + wslot * 16 + li;
+    }
+}
+
 // Column layout: every wave owns 32 query columns, two 16-column MFMA blocks
-// (nt = 0, 1).  HEADS_PER_WAVE = 1 (Qwen, group 8): wave w is head w of the
-// group, nt selects tokens 16*nt .. of the workgroup's 32 tokens.
-// HEADS_PER_WAVE = 2 (Granite, group 2): nt selects the head, wave w covers
-// 16 tokens of the workgroup's 128 (waves w and w+4 take adjacent blocks).
-template <int D, int DT, int HEADS_PER_WAVE>
-__global__ __launch_bounds__(512, 1) void prefill_pipe_kernel(PrefillPipeArgs a) {
+// (nt = 0, 1).  HEADS_PER_WAVE = 1 (Qwen, group 8, NW = 8 waves): wave w is
+// head w of the group, nt selects tokens 16*nt .. of the workgroup's 32
+// tokens.  HEADS_PER_WAVE = 2 (Granite, group 2, NW = 4 waves): nt selects
+// the head, wave w covers tokens 16w .. of the workgroup's 64; three such
+// workgroups share a CU (under 168 VGPRs, 48 KB LDS) and overlap each other's
+// phases.
+template <int D, int DT, int HEADS_PER_WAVE, int NW>
+__global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 3) void prefill_pipe_kernel(PrefillPipeArgs a) {
     using M = MfmaT<DT>;
     using MH = MfmaT<F16>;
     using vec = typename M::vec;
@@ -174,11 +200,12 @@ __global__ __launch_bounds__(512, 1) void prefill_pipe_kernel(PrefillPipeArgs a)
     constexpr int STAGEB = KTILEB + VTILEB;
     constexpr int KI = KTILEB / 1024;             // 1 KB direct loads per K tile
     constexpr int VI = VTILEB / 1024;
-    constexpr int LPW = (KI + VI) / 8;            // loads per wave per stage
+    constexpr int LPW = (KI + VI) / NW;           // loads per wave per stage
     constexpr int KCH = D / 8;                    // 16-byte chunks per K row
     constexpr int TOKW = HEADS_PER_WAVE == 1 ? 32 : 16;   // tokens per wave
-    constexpr int WGT = HEADS_PER_WAVE == 1 ? 32 : 128;   // tokens per workgroup
-    static_assert(LPW * 8 == KI + VI, "stage loads must split evenly over 8 waves");
+    constexpr int WGT = HEADS_PER_WAVE == 1 ? 32 : 16 * NW;  // tokens per workgroup
+    constexpr int COLS = 32 * NW;                           // query columns per workgroup
+    static_assert(LPW * NW == KI + VI, "stage loads must split evenly over the waves");
 
     __shared__ __attribute__((aligned(1024))) char lds[3 * STAGEB];
 
@@ -207,25 +234,26 @@ __global__ __launch_bounds__(512, 1) void prefill_pipe_kernel(PrefillPipeArgs a)
     const uint32_t wg_t0 = qblock * WGT;
     const uint32_t kv_len = a.start + min(T, wg_t0 + WGT);
     const uint32_t n = (kv_len + kTile - 1) / kTile;
+    // this workgroup's tiles [t0, t1) of the block's n
+    const uint32_t ch_tiles = a.chunk_tiles ? a.chunk_tiles : n;
+    const uint32_t nchunks = (n + ch_tiles - 1) / ch_tiles;
+    const uint32_t chunk = blockIdx.y;
+    if (chunk >= nchunks) return;  // uniform, before any barrier
+    const uint32_t t0 = chunk * ch_tiles, t1 = min(n, t0 + ch_tiles);
+    const uint32_t m = t1 - t0;
 
     // this wave's columns
-    const int wslot = HEADS_PER_WAVE == 1 ? 0 : 2 * (wave & 3) + (wave >> 2);
+    const int wslot = HEADS_PER_WAVE == 1 ? 0 : (NW == 8 ? 2 * (wave & 3) + (wave >> 2) : wave);
     const uint32_t w_t0 = wg_t0 + wslot * TOKW;  // first token of the wave
     int col_head[2];
     uint32_t col_tok[2];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        if constexpr (HEADS_PER_WAVE == 1) {
-            col_head[nt] = (int)kvh * a.group + wave;
-            col_tok[nt] = w_t0 + 16 * nt + li;
-        } else {
-            col_head[nt] = (int)kvh * a.group + nt;
-            col_tok[nt] = w_t0 + li;
-        }
-    }
+    for (int nt = 0; nt < 2; ++nt) pipe_column<HEADS_PER_WAVE, NW>(wave * 32 + nt * 16 + li, wg_t0, kvh, a.group, col_tok[nt], col_head[nt]);
     const bool wave_live = w_t0 < T;
     const uint32_t w_last = min(T - 1, w_t0 + TOKW - 1);
     const uint32_t wave_n = wave_live ? (a.start + w_last) / kTile + 1 : 0;
+    // this wave's rounds in the chunk: its tiles in [t0, min(t1, wave_n))
+    const uint32_t wave_m = wave_n > t0 ? min(wave_n, t1) - t0 : 0;
     const uint32_t w_qpos_min = a.start + w_t0;
 
     // bf16 caches: rows that reach a tile with V outside the f16 range belong
@@ -266,8 +294,8 @@ __global__ __launch_bounds__(512, 1) void prefill_pipe_kernel(PrefillPipeArgs a)
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vtbase, n * VTILEB);
     auto issue_stage = [&](uint32_t r) {
         char* sb = lds + (r % 3) * STAGEB;
-        const uint32_t kt = min(r, n - 1);
-        const uint32_t vtile = r == 0 ? 0u : min(r - 1, n - 1);
+        const uint32_t kt = t0 + min(r, m - 1);
+        const uint32_t vtile = t0 + (r == 0 ? 0u : min(r - 1, m - 1));
 #pragma unroll
         for (int k = 0; k < LPW; ++k) {
             const int j = wave * LPW + k;
@@ -453,20 +481,20 @@ __global__ __launch_bounds__(512, 1) void prefill_pipe_kernel(PrefillPipeArgs a)
 
     // prologue: stages 0 and 1 in flight, stage 0 complete
     issue_stage(0);
-    issue_stage(1);
+    issue_stage(1);  // m >= 1: stage 1 exists
     wait_vmcnt<LPW>();
     phase_barrier();
 
-    for (uint32_t r = 0; r <= n; ++r) {
-        const bool more = r + 2 <= n;
+    for (uint32_t r = 0; r <= m; ++r) {
+        const bool more = r + 2 <= m;
         if (more) issue_stage(r + 2);
-        // MFMA phase: P.V of tile r-1, then S = Q.K of tile r.  Round 0 runs
-        // P.V with P = 0, and round wave_n computes a Q.K that no softmax
-        // reads: one code path for every round the wave takes part in.  A
-        // wave that runs ahead into this phase while its SIMD partner is
-        // still in softmax takes issue priority.
+        // MFMA phase: P.V of tile r-1, then S = Q.K of tile r (tiles counted
+        // from t0).  Round 0 runs P.V with P = 0, and round wave_m computes a
+        // Q.K that no softmax reads: one code path for every round the wave
+        // takes part in.  A wave that runs ahead into this phase while its
+        // SIMD partner is still in softmax takes issue priority.
         __builtin_amdgcn_s_setprio(1);
-        if (r <= wave_n) mfma_phase(r, std::true_type{}, std::true_type{});
+        if (r <= wave_m) mfma_phase(r, std::true_type{}, std::true_type{});
         __builtin_amdgcn_s_setprio(0);
         // stage r+1 complete; stage r+2 (issued above) may still be in flight
         if (more) wait_vmcnt<LPW>();
@@ -474,10 +502,26 @@ __global__ __launch_bounds__(512, 1) void prefill_pipe_kernel(PrefillPipeArgs a)
         phase_barrier();
         // softmax phase of tile r (no LDS access: the next round's MFMA phase
         // needs no second barrier)
-        if (r < wave_n) softmax(r);
+        if (r < wave_m) softmax(t0 + r);
     }
 
     if (!wave_live) return;
+    if (nchunks > 1) {
+        // partial of this chunk: (m * c, l) and unnormalised O per column
+        const size_t slot = (((size_t)kvh * nqb + qblock) * a.max_chunks + chunk) * COLS;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const size_t colx = slot + wave * 32 + nt * 16 + li;
+            if (lg == 0) {
+                a.part_ml[2 * colx] = mrun[nt] * c;
+                a.part_ml[2 * colx + 1] = lacc[nt][0];
+            }
+#pragma unroll
+            for (int dt = 0; dt < DTILES; ++dt)
+                *reinterpret_cast<f32x4*>(a.part_o + colx * D + 16 * dt + 4 * lg) = oacc[dt][nt];
+        }
+        return;
+    }
     // lane holds dims 16*dt + 4*lg + j of column li: one 4-element vector store per dt
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
@@ -507,14 +551,112 @@ __global__ __launch_bounds__(512, 1) void prefill_pipe_kernel(PrefillPipeArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// merge of split-KV partials: out = sum_c O_c 2^(m_c - M) / sum_c l_c 2^(m_c - M)
+// grid (Hkv * qblocks, 32 NW / CPB), block 256 = CPB columns x D/4 threads
+// ---------------------------------------------------------------------------
+constexpr int kMaxPipeChunks = 4;
+
+template <int D, int HEADS_PER_WAVE, int NW>
+__global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillPipeArgs a) {
+    constexpr int D4 = D / 4;
+    constexpr int CPB = 256 / D4;
+    constexpr int WGT = HEADS_PER_WAVE == 1 ? 32 : 16 * NW;
+    constexpr int COLS = 32 * NW;
+    const uint32_t nqb = a.qblocks;
+    const uint32_t kvh = blockIdx.x / nqb, qblock = blockIdx.x % nqb;
+    const uint32_t T = a.tokens;
+    const uint32_t wg_t0 = qblock * WGT;
+    const uint32_t kv_len = a.start + min(T, wg_t0 + WGT);
+    const uint32_t n = (kv_len + kTile - 1) / kTile;
+    const uint32_t nchunks = (n + a.chunk_tiles - 1) / a.chunk_tiles;
+    if (nchunks <= 1) return;  // written directly by the attention kernel
+    if (a.flags) {
+        // the attention kernel wrote no partials for a block that reaches a
+        // flagged tile: the exact pass owns its rows
+        const uint32_t* f = a.flags + (size_t)kvh * a.vt_tiles;
+        for (uint32_t i = 0; i < n; ++i)
+            if (f[i]) return;
+    }
+    const int col = blockIdx.y * CPB + threadIdx.x / D4, d4 = threadIdx.x % D4;
+    uint32_t tok;
+    int head;
+    pipe_column<HEADS_PER_WAVE, NW>(col, wg_t0, kvh, a.group, tok, head);
+    if (tok >= T) return;
+    const size_t slot = ((size_t)kvh * nqb + qblock) * a.max_chunks * COLS + col;
+    float mc[kMaxPipeChunks], lc[kMaxPipeChunks];
+    f32x4 oc[kMaxPipeChunks];
+#pragma unroll
+    for (int k = 0; k < kMaxPipeChunks; ++k) {
+        mc[k] = -1.0e30f;
+        lc[k] = 0.0f;
+        oc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if ((uint32_t)k < nchunks) {
+            const size_t cx = slot + (size_t)k * COLS;
+            mc[k] = a.part_ml[2 * cx];
+            lc[k] = a.part_ml[2 * cx + 1];
+            oc[k] = *reinterpret_cast<const f32x4*>(a.part_o + cx * D + 4 * d4);
+        }
+    }
+    float M = mc[0];
+#pragma unroll
+    for (int k = 1; k < kMaxPipeChunks; ++k) M = fmaxf(M, mc[k]);
+    float L = 0.0f;
+    f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < kMaxPipeChunks; ++k) {
+        const float f = fast_exp2(mc[k] - M);
+        L = __builtin_fmaf(lc[k], f, L);
+        O += oc[k] * f;
+    }
+    const float inv = 1.0f / L;
+    const size_t obase = ((size_t)tok * a.q_heads + head) * D + 4 * d4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store_any(a.out, obase + j, O[j] * inv, a.out_dtype);
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 uint32_t prefill_pipe_vt_tiles(uint32_t capacity) { return (capacity + kTile - 1) / kTile; }
 
-uint64_t prefill_pipe_workspace_bytes(const ShapeDims& s, uint32_t capacity) {
+// waves per workgroup, tokens per workgroup, query columns per workgroup
+static int pipe_waves(const ShapeDims& s) { return s.head_dim == 128 ? 8 : 4; }
+static uint32_t pipe_tokens_per_wg(const ShapeDims& s) { return s.head_dim == 128 ? 32 : 16 * pipe_waves(s); }
+static uint32_t pipe_columns(const ShapeDims& s) { return 32 * pipe_waves(s); }
+
+// Fewer workgroups than this split their blocks' KV ranges (at most
+// kMaxPipeChunks chunks) so that short prompts still fill the CUs.
+constexpr uint32_t kSplitBelowWgs = 512;
+
+static bool pipe_split_possible(const ShapeDims& s, uint32_t tokens) {
+    const uint32_t wgt = pipe_tokens_per_wg(s);
+    return (uint64_t)(tokens + wgt - 1) / wgt * s.kv_heads < kSplitBelowWgs;
+}
+
+// Chunk size in tiles: a quarter of the longest block's range (at least 4
+// tiles), so no block has more than kMaxPipeChunks chunks.
+static uint32_t pipe_chunk_tiles(const ShapeDims& s, uint32_t start, uint32_t tokens) {
+    if (!pipe_split_possible(s, tokens)) return 0;
+    const uint32_t n_max = (start + tokens + kTile - 1) / kTile;
+    const uint32_t q = (n_max + kMaxPipeChunks - 1) / kMaxPipeChunks;
+    return q < 4 ? 4 : q;
+}
+
+static uint64_t pipe_part_bytes(const ShapeDims& s, uint32_t tokens) {
+    if (!pipe_split_possible(s, tokens)) return 0;
+    const uint64_t slots = (uint64_t)(tokens + pipe_tokens_per_wg(s) - 1) / pipe_tokens_per_wg(s) * s.kv_heads *
+                           kMaxPipeChunks * pipe_columns(s);
+    return slots * 2 * 4 + slots * s.head_dim * 4;
+}
+
+static uint64_t pipe_flag_bytes(const ShapeDims& s, uint32_t vt_tiles) {
+    return ((uint64_t)s.kv_heads * vt_tiles * 4 + 255) / 256 * 256;
+}
+
+// workspace: [tile flags][V^T tiles][split partials: (m, l) then O]
+uint64_t prefill_pipe_workspace_bytes(const ShapeDims& s, uint32_t capacity, uint32_t tokens) {
     const uint64_t tiles = prefill_pipe_vt_tiles(capacity);
-    const uint64_t flags = ((uint64_t)s.kv_heads * tiles * 4 + 255) / 256 * 256;
-    return flags + (uint64_t)s.kv_heads * tiles * s.head_dim * kTile * 2;
+    return pipe_flag_bytes(s, tiles) + (uint64_t)s.kv_heads * tiles * s.head_dim * kTile * 2 + pipe_part_bytes(s, tokens);
 }
 
 bool prefill_pipe_supported(const ShapeDims& s, uint32_t tokens) {
@@ -527,9 +669,11 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
     const uint32_t vt_tiles = prefill_pipe_vt_tiles(kv.capacity);
     const uint32_t kv_len = start + tokens;
     const uint32_t tiles = (kv_len + kTile - 1) / kTile;
-    uint32_t* flags = reinterpret_cast<uint32_t*>(workspace);
-    const uint64_t flag_bytes = ((uint64_t)s.kv_heads * vt_tiles * 4 + 255) / 256 * 256;
-    uint16_t* vt = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(workspace) + flag_bytes);
+    char* ws = reinterpret_cast<char*>(workspace);
+    uint32_t* flags = reinterpret_cast<uint32_t*>(ws);
+    const uint64_t flag_bytes = pipe_flag_bytes(s, vt_tiles);
+    uint16_t* vt = reinterpret_cast<uint16_t*>(ws + flag_bytes);
+    char* parts = ws + flag_bytes + (uint64_t)s.kv_heads * vt_tiles * s.head_dim * kTile * 2;
 
     VtArgs va{kv.values, vt, flags, kv.head_stride, vt_tiles, kv_len};
     dim3 vgrid(tiles, s.kv_heads);
@@ -557,18 +701,32 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
     a.out_dtype = out_dtype;
     a.scale_log2 = s.scale * kLog2e;
     a.kv_heads = s.kv_heads;
-    const uint32_t wgt = s.head_dim == 128 ? 32 : 128;
+    const uint32_t wgt = pipe_tokens_per_wg(s);
     a.qblocks = (tokens + wgt - 1) / wgt;
     a.xcd_map = (8 % s.kv_heads == 0) && ((uint64_t)a.qblocks * s.kv_heads) % 8 == 0;
-    dim3 grid(a.qblocks * s.kv_heads);
+    a.chunk_tiles = pipe_chunk_tiles(s, start, tokens);
+    a.max_chunks = kMaxPipeChunks;
+    const uint64_t slots = (uint64_t)a.qblocks * s.kv_heads * kMaxPipeChunks * pipe_columns(s);
+    a.part_ml = reinterpret_cast<float*>(parts);
+    a.part_o = a.part_ml + 2 * slots;
+    // chunks of the longest block (the last one; with start it is the longest)
+    const uint32_t chunks = a.chunk_tiles ? (tiles + a.chunk_tiles - 1) / a.chunk_tiles : 1;
+    dim3 grid(a.qblocks * s.kv_heads, chunks);
     if (s.head_dim == 128) {
-        if (bf) hipLaunchKernelGGL((prefill_pipe_kernel<128, BF16, 1>), grid, dim3(512), 0, st, a);
-        else hipLaunchKernelGGL((prefill_pipe_kernel<128, F16, 1>), grid, dim3(512), 0, st, a);
+        if (bf) hipLaunchKernelGGL((prefill_pipe_kernel<128, BF16, 1, 8>), grid, dim3(512), 0, st, a);
+        else hipLaunchKernelGGL((prefill_pipe_kernel<128, F16, 1, 8>), grid, dim3(512), 0, st, a);
     } else {
-        if (bf) hipLaunchKernelGGL((prefill_pipe_kernel<64, BF16, 2>), grid, dim3(512), 0, st, a);
-        else hipLaunchKernelGGL((prefill_pipe_kernel<64, F16, 2>), grid, dim3(512), 0, st, a);
+        if (bf) hipLaunchKernelGGL((prefill_pipe_kernel<64, BF16, 2, 4>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((prefill_pipe_kernel<64, F16, 2, 4>), grid, dim3(256), 0, st, a);
     }
     *dispatches = 2;
+    if (chunks > 1) {
+        const uint32_t cpb = 256 / (s.head_dim / 4);
+        dim3 cgrid(a.qblocks * s.kv_heads, pipe_columns(s) / cpb);
+        if (s.head_dim == 128) hipLaunchKernelGGL((prefill_combine_kernel<128, 1, 8>), cgrid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((prefill_combine_kernel<64, 2, 4>), cgrid, dim3(256), 0, st, a);
+        *dispatches = 3;
+    }
     return hipGetLastError();
 }
 

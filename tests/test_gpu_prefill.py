@@ -37,7 +37,7 @@ def bits(t):
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("T,start", [(2048, 0), (100, 0), (77, 30), (1, 5), (33, 0)])
+@pytest.mark.parametrize("T,start", [(2048, 0), (100, 0), (77, 30), (1, 5), (33, 0), (200, 900)])
 def test_granite_prefill_fp16(ctx, T, start):
     log("granite prefill", T, start)
     rng = np.random.default_rng(T * 31 + start)
