@@ -175,3 +175,61 @@ def test_prefill_rejects_rows_beyond_cursor_and_fp32(ctx):
         with pytest.raises(abi.QxhError) as ei:
             rt.prefill_attention(g, a32, 0, 0, torch.zeros((10, 16, 64), device="cuda:0"))
         assert ei.value.code == abi.QXH_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("shape,dtype", [(abi.SHAPE_GRANITE, abi.F16), (abi.SHAPE_QWEN3, abi.BF16)])
+def test_k_wide_verifier_with_rollback(ctx, shape, dtype):
+    """Speculative verification: K = 4 draft tokens are RoPE'd and appended at
+    the cursor and attended causally in one call (encode_rope_kv_batch +
+    encode_attention_batch_with_plan, crates/qx-metal/src/lib.rs:8105-8267).
+    Two drafts are accepted: the cursor rolls back (rollback_kv,
+    crates/qx-runtime-v2/src/lib.rs:3271-3285) and four new drafts overwrite
+    the rejected slots.  Each verifier row must match the oracle over the cache
+    as it stands, the accepted rows must keep their bits, and the overwritten
+    slots must hold the new drafts."""
+    log("k-wide verifier", shape)
+    info = rt.shape_info(shape)
+    tdt = rt.torch_dtype(dtype)
+    L0, K, accepted = 300, 4, 2
+    arena = rt.KvArena(ctx, shape, 1, 1, L0 + 8, dtype)
+
+    def drafts(seed, start):
+        q = torch.empty((1, K, info.q_heads, info.head_dim), dtype=tdt, device="cuda:0")
+        k = torch.empty((1, K, info.kv_heads, info.head_dim), dtype=tdt, device="cuda:0")
+        v = torch.empty_like(k)
+        qo = torch.empty_like(q)
+        with rt.Graph(ctx) as g:
+            for i, t in enumerate((q, k, v)):
+                rt.fill_normal(g, t, seed=seed + i)
+            rt.rope_kv_batch(g, arena, 0, start, q, k, v, query_out=qo)
+            out = rt.prefill_attention(g, arena, 0, start, qo[0], out_dtype=torch.float32)
+            kk, vv = arena.gather(g, 0, 0, 0, start + K)
+        return qo[0], out, kk, vv
+
+    def check(qo, out, kk, vv, start):
+        rows = np.arange(K, dtype=np.uint32)
+        if shape == abi.SHAPE_QWEN3:
+            _, ref = O.qwen_prefill_rows(bits(qo), bits(kk), bits(vv), start, rows, O.BF16)
+        else:
+            c = O.KvCache(start + K)
+            c.extend(kk.float().cpu().numpy(), vv.float().cpu().numpy())
+            ref = O.granite_prefill_rows(qo.float().cpu().numpy().reshape(K, -1), c, start, rows)
+        e = rel_err(out.cpu().numpy().reshape(K, -1), ref)
+        log(f"verifier start={start}: max-abs/rms {e:.3e}")
+        assert e <= TOL_16
+
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=31, length=L0)
+    qo1, out1, kk1, vv1 = drafts(40, L0)
+    assert arena.len() == L0 + K
+    check(qo1, out1, kk1, vv1, L0)
+
+    arena.rollback(0, L0 + accepted)
+    assert arena.len() == L0 + accepted
+    qo2, out2, kk2, vv2 = drafts(50, L0 + accepted)
+    assert arena.len() == L0 + accepted + K
+    check(qo2, out2, kk2, vv2, L0 + accepted)
+    # accepted rows keep their bits; the rejected slots now hold the new drafts
+    n = L0 + accepted
+    assert np.array_equal(bits(kk2[:n]), bits(kk1[:n])) and np.array_equal(bits(vv2[:n]), bits(vv1[:n]))
+    assert not np.array_equal(bits(kk2[n:n + K - accepted]), bits(kk1[n:]))
