@@ -271,6 +271,37 @@ QXH_API int32_t qxh_encode_kv_gather_token_rows(qxh_graph* graph, const qxh_kv_c
                                         uint32_t sequence, uint32_t position_begin, uint32_t count,
                                         void* keys_out, void* values_out);
 
+/* KV commitment leaves of token rows, hashed on the GPU straight out of the
+ * head-major arena: digest i of sequence s (32 bytes, out[(s * count + i) * 32])
+ * is kv_leaf_hash_v1(layer, position_begin + i, K row, V row)
+ * (crates/qx-commit/src/state.rs:334-370), where a row is the token's raw
+ * cache bytes in the reference's position-major order [kv_head][head_dim]
+ * (crates/qx-runtime-v2/src/lib.rs:2194-2213: the bytes the reference's
+ * verification kernel hashes).  BLAKE3 throughout, 256-byte chunk trees.
+ * Rows must be [position_begin, position_begin + count) < the committed length
+ * of every sequence in [first_sequence, first_sequence + sequences); K and V
+ * must share one dtype.  out_bytes >= sequences * count * 32. */
+QXH_API int32_t qxh_encode_kv_leaf_hashes(qxh_graph* graph, const qxh_kv_cache* cache, uint32_t layer,
+                                          uint32_t first_sequence, uint32_t sequences, uint32_t position_begin,
+                                          uint32_t count, void* out, uint64_t out_bytes);
+
+/* Per-token verification digests, the counterpart of encode_verification_hashes
+ * (crates/qx-metal/src/lib.rs:9247-9345; kernel kernels/verification_hash.metal:349-522):
+ * output[p] (64 bytes) for p = 0..layers.  p = 0: state_hash_v1 of residual
+ * snapshot 0, then 32 zero bytes.  p >= 1 (layer p-1): state_hash_v1 of snapshot
+ * p when (layer + 1) % checkpoint_interval == 0 or layer + 1 == layers, else 32
+ * zero bytes; then kv_leaf_hash_v1(layer, token, K row, V row) of the row at
+ * position `token` of `sequence` in layers [0, layers).  residual_snapshots is
+ * device memory of (layers + 1) * residual_stride bytes; residual_stride and the
+ * KV row bytes must be power-of-two multiples of 256 (at most 64 and 8 chunks).
+ * The reference's key/value offset and size arrays are derived from the cache
+ * here.  Errors: layers outside 1..=cache layers, checkpoint_interval outside
+ * 1..=layers, short buffers, a token at or beyond a layer's committed length. */
+QXH_API int32_t qxh_encode_verification_hashes(qxh_graph* graph, const qxh_kv_cache* cache, uint32_t sequence,
+                                               const void* residual_snapshots, uint64_t residual_bytes,
+                                               uint32_t residual_stride, uint32_t token, uint32_t layers,
+                                               uint32_t checkpoint_interval, void* output, uint64_t output_bytes);
+
 /* ---- Granite attention block (attention half of a decoder layer) -----------
  * GpuRuntimeBuffers::encode_attention_layer_with_plan attention half
  * (crates/qx-runtime-v2/src/lib.rs:6919-6994) with fp32 dense weights, as the

@@ -325,3 +325,80 @@ def qwen_prefill_rows(query_bits, key_cache_bits, value_cache_bits, start: int, 
     _check(lib().qxo_qwen_prefill_rows(_p(q, _u16p), _p(kc, _u16p), _p(vc, _u16p), start, _p(rows, _u32p),
                                        rows.size, fmt, _p(out, _u16p), _p(of)))
     return out, of
+
+
+# ---------------------------------------------------------------------------
+# KV / state commitment hashing (oracle/qx_oracle_hash.c)
+# ---------------------------------------------------------------------------
+D_KV = b"QX:KV:V1"
+D_MERKLE = b"QX:MERKLE:V1"
+D_CHECKPOINT = b"QX:CHECKPOINT:V1"
+D_STATE, D_STATE_CHUNK = b"QX:STATE:V1", b"QX:STATE:CHUNK:V1"
+D_KV_KEY_CHUNK, D_KV_KEY_TREE = b"QX:KV:KEY:CHUNK:V1", b"QX:KV:KEY:TREE:V1"
+D_KV_VALUE_CHUNK, D_KV_VALUE_TREE = b"QX:KV:VALUE:CHUNK:V1", b"QX:KV:VALUE:TREE:V1"
+
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+
+
+def _bytes_arg(b: bytes):
+    buf = (ctypes.c_uint8 * max(len(b), 1)).from_buffer_copy(b if b else b"\0")
+    return buf
+
+
+def _digest_call(fn, *args) -> bytes:
+    out = (ctypes.c_uint8 * 32)()
+    if fn(*args, out) != 0:
+        raise RuntimeError("oracle hash: input rejected")
+    return bytes(out)
+
+
+def blake3(data: bytes) -> bytes:
+    """BLAKE3 (blake3 crate 1.8.7) of at most one 1024-byte chunk."""
+    L = lib()
+    return _digest_call(L.qxo_blake3, _bytes_arg(data), ctypes.c_size_t(len(data)))
+
+
+def hash_domain_b3(domain: bytes, fields) -> bytes:
+    """hash_domain(Blake3V1, domain, fields), crates/qx-commit/src/hash.rs:36-65."""
+    L = lib()
+    bufs = [_bytes_arg(f) for f in fields]
+    n = len(fields)
+    ptrs = (ctypes.POINTER(ctypes.c_uint8) * max(n, 1))(*[ctypes.cast(b, _u8p) for b in bufs])
+    lens = (ctypes.c_size_t * max(n, 1))(*[len(f) for f in fields])
+    return _digest_call(L.qxo_hash_domain_b3, _bytes_arg(domain), ctypes.c_size_t(len(domain)), ctypes.c_size_t(n),
+                        ptrs, lens)
+
+
+def chunk_tree_hash(data: bytes, chunk_bytes: int, leaf_domain: bytes, tree_domain: bytes) -> bytes:
+    """chunk_tree_hash, crates/qx-commit/src/state.rs:213-250."""
+    L = lib()
+    return _digest_call(L.qxo_chunk_tree_hash, _bytes_arg(data), ctypes.c_size_t(len(data)),
+                        ctypes.c_size_t(chunk_bytes), ctypes.c_char_p(leaf_domain), ctypes.c_char_p(tree_domain))
+
+
+def state_hash_v1(data: bytes) -> bytes:
+    """state_hash_v1, crates/qx-commit/src/state.rs:353-355."""
+    return _digest_call(lib().qxo_state_hash_v1, _bytes_arg(data), ctypes.c_size_t(len(data)))
+
+
+def kv_leaf_hash_v1(layer: int, token: int, key: bytes, value: bytes) -> bytes:
+    """kv_leaf_hash_v1, crates/qx-commit/src/state.rs:334-348."""
+    return _digest_call(lib().qxo_kv_leaf_hash_v1, ctypes.c_uint16(layer), ctypes.c_uint32(token), _bytes_arg(key),
+                        ctypes.c_size_t(len(key)), _bytes_arg(value), ctypes.c_size_t(len(value)))
+
+
+def verification_hashes(residuals: bytes, residual_stride: int, key_rows, value_rows, token: int, layers: int,
+                        interval: int) -> bytes:
+    """Per-token digests of kernels/verification_hash.metal:349-522: (layers + 1) x 64 bytes."""
+    L = lib()
+    row_bytes = len(key_rows[0])
+    kb = [_bytes_arg(r) for r in key_rows]
+    vb = [_bytes_arg(r) for r in value_rows]
+    kp = (ctypes.POINTER(ctypes.c_uint8) * layers)(*[ctypes.cast(b, _u8p) for b in kb])
+    vp = (ctypes.POINTER(ctypes.c_uint8) * layers)(*[ctypes.cast(b, _u8p) for b in vb])
+    out = (ctypes.c_uint8 * (64 * (layers + 1)))()
+    if L.qxo_verification_hashes(_bytes_arg(residuals), ctypes.c_size_t(residual_stride), kp, vp,
+                                 ctypes.c_size_t(row_bytes), ctypes.c_uint32(token), ctypes.c_uint32(layers),
+                                 ctypes.c_uint32(interval), out) != 0:
+        raise RuntimeError("oracle verification hashes: input rejected")
+    return bytes(out)

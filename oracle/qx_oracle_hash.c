@@ -1,0 +1,230 @@
+/*
+ * qx_oracle_hash.c -- CPU restatement of the reference's KV / state commitment
+ * hashing, used ONLY as test infrastructure (the parity checker of the HIP
+ * hashing kernels).  Nothing in the product (qx_amd/) links or calls it.
+ *
+ * Follows:
+ *   hash_domain (BLAKE3 branch)        crates/qx-commit/src/hash.rs:36-65
+ *   state_parent_v1, chunk_tree_hash   crates/qx-commit/src/state.rs:206-250
+ *   state_hash_v1                      crates/qx-commit/src/state.rs:353-355
+ *   kv_leaf_hash_v1 / _from_roots_v1   crates/qx-commit/src/state.rs:334-370
+ *   verification digests (per layer)   kernels/verification_hash.metal:349-522
+ *   domain strings                     crates/qx-commit/src/lib.rs:75-82
+ * BLAKE3 itself comes from the `blake3` crate 1.8.7 (Cargo.lock:656-659), which
+ * is not vendored in the reference; restated here from the published BLAKE3
+ * specification (compression function, message permutation, chunk flags).
+ * Every input the commitment scheme hashes fits one 1024-byte BLAKE3 chunk
+ * (a 256-byte state chunk plus its framing, two 32-byte digests, or a KV leaf
+ * header), so only the single-chunk case is implemented; longer inputs are
+ * rejected.
+ *
+ * Pins (tests/test_oracle_hash.py):
+ *   BLAKE3("")                      -> the specification's test vector
+ *   kv_leaf_hash_v1, kv_root,
+ *   checkpoint digest               -> crates/qx-commit/tests/golden_vectors.rs:66-190
+ *                                      (one-chunk trees; one- and two-block inputs)
+ *   multi-chunk trees, inputs of
+ *   three or more blocks            -> parity unpinned (no reference vector holds
+ *                                      them); they follow the texts above.
+ */
+#include <stddef.h>
+#include <stdint.h>
+#include <string.h>
+
+#define QXO_EXPORT __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------------------ */
+/* BLAKE3, single chunk                                                     */
+/* ------------------------------------------------------------------------ */
+static const uint32_t kIv[8] = {0x6A09E667u, 0xBB67AE85u, 0x3C6EF372u, 0xA54FF53Au,
+                                0x510E527Fu, 0x9B05688Cu, 0x1F83D9ABu, 0x5BE0CD19u};
+/* message word permutation applied between rounds */
+static const uint8_t kPerm[16] = {2, 6, 3, 10, 7, 0, 4, 13, 1, 11, 12, 5, 9, 14, 15, 8};
+enum { CHUNK_START = 1, CHUNK_END = 2, ROOT = 8 };
+
+static inline uint32_t rotr32(uint32_t x, int n) { return (x >> n) | (x << (32 - n)); }
+
+static void g_mix(uint32_t* v, int a, int b, int c, int d, uint32_t mx, uint32_t my) {
+    v[a] = v[a] + v[b] + mx;
+    v[d] = rotr32(v[d] ^ v[a], 16);
+    v[c] = v[c] + v[d];
+    v[b] = rotr32(v[b] ^ v[c], 12);
+    v[a] = v[a] + v[b] + my;
+    v[d] = rotr32(v[d] ^ v[a], 8);
+    v[c] = v[c] + v[d];
+    v[b] = rotr32(v[b] ^ v[c], 7);
+}
+
+/* compression of one 64-byte block; returns the 8-word chaining value */
+static void compress(uint32_t cv[8], const uint32_t block[16], uint32_t block_len, uint32_t flags) {
+    uint32_t v[16], m[16], t[16];
+    for (int i = 0; i < 8; ++i) v[i] = cv[i];
+    for (int i = 0; i < 4; ++i) v[8 + i] = kIv[i];
+    v[12] = 0;  /* chunk counter (low): the only chunk is chunk 0 */
+    v[13] = 0;
+    v[14] = block_len;
+    v[15] = flags;
+    memcpy(m, block, sizeof m);
+    for (int r = 0; r < 7; ++r) {
+        g_mix(v, 0, 4, 8, 12, m[0], m[1]);
+        g_mix(v, 1, 5, 9, 13, m[2], m[3]);
+        g_mix(v, 2, 6, 10, 14, m[4], m[5]);
+        g_mix(v, 3, 7, 11, 15, m[6], m[7]);
+        g_mix(v, 0, 5, 10, 15, m[8], m[9]);
+        g_mix(v, 1, 6, 11, 12, m[10], m[11]);
+        g_mix(v, 2, 7, 8, 13, m[12], m[13]);
+        g_mix(v, 3, 4, 9, 14, m[14], m[15]);
+        for (int i = 0; i < 16; ++i) t[i] = m[kPerm[i]];
+        memcpy(m, t, sizeof m);
+    }
+    for (int i = 0; i < 8; ++i) cv[i] = v[i] ^ v[i + 8];
+}
+
+/* BLAKE3 of len <= 1024 bytes (one chunk, which is also the root) */
+QXO_EXPORT int qxo_blake3(const uint8_t* in, size_t len, uint8_t out[32]) {
+    if (len > 1024) return -1;
+    uint32_t cv[8];
+    memcpy(cv, kIv, sizeof cv);
+    const size_t blocks = len == 0 ? 1 : (len + 63) / 64;
+    for (size_t b = 0; b < blocks; ++b) {
+        uint8_t buf[64] = {0};
+        const size_t off = b * 64;
+        const size_t n = len - off < 64 ? len - off : 64;
+        if (n) memcpy(buf, in + off, n);
+        uint32_t w[16];
+        for (int i = 0; i < 16; ++i)
+            w[i] = (uint32_t)buf[4 * i] | ((uint32_t)buf[4 * i + 1] << 8) | ((uint32_t)buf[4 * i + 2] << 16) |
+                   ((uint32_t)buf[4 * i + 3] << 24);
+        uint32_t flags = 0;
+        if (b == 0) flags |= CHUNK_START;
+        if (b + 1 == blocks) flags |= CHUNK_END | ROOT;
+        compress(cv, w, (uint32_t)n, flags);
+    }
+    for (int i = 0; i < 8; ++i) {
+        out[4 * i] = (uint8_t)cv[i];
+        out[4 * i + 1] = (uint8_t)(cv[i] >> 8);
+        out[4 * i + 2] = (uint8_t)(cv[i] >> 16);
+        out[4 * i + 3] = (uint8_t)(cv[i] >> 24);
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* hash_domain (hash.rs:36-65): domain || for each field: u64 LE len || field */
+/* ------------------------------------------------------------------------ */
+QXO_EXPORT int qxo_hash_domain_b3(const uint8_t* domain, size_t domain_len, size_t nfields, const uint8_t* const* fields,
+                                  const size_t* lens, uint8_t out[32]) {
+    uint8_t buf[1024];
+    size_t n = 0;
+    if (domain_len > sizeof buf) return -1;
+    memcpy(buf, domain, domain_len);
+    n = domain_len;
+    for (size_t f = 0; f < nfields; ++f) {
+        if (n + 8 + lens[f] > sizeof buf) return -1;
+        const uint64_t l = lens[f];
+        for (int i = 0; i < 8; ++i) buf[n + i] = (uint8_t)(l >> (8 * i));
+        n += 8;
+        if (lens[f]) memcpy(buf + n, fields[f], lens[f]);
+        n += lens[f];
+    }
+    return qxo_blake3(buf, n, out);
+}
+
+/* ------------------------------------------------------------------------ */
+/* chunk tree (state.rs:206-250)                                             */
+/* ------------------------------------------------------------------------ */
+static const char kMerkleEmpty[] = "QX:MERKLE:EMPTY:V1";
+
+/* parent = BLAKE3(left || right), no domain (state_parent_v1) */
+static void parent_hash(const uint8_t l[32], const uint8_t r[32], uint8_t out[32]) {
+    uint8_t b[64];
+    memcpy(b, l, 32);
+    memcpy(b + 32, r, 32);
+    qxo_blake3(b, 64, out);
+}
+
+#define QXO_MAX_TREE_LEAVES 4096
+
+QXO_EXPORT int qxo_chunk_tree_hash(const uint8_t* bytes, size_t len, size_t chunk_bytes, const char* leaf_domain,
+                                   const char* tree_domain, uint8_t out[32]) {
+    if (len == 0 || chunk_bytes == 0) return -1;  /* "state commitment input must not be empty" */
+    const size_t leaves = (len + chunk_bytes - 1) / chunk_bytes;
+    size_t cap = 1;
+    while (cap < leaves) cap <<= 1;
+    if (cap > QXO_MAX_TREE_LEAVES) return -1;
+    static uint8_t nodes[QXO_MAX_TREE_LEAVES][32];
+    for (size_t i = 0; i < leaves; ++i) {
+        const uint32_t idx = (uint32_t)i;
+        const uint8_t ib[4] = {(uint8_t)idx, (uint8_t)(idx >> 8), (uint8_t)(idx >> 16), (uint8_t)(idx >> 24)};
+        const size_t off = i * chunk_bytes;
+        const size_t n = len - off < chunk_bytes ? len - off : chunk_bytes;
+        const uint8_t* fields[2] = {ib, bytes + off};
+        const size_t lens[2] = {4, n};
+        if (qxo_hash_domain_b3((const uint8_t*)leaf_domain, strlen(leaf_domain), 2, fields, lens, nodes[i])) return -1;
+    }
+    if (leaves < cap) {
+        uint8_t empty[32];
+        const uint8_t* fields[1] = {(const uint8_t*)tree_domain};
+        const size_t lens[1] = {strlen(tree_domain)};
+        if (qxo_hash_domain_b3((const uint8_t*)kMerkleEmpty, strlen(kMerkleEmpty), 1, fields, lens, empty)) return -1;
+        for (size_t i = leaves; i < cap; ++i) memcpy(nodes[i], empty, 32);
+    }
+    for (size_t w = cap; w > 1; w >>= 1)
+        for (size_t i = 0; i < w / 2; ++i) parent_hash(nodes[2 * i], nodes[2 * i + 1], nodes[i]);
+    memcpy(out, nodes[0], 32);
+    return 0;
+}
+
+QXO_EXPORT int qxo_state_hash_v1(const uint8_t* bytes, size_t len, uint8_t out[32]) {
+    return qxo_chunk_tree_hash(bytes, len, 256, "QX:STATE:CHUNK:V1", "QX:STATE:V1", out);
+}
+
+/* kv_leaf_hash_from_roots_v1: hash_domain(D_KV, [u16 layer, u32 token, key_root, value_root]) */
+QXO_EXPORT int qxo_kv_leaf_hash_from_roots_v1(uint16_t layer, uint32_t token, const uint8_t key_root[32],
+                                              const uint8_t value_root[32], uint8_t out[32]) {
+    const uint8_t lb[2] = {(uint8_t)layer, (uint8_t)(layer >> 8)};
+    const uint8_t tb[4] = {(uint8_t)token, (uint8_t)(token >> 8), (uint8_t)(token >> 16), (uint8_t)(token >> 24)};
+    const uint8_t* fields[4] = {lb, tb, key_root, value_root};
+    const size_t lens[4] = {2, 4, 32, 32};
+    return qxo_hash_domain_b3((const uint8_t*)"QX:KV:V1", 8, 4, fields, lens, out);
+}
+
+QXO_EXPORT int qxo_kv_leaf_hash_v1(uint16_t layer, uint32_t token, const uint8_t* key, size_t key_len,
+                                   const uint8_t* value, size_t value_len, uint8_t out[32]) {
+    uint8_t kr[32], vr[32];
+    if (qxo_chunk_tree_hash(key, key_len, 256, "QX:KV:KEY:CHUNK:V1", "QX:KV:KEY:TREE:V1", kr)) return -1;
+    if (qxo_chunk_tree_hash(value, value_len, 256, "QX:KV:VALUE:CHUNK:V1", "QX:KV:VALUE:TREE:V1", vr)) return -1;
+    return qxo_kv_leaf_hash_from_roots_v1(layer, token, kr, vr, out);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Per-token verification digests, kernels/verification_hash.metal:349-522:  */
+/* out[p] (64 bytes) for p = 0..layers.  p = 0 (genesis): state root of      */
+/* residual snapshot 0, then 32 zero bytes.  p >= 1 (layer p-1): the state   */
+/* root of snapshot p when the layer is a checkpoint ((layer+1) % interval   */
+/* == 0 or the last layer) else 32 zero bytes, then kv_leaf_hash_v1(layer,  */
+/* token, key row, value row).                                               */
+/* ------------------------------------------------------------------------ */
+QXO_EXPORT int qxo_verification_hashes(const uint8_t* residuals, size_t residual_stride, const uint8_t* const* key_rows,
+                                       const uint8_t* const* value_rows, size_t row_bytes, uint32_t token,
+                                       uint32_t layers, uint32_t interval, uint8_t* out) {
+    if (layers == 0 || interval == 0 || interval > layers) return -1;
+    for (uint32_t p = 0; p <= layers; ++p) {
+        uint8_t* o = out + (size_t)p * 64;
+        const int genesis = p == 0;
+        const uint32_t layer = genesis ? 0 : p - 1;
+        const int checkpoint = genesis || (layer + 1) % interval == 0 || layer + 1 == layers;
+        if (checkpoint) {
+            if (qxo_state_hash_v1(residuals + (size_t)p * residual_stride, residual_stride, o)) return -1;
+        } else {
+            memset(o, 0, 32);
+        }
+        if (genesis) {
+            memset(o + 32, 0, 32);
+        } else if (qxo_kv_leaf_hash_v1((uint16_t)layer, token, key_rows[layer], row_bytes, value_rows[layer], row_bytes,
+                                       o + 32)) {
+            return -1;
+        }
+    }
+    return 0;
+}

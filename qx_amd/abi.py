@@ -102,6 +102,10 @@ SIGNATURES = {
                                                c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_uint64]),
     "qxh_encode_kv_gather_token_rows": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32,
                                                   c_void_p, c_void_p]),
+    "qxh_encode_kv_leaf_hashes": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
+                                            c_void_p, c_uint64]),
+    "qxh_encode_verification_hashes": (c_int32, [c_void_p, c_void_p, c_uint32, c_void_p, c_uint64, c_uint32,
+                                                 c_uint32, c_uint32, c_uint32, c_void_p, c_uint64]),
     "qxh_granite_block_workspace_bytes": (c_int32, [c_void_p, c_uint32, P(c_uint64)]),
     "qxh_encode_granite_attention_block": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32,
                                                      P(GraniteLayerWeights), c_void_p, c_void_p, c_void_p,

@@ -51,6 +51,12 @@ hipError_t launch_qwen_qk_norm_rope(void* q, void* k, const float* qn, const flo
 hipError_t launch_kv_gather(const ShapeDims& s, const KvLayer& kv, uint32_t pos_begin, uint32_t count, void* keys_out,
                             void* values_out, hipStream_t st);
 hipError_t launch_fill_normal(void* data, int dtype, uint64_t count, uint64_t seed, float stddev, hipStream_t st);
+// kv_hash.hip: BLAKE3 commitments of token rows
+hipError_t launch_kv_leaf_hashes(const ShapeDims& s, const KvLayer& kv, uint32_t layer, uint32_t sequences,
+                                 uint32_t token_begin, uint32_t count, void* out, hipStream_t st);
+hipError_t launch_verification_hashes(const ShapeDims& s, const KvLayer& kv_layer0, uint64_t layer_stride_elems,
+                                      const void* residuals, uint32_t residual_stride, uint32_t token, uint32_t layers,
+                                      uint32_t interval, void* out, hipStream_t st);
 hipError_t launch_kv_fill_normal(const ShapeDims& s, const KvLayer& kv_all_layers_seq0, uint32_t layers, uint32_t sequences,
                                  uint64_t layer_stride, uint32_t length, uint64_t seed, hipStream_t st);
 hipError_t launch_conformance(const float* in, const uint32_t* coords, uint32_t n, uint32_t* e, uint32_t* r, uint32_t* sn,

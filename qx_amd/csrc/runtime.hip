@@ -670,6 +670,71 @@ extern "C" int32_t qxh_encode_kv_gather_token_rows(qxh_graph* g, const qxh_kv_ca
     return QXH_OK;
 }
 
+extern "C" int32_t qxh_encode_kv_leaf_hashes(qxh_graph* g, const qxh_kv_cache* c, uint32_t layer, uint32_t first_seq,
+                                             uint32_t sequences, uint32_t begin, uint32_t count, void* out,
+                                             uint64_t out_bytes) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    QXH_REQUIRE(sequences > 0, QXH_ERR_INVALID_ARGUMENT, "kv leaf hashes of zero sequences");
+    if ((r = check_range(c, layer, first_seq, sequences))) return r;
+    QXH_REQUIRE(count > 0, QXH_ERR_INVALID_ARGUMENT, "kv leaf hashes of zero rows");
+    QXH_REQUIRE(out, QXH_ERR_INVALID_ARGUMENT, "kv leaf hashes: null output");
+    QXH_REQUIRE(c->desc.key_dtype == c->desc.value_dtype, QXH_ERR_UNSUPPORTED,
+                "kv leaf hashes need equal K and V dtypes");
+    QXH_REQUIRE(out_bytes >= (uint64_t)sequences * count * 32, QXH_ERR_INVALID_ARGUMENT,
+                "kv leaf hash output of %llu bytes is smaller than %llu", (unsigned long long)out_bytes,
+                (unsigned long long)sequences * count * 32);
+    for (uint32_t s = first_seq; s < first_seq + sequences; ++s) {
+        const uint32_t len = c->cursor[(size_t)layer * c->desc.sequences + s];
+        QXH_REQUIRE((uint64_t)begin + count <= len, QXH_ERR_KV_POSITION,
+                    "KV position %llu is outside committed length %u", (unsigned long long)begin + count - 1, len);
+    }
+    hipError_t e = launch_kv_leaf_hashes(c->dims, kv_layer(c, layer, first_seq), layer, sequences, begin, count, out,
+                                         g->stream);
+    if (e != hipSuccess) return hip_fail(e, "kv leaf hash launch");
+    g->dispatches += 1;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_encode_verification_hashes(qxh_graph* g, const qxh_kv_cache* c, uint32_t seq,
+                                                  const void* residuals, uint64_t residual_bytes,
+                                                  uint32_t residual_stride, uint32_t token, uint32_t layers,
+                                                  uint32_t interval, void* out, uint64_t out_bytes) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    QXH_REQUIRE(c && residuals && out, QXH_ERR_INVALID_ARGUMENT, "verification hashes: null argument");
+    QXH_REQUIRE(layers >= 1 && layers <= c->desc.layers, QXH_ERR_INVALID_ARGUMENT,
+                "verification layer count %u is outside 1..=%u", layers, c->desc.layers);
+    if ((r = check_range(c, 0, seq, 1))) return r;
+    QXH_REQUIRE(interval >= 1 && interval <= layers, QXH_ERR_INVALID_ARGUMENT,
+                "verification checkpoint interval %u is outside 1..=%u", interval, layers);
+    QXH_REQUIRE(out_bytes >= (uint64_t)(layers + 1) * 64, QXH_ERR_INVALID_ARGUMENT,
+                "verification digest output is too small");
+    QXH_REQUIRE(residual_bytes >= (uint64_t)(layers + 1) * residual_stride, QXH_ERR_INVALID_ARGUMENT,
+                "verification residual snapshot buffer is too small");
+    const uint32_t chunks = residual_stride / 256;
+    QXH_REQUIRE(residual_stride % 256 == 0 && chunks >= 1 && chunks <= 64 && (chunks & (chunks - 1)) == 0,
+                QXH_ERR_INVALID_ARGUMENT, "verification residual size %u is not a power-of-two multiple of 256 (<= 64 chunks)",
+                residual_stride);
+    QXH_REQUIRE(c->desc.key_dtype == c->desc.value_dtype, QXH_ERR_UNSUPPORTED,
+                "verification hashes need equal K and V dtypes");
+    const uint64_t row = (uint64_t)c->dims.kv_heads * c->dims.head_dim * dtype_bytes(c->desc.key_dtype);
+    const uint64_t kv_chunks = row / 256;
+    QXH_REQUIRE(row % 256 == 0 && kv_chunks <= 8 && (kv_chunks & (kv_chunks - 1)) == 0, QXH_ERR_UNSUPPORTED,
+                "verification KV row of %llu bytes is not a power-of-two multiple of 256 (<= 8 chunks)",
+                (unsigned long long)row);
+    for (uint32_t l = 0; l < layers; ++l) {
+        const uint32_t len = c->cursor[(size_t)l * c->desc.sequences + seq];
+        QXH_REQUIRE(token < len, QXH_ERR_KV_POSITION, "verification token %u is outside layer %u's committed length %u",
+                    token, l, len);
+    }
+    hipError_t e = launch_verification_hashes(c->dims, kv_layer(c, 0, seq), c->layer_stride, residuals,
+                                              residual_stride, token, layers, interval, out, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "verification hash launch");
+    g->dispatches += 1;
+    return QXH_OK;
+}
+
 extern "C" int32_t qxh_granite_block_workspace_bytes(const qxh_kv_cache* c, uint32_t length, uint64_t* bytes) {
     QXH_REQUIRE(c && bytes, QXH_ERR_INVALID_ARGUMENT, "granite_block_workspace_bytes: null argument");
     QXH_REQUIRE(c->desc.shape == QXH_SHAPE_GRANITE, QXH_ERR_INVALID_ARGUMENT, "Granite block needs a Granite cache");

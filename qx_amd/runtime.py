@@ -205,6 +205,27 @@ class KvArena:
                                                     _ptr(k), _ptr(v)))
         return k, v
 
+    def leaf_hashes(self, graph: Graph, layer: int, begin: int, count: int, first_sequence: int = 0,
+                    sequences: int = 1, out=None):
+        """kv_leaf_hash_v1 digests of token rows [begin, begin + count) of each
+        sequence: uint8 [sequences][count][32] on the device."""
+        if out is None:
+            out = torch.empty((sequences, count, 32), dtype=torch.uint8, device=f"cuda:{self.ctx.device}")
+        check(lib().qxh_encode_kv_leaf_hashes(graph.handle, self._h, layer, first_sequence, sequences, begin, count,
+                                              _ptr(out), out.numel()))
+        return out
+
+    def verification_hashes(self, graph: Graph, residual_snapshots, residual_stride: int, token: int, layers: int,
+                            checkpoint_interval: int, sequence: int = 0, out=None):
+        """Per-token digests (state root, KV leaf) for p = 0..layers: uint8 [layers + 1][64]."""
+        if out is None:
+            out = torch.empty((layers + 1, 64), dtype=torch.uint8, device=f"cuda:{self.ctx.device}")
+        rb = residual_snapshots.numel() * residual_snapshots.element_size()
+        check(lib().qxh_encode_verification_hashes(graph.handle, self._h, sequence, _ptr(residual_snapshots), rb,
+                                                   residual_stride, token, layers, checkpoint_interval, _ptr(out),
+                                                   out.numel()))
+        return out
+
     def fill_normal(self, graph: Graph, seed: int, length: int):
         check(lib().qxh_encode_kv_fill_normal(graph.handle, self._h, seed, length))
 
