@@ -224,6 +224,43 @@ def bench_cfg5a(ctx, steps, warmup):
 
 
 # ---------------------------------------------------------------------------
+# KV commitment leaves of every token row of one cfg4-sized layer
+# ---------------------------------------------------------------------------
+# Algorithmic VALU work of one BLAKE3 compression: 7 rounds x 8 G functions x
+# (6 adds + 4 xors + 4 rotates) on 32-bit words.  A leaf of 1024-byte K and V
+# rows takes 2 x 4 chunk leaves of 5 blocks, 2 x 3 tree parents and 2 blocks of
+# the leaf itself: 48 compressions.
+B3_OPS_PER_COMPRESSION = 7 * 8 * 14
+VALU_PEAK_TOPS = 256 * 4 * 32 * 2.4e9 / 1e12  # 32-bit lane ops/s: MI355X FP32 vector peak / 2
+
+
+def bench_kv_hash(ctx, steps, warmup):
+    import torch
+    from qx_amd import abi
+    from qx_amd import runtime as rt
+
+    SEQS, L = 256, 4096
+    stream = torch.cuda.current_stream()
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, SEQS, L, abi.F16)
+    with rt.Graph(ctx, stream) as g:
+        arena.fill_normal(g, seed=21, length=L)
+    out = torch.empty((SEQS, L, 32), dtype=torch.uint8, device="cuda:0")
+    g = rt.Graph(ctx, stream)
+    ms = timed(lambda: arena.leaf_hashes(g, 0, 0, L, sequences=SEQS, out=out), steps, warmup, stream)
+    g.finish()
+    leaves = SEQS * L
+    row = 8 * 64 * 2
+    ops = leaves * 48 * B3_OPS_PER_COMPRESSION
+    tops = ops / (ms * 1e-3) / 1e12
+    return {"us_per_layer": ms * 1000.0, "leaves": leaves, "kv_bytes": leaves * 2 * row,
+            "gb_per_s": leaves * 2 * row / (ms * 1e-3) / 1e9, "leaves_per_s": leaves / (ms * 1e-3),
+            "roofline": {"bound": "valu", "achieved": round(tops, 2), "peak": round(VALU_PEAK_TOPS, 1),
+                         "unit": "Top/s", "frac": round(tops / VALU_PEAK_TOPS, 4), "traffic": None},
+            "note": "kv_leaf_hash_v1 (BLAKE3) of all 256 x 4096 fp16 token rows of one Granite layer; "
+                    "ops = 48 compressions x 784 32-bit ops per leaf"}
+
+
+# ---------------------------------------------------------------------------
 # cfg3 / cfg5b: causal prefill (MFMA)
 # ---------------------------------------------------------------------------
 def bench_prefill(ctx, steps, warmup, shape_name):
@@ -304,12 +341,25 @@ def cpu_baseline(seconds=10.0):
     with cf.ThreadPoolExecutor(cores) as ex:
         list(ex.map(work, caches))
     tall = (time.perf_counter() - t0) / (per_thread * cores)
+    # KV commitment leaves of fp16 token rows (1024-byte K and V rows), one thread
+    krow = keys[:256].astype(np.float16).tobytes()
+    vrow = vals[:256].astype(np.float16).tobytes()
+    nh = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 2.0 or nh < 100:
+        O.kv_leaf_hash_v1(0, nh, krow[(nh % 256) * 1024:(nh % 256 + 1) * 1024],
+                          vrow[(nh % 256) * 1024:(nh % 256 + 1) * 1024])
+        nh += 1
+    th = (time.perf_counter() - t0) / nh
     return {
         "value": round(t1 * 24 * 1e6, 1), "unit": "us/sequence-token (24 layers)", "cores": 1, "kind": "port",
         "sample": f"{n} single-thread oracle attends of one Granite layer at ctx 4096 (fp16-rounded KV, "
                   f"upcast fp32 math), x24 layers; cfg4 step = 256 sequences",
         "all_core": {"value": round(tall * 24 * 1e6, 1), "cores": cores,
                      "sample": f"{per_thread * cores} attends over {cores} threads (independent sequences)"},
+        "kv_hash": {"value": round(1.0 / th, 1), "unit": "leaves/s", "cores": 1, "kind": "port",
+                    "sample": f"{nh} oracle kv_leaf_hash_v1 calls on 1024-byte fp16 K and V rows "
+                              f"(includes the Python call overhead)"},
     }
 
 
@@ -357,7 +407,8 @@ def run(ctx, args):
         log("cfg4", json.dumps(head))
     if not args.no_detail:
         for name, fn in (("cfg1", bench_cfg1), ("cfg2", bench_cfg2), ("cfg3", lambda c, k, w: bench_prefill(c, k, w, "cfg3")),
-                         ("cfg5a", bench_cfg5a), ("cfg5b", lambda c, k, w: bench_prefill(c, k, w, "cfg5b"))):
+                         ("cfg5a", bench_cfg5a), ("cfg5b", lambda c, k, w: bench_prefill(c, k, w, "cfg5b")),
+                         ("kvhash", bench_kv_hash)):
             if only and name not in only:
                 continue
             try:

@@ -16,9 +16,10 @@
 // compile-time except the chunk index) and runs five compressions.  The
 // chunk digests of a row sit in a power-of-two group of adjacent lanes and
 // are reduced with cross-lane shuffles; lane 0 of the group finishes the leaf.
-// All lanes of a group run every step (no divergence): the waste is the upper
-// tree levels and the final leaf, 4 of 16 compressions per lane for 4-chunk
-// rows.
+// Every lane of a group runs every step (no divergence).  Per lane: 10
+// compressions for its K and V chunks, one for the first tree level of both
+// sides together, one per further level, two for the leaf: 14 for 4-chunk
+// rows, the minimum for 16 leaves per wave.
 #include "common.h"
 #include "internal.h"
 
@@ -105,18 +106,26 @@ constexpr Prefix make_prefix(const char (&domain)[N]) {
 }
 
 // Word w of the message stream prefix || chunk || zero padding (P = prefix
-// bytes, compile-time after unrolling).
+// bytes; everything but the chunk words is compile-time after unrolling).
+// The chunk arrives as sixteen 16-byte groups g[0..15].
 template <int P>
-__device__ __forceinline__ uint32_t stream_word(int w, const uint32_t (&pw)[12], const uint32_t (&c)[64]) {
+__device__ __forceinline__ uint32_t stream_word(int w, const uint32_t (&pw)[12], const u32x4 (&g)[16]) {
+    auto cw = [&](int q) -> uint32_t { return q < 64 ? g[q >> 2][q & 3] : 0u; };
     const int b0 = 4 * w;
     if (b0 + 4 <= P) return pw[w];
-    if (b0 < P) return pw[w] | (c[0] << (8 * (P - b0)));
+    if (b0 < P) return pw[w] | (cw(0) << (8 * (P - b0)));
     const int s = b0 - P;
     if (s >= 256) return 0u;
     const int q = s >> 2, r = s & 3;
-    if (r == 0) return c[q];
-    const uint32_t hi = q + 1 < 64 ? c[q + 1] : 0u;
-    return (c[q] >> (8 * r)) | (hi << (32 - 8 * r));
+    if (r == 0) return cw(q);
+    return (cw(q) >> (8 * r)) | (cw(q + 1) << (32 - 8 * r));
+}
+
+// last 16-byte chunk group that message block b reads (-1: none)
+template <int P>
+constexpr int last_group(int b) {
+    const int hi = 64 * b + 63 - P;   // last chunk byte the block can touch
+    return hi < 0 ? -1 : (hi >> 4) > 15 ? 15 : (hi >> 4);
 }
 
 // Leaf domains (crates/qx-commit/src/lib.rs:78-81)
@@ -133,9 +142,12 @@ struct ValueChunkDomain {
     static constexpr Prefix prefix() { return make_prefix("QX:KV:VALUE:CHUNK:V1"); }
 };
 
-// BLAKE3 digest of one chunk leaf (chunk index idx, 256 data bytes in c).
-template <class Dom>
-__device__ __forceinline__ void chunk_leaf(uint32_t idx, const uint32_t (&c)[64], uint32_t (&out)[8]) {
+// BLAKE3 digest of one chunk leaf (chunk index idx).  load(i) returns bytes
+// [16 i, 16 i + 16) of the chunk; each group is loaded once, one message
+// block ahead of its first use, so only about two blocks' worth of chunk
+// data is live at a time.
+template <class Dom, class Load>
+__device__ __forceinline__ void chunk_leaf(uint32_t idx, Load load, uint32_t (&out)[8]) {
     constexpr Prefix pre = Dom::prefix();
     constexpr int P = Dom::len + 20;
     static_assert(P == pre.len && P <= 48, "framing length");
@@ -148,12 +160,19 @@ __device__ __forceinline__ void chunk_leaf(uint32_t idx, const uint32_t (&c)[64]
     if constexpr (sh != 0) pw[ib / 4 + 1] |= idx >> (32 - sh);
     constexpr int total = P + 256;
     constexpr int blocks = (total + 63) / 64;
+    u32x4 g[16];
+#pragma unroll
+    for (int i = 0; i <= last_group<P>(1); ++i) g[i] = load(i);
     iv_init(out);
 #pragma unroll
     for (int b = 0; b < blocks; ++b) {
+        if (b + 1 < blocks) {
+#pragma unroll
+            for (int i = last_group<P>(b + 1) + 1; i <= last_group<P>(b + 2); ++i) g[i] = load(i);
+        }
         uint32_t m[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) m[i] = stream_word<P>(16 * b + i, pw, c);
+        for (int i = 0; i < 16; ++i) m[i] = stream_word<P>(16 * b + i, pw, g);
         const uint32_t len = b + 1 < blocks ? 64u : (uint32_t)(total - 64 * (blocks - 1));
         const uint32_t flags = (b == 0 ? kFlagStart : 0u) | (b + 1 == blocks ? kFlagEnd | kFlagRoot : 0u);
         compress(out, m, len, flags);
@@ -175,8 +194,8 @@ __device__ __forceinline__ void parent_digest(const uint32_t (&l)[8], const uint
 // Pairwise reduction of the digests held by a power-of-two group of `width`
 // adjacent lanes (lane index within the group: gl).  Both lanes of a pair
 // compute the parent, so after the loop every lane of the group holds the root.
-__device__ __forceinline__ void group_tree(uint32_t (&d)[8], int gl, int width) {
-    for (int lvl = 1; lvl < width; lvl <<= 1) {
+__device__ __forceinline__ void group_tree(uint32_t (&d)[8], int gl, int width, int first = 1) {
+    for (int lvl = first; lvl < width; lvl <<= 1) {
         uint32_t o[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[i] = (uint32_t)__shfl_xor((int)d[i], lvl);
@@ -189,6 +208,31 @@ __device__ __forceinline__ void group_tree(uint32_t (&d)[8], int gl, int width) 
         }
         parent_digest(l, r, d);
     }
+}
+
+// K and V chunk digests of one row sit in a group of CH lanes (lane c holds
+// chunk c of both).  The first tree level of both sides takes one compression
+// per lane: lane c < CH/2 forms K node c from chunks 2c and 2c+1, lane
+// c >= CH/2 forms V node c - CH/2.  The remaining levels reduce each half of
+// the group; afterwards lanes [0, CH/2) hold the key root and lanes
+// [CH/2, CH) the value root.
+template <int CH>
+__device__ __forceinline__ void kv_roots(const uint32_t (&kd)[8], const uint32_t (&vd)[8], int lane, int gl,
+                                         uint32_t (&node)[8]) {
+    constexpr int H = CH / 2;
+    const bool vside = gl >= H;
+    const int p = vside ? gl - H : gl;
+    const int base = lane - gl;
+    uint32_t l[8], r[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int lk = __shfl((int)kd[i], base + 2 * p), rk = __shfl((int)kd[i], base + 2 * p + 1);
+        const int lv = __shfl((int)vd[i], base + 2 * p), rv = __shfl((int)vd[i], base + 2 * p + 1);
+        l[i] = (uint32_t)(vside ? lv : lk);
+        r[i] = (uint32_t)(vside ? rv : rk);
+    }
+    parent_digest(l, r, node);
+    group_tree(node, p, H);
 }
 
 // KV leaf: BLAKE3("QX:KV:V1" || u64 2 || u16 layer || u64 4 || u32 token ||
@@ -221,21 +265,12 @@ __device__ __forceinline__ void kv_leaf(uint32_t layer, uint32_t token, const ui
     compress(out, m1, 46u, kFlagEnd | kFlagRoot);
 }
 
-// 256 bytes of a token row [kv_head][head_bytes] starting at row byte `off`
-// (a multiple of 256), from the head-major layer base.
-__device__ __forceinline__ void load_chunk(const char* base, uint64_t head_stride_bytes, uint32_t head_shift,
-                                           uint64_t row_off, uint32_t off, uint32_t (&c)[64]) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const uint32_t o = off + 16u * j;
-        const uint32_t head = o >> head_shift, within = o & ((1u << head_shift) - 1u);
-        const u32x4 v =
-            *reinterpret_cast<const u32x4*>(base + head * head_stride_bytes + row_off + within);
-        c[4 * j] = v[0];
-        c[4 * j + 1] = v[1];
-        c[4 * j + 2] = v[2];
-        c[4 * j + 3] = v[3];
-    }
+// Byte address of row byte o of a token row [kv_head][head_bytes] in the
+// head-major layer base (o is a multiple of 16).
+__device__ __forceinline__ const char* row_byte(const char* base, uint64_t head_stride_bytes, uint32_t head_shift,
+                                                uint64_t row_off, uint32_t o) {
+    const uint32_t head = o >> head_shift, within = o & ((1u << head_shift) - 1u);
+    return base + head * head_stride_bytes + row_off + within;
 }
 
 __device__ __forceinline__ void store_digest(uint8_t* dst, const uint32_t (&d)[8]) {
@@ -264,7 +299,7 @@ struct KvLeafArgs {
 
 // CH = chunks per row (4 or 8): 64 / CH leaves per wave, 4 waves per block
 template <int CH>
-__global__ __launch_bounds__(256) void kv_leaf_hash_kernel(KvLeafArgs a) {
+__global__ __launch_bounds__(256, 3) void kv_leaf_hash_kernel(KvLeafArgs a) {
     constexpr int LPW = 64 / CH;
     const int lane = threadIdx.x & 63;
     const int gl = lane % CH;
@@ -275,15 +310,21 @@ __global__ __launch_bounds__(256) void kv_leaf_hash_kernel(KvLeafArgs a) {
     const uint32_t s = (uint32_t)(lf / a.count), i = (uint32_t)(lf % a.count);
     const uint32_t tok = a.token_begin + i;
     const uint64_t row_off = (uint64_t)tok << a.head_shift;
-    uint32_t c[64], kr[8], vr[8];
-    load_chunk(a.keys + s * a.seq_stride_bytes, a.head_stride_bytes, a.head_shift, row_off, 256u * gl, c);
-    chunk_leaf<KeyChunkDomain>((uint32_t)gl, c, kr);
-    load_chunk(a.values + s * a.seq_stride_bytes, a.head_stride_bytes, a.head_shift, row_off, 256u * gl, c);
-    chunk_leaf<ValueChunkDomain>((uint32_t)gl, c, vr);
-    group_tree(kr, gl, CH);
-    group_tree(vr, gl, CH);
-    uint32_t d[8];
-    kv_leaf(a.layer, tok, kr, vr, d);
+    const char* kb = a.keys + s * a.seq_stride_bytes;
+    const char* vb = a.values + s * a.seq_stride_bytes;
+    uint32_t kd[8], vd[8], node[8], d[8];
+    chunk_leaf<KeyChunkDomain>((uint32_t)gl, [&](int i) {
+        return *reinterpret_cast<const u32x4*>(row_byte(kb, a.head_stride_bytes, a.head_shift, row_off, 256u * gl + 16u * i));
+    }, kd);
+    chunk_leaf<ValueChunkDomain>((uint32_t)gl, [&](int i) {
+        return *reinterpret_cast<const u32x4*>(row_byte(vb, a.head_stride_bytes, a.head_shift, row_off, 256u * gl + 16u * i));
+    }, vd);
+    kv_roots<CH>(kd, vd, lane, gl, node);
+    // lane 0 of the group: key root; lane CH/2: value root
+    uint32_t vr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vr[i] = (uint32_t)__shfl((int)node[i], lane - gl + CH / 2);
+    kv_leaf(a.layer, tok, node, vr, d);
     if (live && gl == 0) store_digest(a.out + leaf * 32, d);
 }
 
@@ -319,20 +360,12 @@ __global__ __launch_bounds__(192) void verification_hash_kernel(VerifyArgs a) {
     const bool checkpoint = genesis || (layer + 1u) % a.interval == 0u || layer + 1u == a.layers;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    uint32_t c[64], d[8];
+    uint32_t d[8];
     if (wave == 0) {
         if (checkpoint) {
             const uint32_t gl = (uint32_t)lane < a.state_chunks ? (uint32_t)lane : 0u;
             const char* src = a.residuals + (uint64_t)p * a.residual_stride + 256u * gl;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const u32x4 v = *reinterpret_cast<const u32x4*>(src + 16 * j);
-                c[4 * j] = v[0];
-                c[4 * j + 1] = v[1];
-                c[4 * j + 2] = v[2];
-                c[4 * j + 3] = v[3];
-            }
-            chunk_leaf<StateChunkDomain>(gl, c, d);
+            chunk_leaf<StateChunkDomain>(gl, [&](int i) { return *reinterpret_cast<const u32x4*>(src + 16 * i); }, d);
             group_tree(d, lane, (int)a.state_chunks);
         } else {
 #pragma unroll
@@ -343,10 +376,13 @@ __global__ __launch_bounds__(192) void verification_hash_kernel(VerifyArgs a) {
         const uint32_t gl = (uint32_t)lane < a.kv_chunks ? (uint32_t)lane : 0u;
         const uint32_t shift = key ? a.head_shift_k : a.head_shift_v;
         const char* base = key ? a.keys + layer * a.layer_stride_bytes_k : a.values + layer * a.layer_stride_bytes_v;
-        load_chunk(base, key ? a.head_stride_bytes_k : a.head_stride_bytes_v, shift, (uint64_t)a.token << shift,
-                   256u * gl, c);
-        if (key) chunk_leaf<KeyChunkDomain>(gl, c, d);
-        else chunk_leaf<ValueChunkDomain>(gl, c, d);
+        const uint64_t hs = key ? a.head_stride_bytes_k : a.head_stride_bytes_v;
+        const uint64_t row_off = (uint64_t)a.token << shift;
+        auto load = [&](int i) {
+            return *reinterpret_cast<const u32x4*>(row_byte(base, hs, shift, row_off, 256u * gl + 16u * i));
+        };
+        if (key) chunk_leaf<KeyChunkDomain>(gl, load, d);
+        else chunk_leaf<ValueChunkDomain>(gl, load, d);
         group_tree(d, lane, (int)a.kv_chunks);
     }
     if (lane == 0 && (wave == 0 || !genesis)) {
