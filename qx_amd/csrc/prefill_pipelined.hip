@@ -80,20 +80,26 @@ struct VtArgs {
     uint32_t kv_len;
 };
 
+// One workgroup of D threads per (tile, kv head).  Thread (half, g, dg) reads
+// the eight positions whose probabilities a lane group leaves in one P^T
+// operand (4g..4g+3 and 16+4g..16+4g+3 of its 32-position half), 8 dims each
+// (one 16-byte load per position, consecutive threads on consecutive dims),
+// transposes the 8 x 8 block of 16-bit values in registers and writes the
+// 8 dims' 16-byte slot groups.
 template <int D, int DT>
-__global__ __launch_bounds__(256) void prefill_vt_kernel(VtArgs a) {
-    constexpr int RB = D * 2 + 16;  // padded LDS row (bytes)
-    __shared__ __attribute__((aligned(16))) char tile[kTile * RB];
+__global__ __launch_bounds__(D) void prefill_vt_kernel(VtArgs a) {
+    constexpr int DG = D / 8;
     const uint32_t t = blockIdx.x, h = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int dg = tid % DG, g = (tid / DG) % 4, half = tid / (DG * 4);
     const char* vbase = reinterpret_cast<const char*>(a.values) + (size_t)h * a.head_stride * 2;
+    u32x4 row[8];
     bool ovf = false;
-    constexpr int CH = kTile * D / 8;
 #pragma unroll
-    for (int c = threadIdx.x; c < CH; c += 256) {
-        const int row = c / (D / 8), col = c % (D / 8);
-        const uint32_t pos = t * kTile + row;
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t pos = t * kTile + 32 * half + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
         const uint32_t src = min(pos, a.kv_len - 1);
-        u32x4 v = *reinterpret_cast<const u32x4*>(vbase + ((size_t)src * D + col * 8) * 2);
+        u32x4 v = *reinterpret_cast<const u32x4*>(vbase + ((size_t)src * D + dg * 8) * 2);
         if constexpr (DT == BF16) {
             // bf16 -> f32 is exact; |x| >= 65520 (or inf / nan) has no finite f16
             u32x4 hv;
@@ -109,27 +115,21 @@ __global__ __launch_bounds__(256) void prefill_vt_kernel(VtArgs a) {
             ovf |= (big != 0) && pos < a.kv_len;
             v = hv;
         }
-        *reinterpret_cast<u32x4*>(&tile[row * RB + col * 16]) = v;
+        row[j] = v;
     }
     ovf = __syncthreads_or(ovf);
-    if (threadIdx.x == 0) a.flags[(size_t)h * a.vt_tiles + t] = ovf ? 1u : 0u;
-    uint16_t* dst = a.vt + ((size_t)h * a.vt_tiles + t) * D * kTile;
+    if (tid == 0) a.flags[(size_t)h * a.vt_tiles + t] = ovf ? 1u : 0u;
+    uint16_t* dst = a.vt + ((size_t)h * a.vt_tiles + t) * D * kTile + 32 * half + 8 * g;
 #pragma unroll
-    for (int c = threadIdx.x; c < D * 8; c += 256) {
-        const int d = c >> 3, ch = c & 7;
-        const int sub = ch >> 2, g = ch & 3;
-        uint32_t w[4];
+    for (int k = 0; k < 8; ++k) {
+        const int w = k >> 1;
+        u32x4 o;
 #pragma unroll
-        for (int j = 0; j < 4; j += 2) {
-            const int r0 = 32 * sub + 4 * g + j;
-            const uint16_t e0 = *reinterpret_cast<const uint16_t*>(&tile[r0 * RB + d * 2]);
-            const uint16_t e1 = *reinterpret_cast<const uint16_t*>(&tile[(r0 + 1) * RB + d * 2]);
-            const uint16_t f0 = *reinterpret_cast<const uint16_t*>(&tile[(r0 + 16) * RB + d * 2]);
-            const uint16_t f1 = *reinterpret_cast<const uint16_t*>(&tile[(r0 + 17) * RB + d * 2]);
-            w[j / 2] = (uint32_t)e0 | ((uint32_t)e1 << 16);
-            w[2 + j / 2] = (uint32_t)f0 | ((uint32_t)f1 << 16);
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t x = row[2 * q][w], y = row[2 * q + 1][w];
+            o[q] = (k & 1) ? (x >> 16) | (y & 0xffff0000u) : (x & 0xffffu) | (y << 16);
         }
-        *reinterpret_cast<u32x4*>(dst + (size_t)d * kTile + ch * 8) = u32x4{w[0], w[1], w[2], w[3]};
+        *reinterpret_cast<u32x4*>(dst + (size_t)(dg * 8 + k) * kTile) = o;
     }
 }
 
@@ -679,11 +679,11 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
     dim3 vgrid(tiles, s.kv_heads);
     const bool bf = dtype == BF16;
     if (s.head_dim == 128) {
-        if (bf) hipLaunchKernelGGL((prefill_vt_kernel<128, BF16>), vgrid, dim3(256), 0, st, va);
-        else hipLaunchKernelGGL((prefill_vt_kernel<128, F16>), vgrid, dim3(256), 0, st, va);
+        if (bf) hipLaunchKernelGGL((prefill_vt_kernel<128, BF16>), vgrid, dim3(128), 0, st, va);
+        else hipLaunchKernelGGL((prefill_vt_kernel<128, F16>), vgrid, dim3(128), 0, st, va);
     } else {
-        if (bf) hipLaunchKernelGGL((prefill_vt_kernel<64, BF16>), vgrid, dim3(256), 0, st, va);
-        else hipLaunchKernelGGL((prefill_vt_kernel<64, F16>), vgrid, dim3(256), 0, st, va);
+        if (bf) hipLaunchKernelGGL((prefill_vt_kernel<64, BF16>), vgrid, dim3(64), 0, st, va);
+        else hipLaunchKernelGGL((prefill_vt_kernel<64, F16>), vgrid, dim3(64), 0, st, va);
     }
 
     PrefillPipeArgs a{};
