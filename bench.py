@@ -130,15 +130,17 @@ def bench_cfg1(ctx, steps, warmup):
     g = rt.Graph(ctx, stream)
     g.capture_begin()
     for p in range(P):
-        rt.rope_kv_batch(g, arena, 0, p, q[p], k[p], v[p], query_out=qo[p])
-        rt.attention(g, arena, 0, qo[p].view(1, 16, 64), p + 1, out=out[p], workspace=ws)
+        # RoPE + append + attention of one token (the reference call site's
+        # encode_rope_kv_for_layer + encode_attention pair) in one dispatch
+        rt.decode_step(g, arena, 0, p, q[p].view(16, 64), k[p].view(8, 64), v[p].view(8, 64),
+                       query_out=qo[p].view(16, 64), out=out[p].view(16, 64), workspace=ws)
     replay = g.capture_end()
     g.discard()
     ms = timed(lambda: replay.launch(stream), steps, warmup, stream)
     total_kv = sum(4096 * (p + 1) for p in range(P))
     return {"us_per_token": ms * 1000.0 / P, "ms_per_512_steps": ms,
             "roofline": roofline_hbm(total_kv / P, ms / P, None),
-            "note": "one token = fused RoPE/append + decode attention (2 launches), HIP-graph replay"}
+            "note": "one token = RoPE + append + decode attention in one launch (qxh_encode_decode_step_for_layer), HIP-graph replay"}
 
 
 # ---------------------------------------------------------------------------

@@ -219,6 +219,21 @@ QXH_API int32_t qxh_encode_rope_kv_for_layer(qxh_graph* graph, qxh_kv_cache* cac
                                      const float* key, const float* value, float* query_output,
                                      uint32_t layer, uint32_t position);
 
+/* One Granite decode step: the work of qxh_encode_rope_kv_for_layer(..., position)
+ * followed by qxh_encode_attention_for_layer(..., length = position + 1) for
+ * sequence 0, the pair GpuRuntimeBuffers::encode_attention_layer_with_plan
+ * issues (crates/qx-runtime-v2/src/lib.rs:6942-6982).  Up to 1024 positions it
+ * is one dispatch (one workgroup per kv head streams the whole context; the
+ * appended row is used from registers); longer contexts take the two-call
+ * path, which needs query_output and a workspace of
+ * qxh_attention_workspace_bytes(cache, 1, position + 1) bytes.  query_output
+ * (rotated q, fp32) may be null on the one-dispatch path and may equal query.
+ * The appended K/V bits equal those of qxh_encode_rope_kv_for_layer. */
+QXH_API int32_t qxh_encode_decode_step_for_layer(qxh_graph* graph, qxh_kv_cache* cache, const float* query,
+                                                 const float* key, const float* value, float* query_output,
+                                                 uint32_t layer, uint32_t position, void* output,
+                                                 int32_t output_dtype, void* workspace, uint64_t workspace_bytes);
+
 /* encode_qwen_store_kv (crates/qx-metal/src/lib.rs:1968-2018): store K/V rows
  * without any transform (keys already normalised and rotated). */
 QXH_API int32_t qxh_encode_store_kv(qxh_graph* graph, qxh_kv_cache* cache, uint32_t layer, uint32_t first_sequence,

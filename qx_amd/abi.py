@@ -102,6 +102,8 @@ SIGNATURES = {
                                                c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_uint64]),
     "qxh_encode_kv_gather_token_rows": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32,
                                                   c_void_p, c_void_p]),
+    "qxh_encode_decode_step_for_layer": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                                   c_uint32, c_uint32, c_void_p, c_int32, c_void_p, c_uint64]),
     "qxh_encode_kv_leaf_hashes": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
                                             c_void_p, c_uint64]),
     "qxh_encode_verification_hashes": (c_int32, [c_void_p, c_void_p, c_uint32, c_void_p, c_uint64, c_uint32,

@@ -79,13 +79,12 @@ def granite_attention_decode(query, key, value, position: int, cache: KvCache):
     """granite_attention_decode (lib.rs:444-452): RoPE q and k, append the
     rotated key and raw value at `position` (which must equal the cache
     length), attend over the cache.  Returns the [1024] output."""
-    q = _dev(query).reshape(1, 1, 16, 64)
-    k = _dev(key).reshape(1, 1, 8, 64)
-    v = _dev(value).reshape(1, 1, 8, 64)
+    q = _dev(query).reshape(16, 64)
+    k = _dev(key).reshape(8, 64)
+    v = _dev(value).reshape(8, 64)
     qo = torch.empty_like(q)
     with rt.Graph(context()) as g:
-        rt.rope_kv_batch(g, cache.arena, 0, position, q, k, v, query_out=qo)
-        out = rt.attention(g, cache.arena, 0, qo.reshape(1, 16, 64), position + 1)
+        out = rt.decode_step(g, cache.arena, 0, position, q, k, v, query_out=qo)
     return out.reshape(-1).cpu().numpy()
 
 

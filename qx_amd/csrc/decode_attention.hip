@@ -18,6 +18,7 @@
 // The kernel is HBM-bound: the algorithmic traffic per launch is the KV
 // bytes of `length` positions per (sequence, kv head) plus q and the output.
 #include "common.h"
+#include "consensus_math.h"
 #include "internal.h"
 #include "mfma.h"
 
@@ -213,6 +214,219 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
                 a.ws_ml[2 * p + 1] = L;
             }
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// One Granite decode step in one dispatch: consensus RoPE of the token's q and
+// k, K/V append at `position`, then attention of the G query heads over
+// positions [0, position].  One workgroup of 16 waves per kv head streams the
+// whole context (no split, no combine), so this is for short contexts, where
+// the three dispatches of the split path cost more than the streaming.  The
+// appended row does not go through memory: the lanes that would hold it in
+// the row loop take it from registers, rounded to the cache dtype exactly as
+// the store rounds it.
+// ---------------------------------------------------------------------------
+struct DecodeStepArgs {
+    const float* query;    // [Hq][D] fp32, this token
+    const float* key;      // [Hkv][D]
+    const float* value;    // [Hkv][D]
+    float* query_out;      // [Hq][D] rotated q (may equal query) or null
+    void* keys;            // layer base of sequence 0 (head-major)
+    void* values;
+    uint64_t head_stride;  // elements
+    void* out;             // [Hq][D]
+    uint32_t position;
+    int out_dtype;
+    float qscale;          // softmax scale * log2(e)
+};
+
+template <int KDT> __device__ __forceinline__ float round_to(float v) {
+    if constexpr (KDT == F16) return (float)(_Float16)v;
+    else if constexpr (KDT == BF16) return __uint_as_float((uint32_t)f32_to_bf16_bits(v) << 16);
+    else return v;
+}
+
+template <int D, int G, int KDT, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs a) {
+    constexpr int EB = Elem<KDT>::bytes;
+    constexpr int EPL = 16 / EB;
+    constexpr int LPR = D / EPL;
+    constexpr int RPW = 64 / LPR;
+    constexpr int UNROLL = 2;
+    constexpr int STEP = RPW * UNROLL;
+    constexpr int P = D / 2;  // rotate-half pairs (i, i + P)
+    static_assert(LPR * EPL == D && RPW * LPR == 64, "row must tile the wave");
+
+    __shared__ float sm_m[WAVES][G];
+    __shared__ float sm_l[WAVES][G];
+    __shared__ float sm_acc[WAVES][G][D];
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int lrow = lane / LPR;
+    const int lcol = (lane % LPR) * EPL;
+    const uint32_t kvh = blockIdx.x;
+    const uint32_t pos = a.position;
+
+    // RoPE once per workgroup, through LDS: 32 threads evaluate the consensus
+    // sin/cos of the pairs; then one thread per element rotates q (G heads) and
+    // k (d < P: fma(-y, s, x c); d >= P: fma(y, c, x s) with x = v[d mod P],
+    // y = v[d mod P + P], granite_rope_pair), rounds k and v to the cache
+    // dtype, and stores the appended row and query_out.
+    __shared__ float sm_sin[P], sm_cos[P];
+    __shared__ float sm_q[G][D], sm_k[D], sm_v[D];
+    const int tid = threadIdx.x;
+    if (tid < P) granite_rope_sin_cos(pos, (uint32_t)tid, sm_sin[tid], sm_cos[tid]);
+    __syncthreads();
+    const size_t head_off = (size_t)kvh * a.head_stride;
+    if (tid < (G + 2) * D) {
+        const int row = tid / D, d = tid % D, i = d % P;
+        const float sn = sm_sin[i], cs = sm_cos[i];
+        if (row < G + 1) {
+            const float* v = row < G ? a.query + ((size_t)kvh * G + row) * D : a.key + (size_t)kvh * D;
+            const float x = v[i], y = v[i + P];
+            const float r = d < P ? __builtin_fmaf(-y, sn, x * cs) : __builtin_fmaf(y, cs, x * sn);
+            if (row < G) sm_q[row][d] = r;
+            else sm_k[d] = round_to<KDT>(r);
+        } else {
+            sm_v[d] = round_to<KDT>(a.value[(size_t)kvh * D + d]);
+        }
+    }
+    __syncthreads();  // every raw q/k/v read is done before query_out (may alias query) is written
+    if (tid < (G + 2) * D) {
+        const int row = tid / D, d = tid % D;
+        if (row < G) {
+            if (a.query_out) a.query_out[((size_t)kvh * G + row) * D + d] = sm_q[row][d];
+        } else if (row == G) {
+            store_any(reinterpret_cast<char*>(a.keys) + (head_off + (size_t)pos * D) * EB, d, sm_k[d], KDT);
+        } else {
+            store_any(reinterpret_cast<char*>(a.values) + (head_off + (size_t)pos * D) * EB, d, sm_v[d], KDT);
+        }
+    }
+    float q[G][EPL], kp[EPL], vp[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) q[g][e] = sm_q[g][lcol + e] * a.qscale;
+        kp[e] = sm_k[lcol + e];
+        vp[e] = sm_v[lcol + e];
+    }
+
+    // rows [0, pos) from the cache, split evenly over the waves
+    const uint32_t wspan = ((pos + WAVES - 1) / WAVES + RPW - 1) / RPW * RPW;
+    const uint32_t w0 = wave * wspan;
+    const uint32_t w1 = min(pos, w0 + wspan);
+    const char* kb = reinterpret_cast<const char*>(a.keys) + head_off * EB;
+    const char* vb = reinterpret_cast<const char*>(a.values) + head_off * EB;
+
+    float m[G], l[G], acc[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = kNegBig;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
+    }
+    for (uint32_t base = w0; base < w1; base += STEP) {
+        u32x4 kr[UNROLL], vr[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const uint32_t row = base + u * RPW + lrow;
+            const uint32_t rc = row < w1 ? row : w1 - 1;
+            kr[u] = load16<false>(kb + ((size_t)rc * D + lcol) * EB);
+            vr[u] = load16<false>(vb + ((size_t)rc * D + lcol) * EB);
+        }
+        float sc[UNROLL][G];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            float kf[EPL];
+            Unpack<KDT>::run(kr[u], kf);
+            const bool valid = base + u * RPW + lrow < w1;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) d = __builtin_fmaf(q[g][e], kf[e], d);
+                d = group_sum<LPR>(d);
+                sc[u][g] = valid ? d : -INFINITY;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float mb = sc[0][g];
+#pragma unroll
+            for (int u = 1; u < UNROLL; ++u) mb = fmaxf(mb, sc[u][g]);
+            const float mn = fmaxf(m[g], mb);
+            const float alpha = fast_exp2(m[g] - mn);
+            m[g] = mn;
+            l[g] *= alpha;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            float vf[EPL];
+            Unpack<KDT>::run(vr[u], vf);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float p = fast_exp2(sc[u][g] - m[g]);
+                l[g] += p;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[g][e] = __builtin_fmaf(p, vf[e], acc[g][e]);
+            }
+        }
+    }
+    // the appended row, on wave 0's first row group (uniform per wave)
+    if (wave == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float d = 0.0f;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) d = __builtin_fmaf(q[g][e], kp[e], d);
+            d = group_sum<LPR>(d);
+            const float sp = lrow == 0 ? d : -INFINITY;
+            const float mn = fmaxf(m[g], sp);
+            const float alpha = fast_exp2(m[g] - mn);
+            const float p = fast_exp2(sp - mn);
+            m[g] = mn;
+            l[g] = __builtin_fmaf(l[g], alpha, p);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[g][e] = __builtin_fmaf(acc[g][e], alpha, p * vp[e]);
+        }
+    }
+
+    if constexpr (LPR <= 1) merge_step<G, EPL, 1>(m, l, acc);
+    if constexpr (LPR <= 2) merge_step<G, EPL, 2>(m, l, acc);
+    if constexpr (LPR <= 4) merge_step<G, EPL, 4>(m, l, acc);
+    if constexpr (LPR <= 8) merge_step<G, EPL, 8>(m, l, acc);
+    if constexpr (LPR <= 16) merge_step<G, EPL, 16>(m, l, acc);
+    if constexpr (LPR <= 32) merge_step<G, EPL, 32>(m, l, acc);
+    if (lrow == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) sm_acc[wave][g][lcol + e] = acc[g][e];
+            if (lcol == 0) {
+                sm_m[wave][g] = m[g];
+                sm_l[wave][g] = l[g];
+            }
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * D; i += 64 * WAVES) {
+        const int g = i / D, d = i % D;
+        float M = kNegBig;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) M = fmaxf(M, sm_m[w][g]);
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float f = fast_exp2(sm_m[w][g] - M);
+            L = __builtin_fmaf(sm_l[w][g], f, L);
+            A = __builtin_fmaf(sm_acc[w][g][d], f, A);
+        }
+        store_any(a.out, ((size_t)kvh * G + g) * D + d, A / L, a.out_dtype);
     }
 }
 
@@ -543,6 +757,30 @@ template <int D, int G, int KDT>
 static void launch_typed(const DecodeArgs& a, dim3 grid, hipStream_t st) {
     hipLaunchKernelGGL((decode_attention_kernel<D, G, KDT, kWaves, kUnroll, true>), grid, dim3(64 * kWaves), 0, st,
                        a);
+}
+
+constexpr int kStepWaves = 16;
+
+hipError_t launch_decode_step(const ShapeDims& s, const KvLayer& kv, const float* query, const float* key,
+                              const float* value, float* query_out, uint32_t position, void* out, int out_dtype,
+                              hipStream_t st) {
+    DecodeStepArgs a{};
+    a.query = query;
+    a.key = key;
+    a.value = value;
+    a.query_out = query_out;
+    a.keys = kv.keys;
+    a.values = kv.values;
+    a.head_stride = kv.head_stride;
+    a.out = out;
+    a.position = position;
+    a.out_dtype = out_dtype;
+    a.qscale = s.scale * kLog2e;
+    const dim3 grid(s.kv_heads), block(64 * kStepWaves);
+    if (kv.key_dtype == F32) hipLaunchKernelGGL((decode_step_kernel<64, 2, F32, kStepWaves>), grid, block, 0, st, a);
+    else if (kv.key_dtype == F16) hipLaunchKernelGGL((decode_step_kernel<64, 2, F16, kStepWaves>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((decode_step_kernel<64, 2, BF16, kStepWaves>), grid, block, 0, st, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t sequences,

@@ -51,6 +51,10 @@ hipError_t launch_qwen_qk_norm_rope(void* q, void* k, const float* qn, const flo
 hipError_t launch_kv_gather(const ShapeDims& s, const KvLayer& kv, uint32_t pos_begin, uint32_t count, void* keys_out,
                             void* values_out, hipStream_t st);
 hipError_t launch_fill_normal(void* data, int dtype, uint64_t count, uint64_t seed, float stddev, hipStream_t st);
+// decode_attention.hip: Granite RoPE + append + attention of one token, one dispatch
+hipError_t launch_decode_step(const ShapeDims& s, const KvLayer& kv, const float* query, const float* key,
+                              const float* value, float* query_out, uint32_t position, void* out, int out_dtype,
+                              hipStream_t st);
 // kv_hash.hip: BLAKE3 commitments of token rows
 hipError_t launch_kv_leaf_hashes(const ShapeDims& s, const KvLayer& kv, uint32_t layer, uint32_t sequences,
                                  uint32_t token_begin, uint32_t count, void* out, hipStream_t st);

@@ -544,6 +544,47 @@ extern "C" int32_t qxh_encode_rope_kv_for_layer(qxh_graph* g, qxh_kv_cache* c, c
                                     query_output, QXH_F32);
 }
 
+// Contexts up to this many positions take the one-dispatch decode step.
+constexpr uint32_t kDecodeStepMaxLength = 1024;
+
+extern "C" int32_t qxh_encode_decode_step_for_layer(qxh_graph* g, qxh_kv_cache* c, const float* query,
+                                                    const float* key, const float* value, float* query_output,
+                                                    uint32_t layer, uint32_t position, void* output,
+                                                    int32_t output_dtype, void* workspace, uint64_t workspace_bytes) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    if ((r = check_range(c, layer, 0, 1))) return r;
+    QXH_REQUIRE(c->desc.shape == QXH_SHAPE_GRANITE, QXH_ERR_INVALID_ARGUMENT,
+                "decode_step is the Granite single-token entry point");
+    QXH_REQUIRE(query && key && value && output, QXH_ERR_INVALID_ARGUMENT, "decode_step: null argument");
+    QXH_REQUIRE(valid_dtype(output_dtype), QXH_ERR_INVALID_ARGUMENT, "decode_step: invalid dtype %d", output_dtype);
+    QXH_REQUIRE(c->desc.key_dtype == c->desc.value_dtype, QXH_ERR_UNSUPPORTED,
+                "decode attention needs equal K and V dtypes");
+    QXH_REQUIRE(position <= 4096, QXH_ERR_INVALID_ARGUMENT, "unregistered Granite RoPE coordinate %u", position);
+    if ((r = check_append(c, layer, 0, 1, position, 1))) return r;
+    const uint32_t length = position + 1;
+    if (length > kDecodeStepMaxLength) {
+        // long context: the two-call path (append, then split-K attention)
+        QXH_REQUIRE(query_output, QXH_ERR_INVALID_ARGUMENT,
+                    "decode_step beyond %u positions needs query_output for the rotated query", kDecodeStepMaxLength);
+        const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, 1, length);
+        QXH_REQUIRE(workspace_bytes >= p.workspace_bytes && (p.workspace_bytes == 0 || workspace),
+                    QXH_ERR_INVALID_ARGUMENT, "decode_step workspace holds %llu bytes, needs %llu",
+                    (unsigned long long)workspace_bytes, (unsigned long long)p.workspace_bytes);
+        if ((r = qxh_encode_rope_kv_batch(g, c, layer, 0, 1, position, 1, query, key, value, QXH_F32, nullptr, nullptr,
+                                          query_output, QXH_F32)))
+            return r;
+        return qxh_encode_attention_for_layer(g, c, layer, 0, 1, length, query_output, QXH_F32, output, output_dtype,
+                                              workspace, workspace_bytes);
+    }
+    hipError_t e = launch_decode_step(c->dims, kv_layer(c, layer, 0), query, key, value, query_output, position, output,
+                                      output_dtype, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "decode step launch");
+    g->dispatches += 1;
+    advance(c, layer, 0, 1, 1);
+    return QXH_OK;
+}
+
 extern "C" int32_t qxh_encode_store_kv(qxh_graph* g, qxh_kv_cache* c, uint32_t layer, uint32_t first, uint32_t count,
                                        uint32_t start, uint32_t tokens, const void* key, const void* value,
                                        int32_t input_dtype) {

@@ -141,8 +141,12 @@ class Replay:
         check(lib().qxh_replay_launch(self._h, ctypes.c_void_p(stream.cuda_stream)))
 
     def __del__(self):
-        if getattr(self, "_h", None):
-            lib().qxh_replay_destroy(self._h)
+        # at interpreter shutdown the module globals may already be gone
+        if getattr(self, "_h", None) and lib is not None:
+            try:
+                lib().qxh_replay_destroy(self._h)
+            except Exception:
+                pass
             self._h = None
 
 
@@ -284,6 +288,25 @@ def attention_workspace_bytes(cache: KvArena, sequences: int, length: int) -> in
     n = ctypes.c_uint64()
     check(lib().qxh_attention_workspace_bytes(cache.handle, sequences, length, ctypes.byref(n)))
     return n.value
+
+
+def decode_step(graph: Graph, cache: KvArena, layer: int, position: int, query, key, value, query_out=None,
+                out=None, out_dtype=None, workspace=None):
+    """RoPE + append + attention of one Granite token (fp32 q [16][64], k/v [8][64])
+    for sequence 0 over positions [0, position]; returns out [16][64]."""
+    if out is None:
+        out = torch.empty((cache.info.q_heads, cache.info.head_dim), dtype=out_dtype or torch.float32,
+                          device=query.device)
+    ws_bytes = 0
+    if workspace is None and position + 1 > 1024:
+        need = attention_workspace_bytes(cache, 1, position + 1)
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=query.device) if need else None
+    if workspace is not None:
+        ws_bytes = workspace.numel() * workspace.element_size()
+    check(lib().qxh_encode_decode_step_for_layer(graph.handle, cache.handle, _ptr(query), _ptr(key), _ptr(value),
+                                                 _ptr(query_out), layer, position, _ptr(out), qxh_dtype(out),
+                                                 _ptr(workspace), ws_bytes))
+    return out
 
 
 def attention(graph: Graph, cache: KvArena, layer: int, query, length: int, out=None, out_dtype=None,

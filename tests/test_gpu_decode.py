@@ -205,3 +205,53 @@ def test_run_qwen_gqa_attention_mirror():
     got = api.run_qwen_gqa_attention(q, kc, vc)
     _, ref = O.qwen_gqa_attention(q, kc, vc, O.F16, want_f32=True)
     assert rel_err(O.from_bits16(got, O.F16), ref) <= TOL_16
+
+
+@pytest.mark.parametrize("kdt,start", [(abi.F32, 0), (abi.F32, 700), (abi.F16, 300), (abi.BF16, 1023),
+                                       (abi.F32, 1500), (abi.F16, 2047)])
+def test_decode_step_matches_the_two_call_path(ctx, kdt, start):
+    """qxh_encode_decode_step_for_layer (one dispatch up to 1024 positions, the
+    two-call path beyond) against qxh_encode_rope_kv_for_layer + attention on
+    a twin cache: bit-identical appended K/V and rotated q, outputs within the
+    dtype's tolerance of each other and of the oracle."""
+    log("decode step", kdt, start)
+    rng = np.random.default_rng(start + 10 * kdt)
+    cap = 2048 + 8
+    a1 = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, cap, kdt)
+    a2 = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, cap, kdt)
+    if start:
+        with rt.Graph(ctx) as g:
+            a1.fill_normal(g, seed=3, length=start)
+            a2.fill_normal(g, seed=3, length=start)
+    tol = TOL_F32 if kdt == abi.F32 else TOL_16
+    for step in range(3):
+        p = start + step
+        q = dev(rng.standard_normal((16, 64), dtype=np.float32))
+        k = dev(rng.standard_normal((8, 64), dtype=np.float32))
+        v = dev(rng.standard_normal((8, 64), dtype=np.float32))
+        qo1 = torch.empty_like(q)
+        qo2 = torch.empty((1, 1, 16, 64), device="cuda:0")
+        with rt.Graph(ctx) as g:
+            out1 = rt.decode_step(g, a1, 0, p, q, k, v, query_out=qo1)
+            rt.rope_kv_batch(g, a2, 0, p, q.view(1, 1, 16, 64), k.view(1, 1, 8, 64), v.view(1, 1, 8, 64),
+                             query_out=qo2)
+            out2 = rt.attention(g, a2, 0, qo2.view(1, 16, 64), p + 1)
+            k1, v1 = a1.gather(g, 0, 0, 0, p + 1)
+            k2, v2 = a2.gather(g, 0, 0, 0, p + 1)
+        assert a1.len() == p + 1
+        assert torch.equal(qo1, qo2.view(16, 64))
+        assert torch.equal(k1, k2) and torch.equal(v1, v2)
+        e = rel_err(out1.cpu().numpy(), out2[0].cpu().numpy())
+        ref = attend64(qo1.cpu().numpy(), k1.float().cpu().numpy(), v1.float().cpu().numpy(), 0.015625)
+        e64 = rel_err(out1.cpu().numpy(), ref)
+        log(f"decode step {kdt} p={p}: vs two-call {e:.2e}, vs float64 {e64:.2e}")
+        assert e <= tol and e64 <= tol
+
+
+def test_decode_step_rejects_out_of_order_positions(ctx):
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, 16, abi.F32)
+    z = torch.zeros((16, 64), device="cuda:0")
+    zk = torch.zeros((8, 64), device="cuda:0")
+    with rt.Graph(ctx) as g:
+        with pytest.raises(abi.QxhError, match="does not follow cache length"):
+            rt.decode_step(g, arena, 0, 1, z, zk, zk)
