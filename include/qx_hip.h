@@ -337,6 +337,70 @@ QXH_API int32_t qxh_encode_granite_attention_block(qxh_graph* graph, qxh_kv_cach
                                            const float* hidden_in, float* hidden_out, void* workspace,
                                            uint64_t workspace_bytes);
 
+/* ---- group-32 Q4 projections -------------------------------------------------
+ * A group-32 Q4 matrix in qx-quant's RowMajor layout (QuantizedTensor,
+ * crates/qx-quant/src/lib.rs:313-360, 707-732): rows x cols, cols a positive
+ * multiple of 32.  `packed` holds rows * cols / 2 bytes: row r's group g of 16
+ * bytes at r*cols/2 + g*16, value i of the group in nibble i%2 (low first) of
+ * byte i/2.  `scales` holds rows * cols / 32 f16 bit patterns, group g of row r
+ * at r*cols/32 + g.  A value decodes to (code - 7) * scale.  `packed` must be
+ * 16-byte aligned and `scales` 2-byte aligned, both in device memory. */
+typedef struct {
+    const uint8_t* packed;
+    const uint16_t* scales;
+    uint32_t rows;
+    uint32_t cols;
+} qxh_q4_matrix;
+
+/* encode_prepared_q4_dense_simd_scaled (crates/qx-metal/src/lib.rs:2655-2736;
+ * kernel qx_q4_dense_simd_gemv, kernels/q4_dense.metal:151-180):
+ * output[r] = (row r . input) * multiplier, each row summed in the order of
+ * QuantizedTensor::mat_vec_simd32 (crates/qx-quant/src/lib.rs:892-938), so the
+ * result is bit-identical to it for multiplier 1.  input [cols] and output
+ * [rows] are fp32 device buffers, 16- and 4-byte aligned, that must not
+ * overlap.  Errors: rows 0, cols not a multiple of 32 or above 65536, null or
+ * misaligned pointers, overlapping input and output. */
+QXH_API int32_t qxh_encode_q4_gemv(qxh_graph* graph, const qxh_q4_matrix* matrix, const float* input, float* output,
+                                   float multiplier);
+
+/* encode_rmsnorm_scalar (crates/qx-metal/src/lib.rs:7777-7810; kernel
+ * qx_v2_rmsnorm_scalar, kernels/v2_decode.metal:105-125): inverse_rms[0] =
+ * rsqrt(sum(x^2) / 1024 + 1e-6) of the 1024-wide fp32 input, with the sum
+ * taken in the 256-thread order of rms_norm_simd
+ * (crates/qx-runtime/src/lib.rs:2416-2432) and the consensus rsqrt: bit-exact. */
+QXH_API int32_t qxh_encode_rms_inverse(qxh_graph* graph, const float* input, float* inverse_rms);
+
+/* ---- Granite attention block with Q4 projections ------------------------------
+ * The attention half of GpuRuntimeBuffers::encode_attention_layer_with_plan
+ * (crates/qx-runtime-v2/src/lib.rs:6890-6994) on the Q4 path:
+ * encode_rmsnorm_scalar + encode_prepared_q4_qkv_simd_normalized
+ * (crates/qx-metal/src/lib.rs:3540-3651), encode_rope_kv_for_layer, attention,
+ * encode_prepared_q4_dense_simd (o projection) and encode_residual_rms_scalar
+ * (crates/qx-metal/src/lib.rs:8867-8916; kernels/q4_dense.metal:24-48):
+ *   hidden_out = fma(0.22, o_proj . attention(rope(q), cache + rope(k), v), hidden_in)
+ * with q, k, v = W . ((hidden_in * inverse) * input_norm).  Norm, projections,
+ * RoPE and the cache rows match the reference bit for bit (V1 `ordered`
+ * profile, crates/qx-runtime/src/lib.rs:847-929); attention and hence
+ * hidden_out match to the fp32 tolerance.  inverse_rms (optional, else NULL)
+ * receives the inverse RMS of hidden_out in rms_norm_simd's order, the value
+ * encode_residual_rms_scalar hands to the router norm.  hidden_in and
+ * hidden_out must be distinct.  The workspace size is
+ * qxh_granite_block_workspace_bytes(cache, position + 1).  Errors as
+ * qxh_encode_granite_attention_block, plus matrix shapes other than
+ * q 1024x1024, k 512x1024, v 512x1024, o 1024x1024 and misaligned weights. */
+typedef struct {
+    const float* input_norm; /* [1024] */
+    qxh_q4_matrix q_proj;
+    qxh_q4_matrix k_proj;
+    qxh_q4_matrix v_proj;
+    qxh_q4_matrix o_proj;
+} qxh_granite_q4_layer_weights;
+
+QXH_API int32_t qxh_encode_granite_attention_block_q4(qxh_graph* graph, qxh_kv_cache* cache, uint32_t layer,
+                                                      uint32_t position, const qxh_granite_q4_layer_weights* weights,
+                                                      const float* hidden_in, float* hidden_out, float* inverse_rms,
+                                                      void* workspace, uint64_t workspace_bytes);
+
 /* ---- synthetic data (bench / tests) ------------------------------------------
  * Counter-based N(0, stddev^2) values (SplitMix64 -> Box-Muller), on device. */
 QXH_API int32_t qxh_encode_fill_normal(qxh_graph* graph, void* data, int32_t dtype, uint64_t count, uint64_t seed,

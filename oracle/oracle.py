@@ -25,6 +25,7 @@ _lib = None
 _f32p = ctypes.POINTER(ctypes.c_float)
 _u16p = ctypes.POINTER(ctypes.c_uint16)
 _u32p = ctypes.POINTER(ctypes.c_uint32)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
 
 
 def build() -> str:
@@ -78,6 +79,17 @@ def lib():
         L.qxo_dense_apply.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, _f32p, _f32p]
         L.qxo_dense_apply.restype = None
         L.qxo_granite_attention_block.argtypes = [_f32p] * 6 + [ctypes.c_uint32, ctypes.c_void_p, _f32p]
+        L.qxo_q4_quantize.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, _u8p, _u16p]
+        L.qxo_q4_dequantize.argtypes = [_u8p, _u16p, ctypes.c_uint32, ctypes.c_uint32, _f32p]
+        L.qxo_q4_dequantize.restype = None
+        L.qxo_q4_mat_vec_simd32.argtypes = [_u8p, _u16p, ctypes.c_uint32, ctypes.c_uint32, _f32p,
+                                            ctypes.c_float, _f32p]
+        L.qxo_granite_rms_norm_simd.argtypes = [_f32p] * 5
+        L.qxo_granite_residual.argtypes = [_f32p, _f32p, _f32p]
+        L.qxo_granite_residual.restype = None
+        L.qxo_granite_attend_simd.argtypes = [_f32p, ctypes.c_void_p, ctypes.c_uint32, _f32p]
+        L.qxo_granite_q4_attention_block.argtypes = ([_f32p, _f32p] + [_u8p, _u16p] * 4
+                                                     + [ctypes.c_uint32, ctypes.c_void_p] + [_f32p] * 4)
         L.qxo_qwen_qk_norm_rope.argtypes = [_u16p, _u16p, _f32p, _f32p, ctypes.c_uint32, ctypes.c_int,
                                             _u16p, _u16p]
         L.qxo_qwen_qk_norm_rope.restype = None
@@ -283,6 +295,96 @@ def granite_attention_block(hidden, norm_weight, wq, wk, wv, wo, position: int, 
     return out
 
 
+# --- group-32 Q4 projections (crates/qx-quant/src/lib.rs) --------------------
+
+class Q4Matrix:
+    """A group-32 Q4 matrix in the reference's RowMajor layout: `packed`
+    uint8 [rows, cols/2] (value i of a group is nibble i%2, low first, of byte
+    i/2) and `scales` f16 bit patterns uint16 [rows, cols/32]."""
+
+    def __init__(self, packed, scales, rows: int, cols: int):
+        self.packed = np.ascontiguousarray(packed, dtype=np.uint8).reshape(rows, cols // 2)
+        self.scales = np.ascontiguousarray(scales, dtype=np.uint16).reshape(rows, cols // 32)
+        self.rows, self.cols = rows, cols
+
+
+def q4_quantize(weight) -> Q4Matrix:
+    """QuantizedTensor::quantize(Q4, group 32), lib.rs:313-360, 1383-1404."""
+    w = _f32(weight)
+    rows, cols = w.shape
+    packed = np.zeros((rows, cols // 2), np.uint8)
+    scales = np.zeros((rows, max(cols // 32, 1)), np.uint16)
+    _check(lib().qxo_q4_quantize(_p(w), rows, cols, _p(packed, _u8p), _p(scales, _u16p)))
+    return Q4Matrix(packed, scales, rows, cols)
+
+
+def q4_dequantize(m: Q4Matrix):
+    """QuantizedTensor::dequantize, lib.rs:819-846."""
+    out = np.zeros((m.rows, m.cols), np.float32)
+    lib().qxo_q4_dequantize(_p(m.packed, _u8p), _p(m.scales, _u16p), m.rows, m.cols, _p(out))
+    return out
+
+
+def q4_mat_vec_simd32(m: Q4Matrix, vector, multiplier: float = 1.0):
+    """QuantizedTensor::mat_vec_simd32, lib.rs:892-938 (times the Metal
+    kernel's multiplier, kernels/q4_dense.metal:151-180)."""
+    x = _f32(vector)
+    out = np.zeros(m.rows, np.float32)
+    _check(lib().qxo_q4_mat_vec_simd32(_p(m.packed, _u8p), _p(m.scales, _u16p), m.rows, m.cols, _p(x),
+                                       float(multiplier), _p(out)))
+    return out
+
+
+def granite_rms_norm_simd(hidden, weight=None):
+    """rms_norm_simd, crates/qx-runtime/src/lib.rs:2416-2432.  Returns
+    (normalized or None, sum of squares, inverse RMS)."""
+    h = _f32(hidden)
+    total, inv = ctypes.c_float(), ctypes.c_float()
+    out = None
+    if weight is not None:
+        w = _f32(weight)
+        out = np.zeros(GRANITE_HIDDEN, np.float32)
+        _check(lib().qxo_granite_rms_norm_simd(_p(h), _p(w), _p(out), ctypes.byref(total), ctypes.byref(inv)))
+    else:
+        _check(lib().qxo_granite_rms_norm_simd(_p(h), None, None, ctypes.byref(total), ctypes.byref(inv)))
+    return out, np.float32(total.value), np.float32(inv.value)
+
+
+def granite_residual(hidden, projection):
+    """fma(0.22, projection, hidden), crates/qx-runtime/src/lib.rs:917-923."""
+    h, pr = _f32(hidden), _f32(projection)
+    out = np.zeros(GRANITE_HIDDEN, np.float32)
+    lib().qxo_granite_residual(_p(h), _p(pr), _p(out))
+    return out
+
+
+def granite_attend_simd(query_rotated, cache: "KvCache", length: int):
+    """Hierarchical attention half of granite_attention_decode_with_profile,
+    crates/qx-runtime/src/lib.rs:476-549 (length <= 512)."""
+    q = _f32(query_rotated)
+    out = np.zeros(GRANITE_HIDDEN, np.float32)
+    _check(lib().qxo_granite_attend_simd(_p(q), cache._h, length, _p(out)))
+    return out
+
+
+def granite_q4_attention_block(hidden, norm_weight, wq: Q4Matrix, wk: Q4Matrix, wv: Q4Matrix, wo: Q4Matrix,
+                               position: int, cache: "KvCache"):
+    """Attention half of the Granite layer with Q4 projections (the V1
+    `ordered` profile, crates/qx-runtime/src/lib.rs:847-929).  Returns
+    (hidden_out, rotated query, attention, inverse RMS of hidden_out)."""
+    h, nw = _f32(hidden), _f32(norm_weight)
+    out = np.zeros(GRANITE_HIDDEN, np.float32)
+    q = np.zeros(GRANITE_HIDDEN, np.float32)
+    att = np.zeros(GRANITE_HIDDEN, np.float32)
+    inv = ctypes.c_float()
+    mats = []
+    for m in (wq, wk, wv, wo):
+        mats += [_p(m.packed, _u8p), _p(m.scales, _u16p)]
+    _check(lib().qxo_granite_q4_attention_block(_p(h), _p(nw), *mats, position, cache._h, _p(out), _p(q),
+                                                _p(att), ctypes.byref(inv)))
+    return out, q, att, np.float32(inv.value)
+
+
 # --- Qwen (tools/qx-qwen-parity/src/main.rs) ---------------------------------
 
 def qwen_qk_norm_rope(query_bits, key_bits, query_norm, key_norm, position: int, fmt: int = F16):
@@ -336,8 +438,6 @@ D_CHECKPOINT = b"QX:CHECKPOINT:V1"
 D_STATE, D_STATE_CHUNK = b"QX:STATE:V1", b"QX:STATE:CHUNK:V1"
 D_KV_KEY_CHUNK, D_KV_KEY_TREE = b"QX:KV:KEY:CHUNK:V1", b"QX:KV:KEY:TREE:V1"
 D_KV_VALUE_CHUNK, D_KV_VALUE_TREE = b"QX:KV:VALUE:CHUNK:V1", b"QX:KV:VALUE:TREE:V1"
-
-_u8p = ctypes.POINTER(ctypes.c_uint8)
 
 
 def _bytes_arg(b: bytes):

@@ -554,3 +554,223 @@ QXO_EXPORT int qxo_granite_prefill_rows(const float* query, qxo_kv_cache* c, uin
     }
     return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Group-32 Q4 weights, crates/qx-quant/src/lib.rs.                          */
+/* RowMajor layout (QuantizedTensor::quantize :313-360, group_location        */
+/* :707-732, packed_len :1147-1152): with cols a multiple of 32, row r's      */
+/* 16-byte group g sits at r*cols/2 + g*16 and its f16 scale at               */
+/* r*(cols/32) + g.  Value i of a group is nibble i%2 (low nibble first) of   */
+/* byte i/2 (pack_scaled :1383-1404, unpack_code :1410-1420); it decodes to   */
+/* (code - 7) * scale (decode_scaled :1472-1486, qmax :139-141).  Groups      */
+/* shorter than 32 (a column count that is not a multiple of 32) are not      */
+/* restated: the GPU layout has none.                                         */
+/* ------------------------------------------------------------------------ */
+
+/* QuantizedTensor::quantize for QuantType::Q4, group_size 32. */
+QXO_EXPORT int qxo_q4_quantize(const float* src, uint32_t rows, uint32_t cols, uint8_t* packed, uint16_t* scales) {
+    if (rows == 0 || cols == 0 || cols % 32) {
+        set_error("Q4 quantize needs rows > 0 and a positive multiple of 32 columns");
+        return 1;
+    }
+    const uint32_t groups = cols / 32;
+    for (uint32_t r = 0; r < rows; ++r) {
+        for (uint32_t g = 0; g < groups; ++g) {
+            const float* v = src + (size_t)r * cols + (size_t)g * 32;
+            float max_abs = 0.0f; /* fold(0.0, f32::max) over |v| */
+            for (int i = 0; i < 32; ++i) max_abs = fmaxf(max_abs, fabsf(v[i]));
+            float scale = max_abs == 0.0f ? 1.0f : max_abs / 7.0f;
+            uint16_t h = qxo_f32_to_f16(scale);
+            scales[(size_t)r * groups + g] = h;
+            float s = qxo_f16_to_f32(h);
+            uint8_t* dst = packed + (size_t)r * (cols / 2) + (size_t)g * 16;
+            memset(dst, 0, 16);
+            for (int i = 0; i < 32; ++i) {
+                /* (value / scale).round().clamp(-7, 7) as i32: round half away
+                 * from zero, NaN stays NaN through clamp and casts to 0. */
+                float q = roundf(v[i] / s);
+                int k;
+                if (q != q) k = 0;
+                else if (q < -7.0f) k = -7;
+                else if (q > 7.0f) k = 7;
+                else k = (int)q;
+                uint8_t code = (uint8_t)(k + 7);
+                dst[i / 2] |= (uint8_t)((code & 0xf) << ((i % 2) * 4));
+            }
+        }
+    }
+    return 0;
+}
+
+/* QuantizedTensor::dequantize (lib.rs:819-846), RowMajor Q4. */
+QXO_EXPORT void qxo_q4_dequantize(const uint8_t* packed, const uint16_t* scales, uint32_t rows, uint32_t cols,
+                                  float* out) {
+    const uint32_t groups = cols / 32;
+    for (uint32_t r = 0; r < rows; ++r)
+        for (uint32_t c = 0; c < cols; ++c) {
+            uint32_t g = c / 32, local = c % 32;
+            uint8_t byte = packed[(size_t)r * (cols / 2) + (size_t)g * 16 + local / 2];
+            uint32_t code = (byte >> ((local % 2) * 4)) & 0xfu;
+            float s = qxo_f16_to_f32(scales[(size_t)r * groups + g]);
+            out[(size_t)r * cols + c] = (float)((int)code - 7) * s;
+        }
+}
+
+/* reduce_simd32: crates/qx-runtime/src/lib.rs:2298-2305 (the same tree as
+ * crates/qx-runtime-v2/src/lib.rs:4946-4953 and qx_ordered_simd_sum,
+ * kernels/q4_dense.metal:6-13). */
+static float reduce_simd32(float* lanes) {
+    static const int offsets[5] = {16, 8, 4, 2, 1};
+    for (int o = 0; o < 5; ++o)
+        for (int lane = 0; lane < offsets[o]; ++lane) lanes[lane] += lanes[lane + offsets[o]];
+    return lanes[0];
+}
+
+/* QuantizedTensor::mat_vec_simd32: crates/qx-quant/src/lib.rs:892-938.  Lane
+ * column % 32 folds its columns in ascending order with fma, then the fixed
+ * 32-lane tree.  `multiplier` is the Metal kernel's final `sum * multiplier`
+ * (qx_q4_dense_simd_gemv, kernels/q4_dense.metal:151-180); 1.0 reproduces the
+ * CPU function exactly. */
+QXO_EXPORT int qxo_q4_mat_vec_simd32(const uint8_t* packed, const uint16_t* scales, uint32_t rows, uint32_t cols,
+                                     const float* input, float multiplier, float* out) {
+    if (cols == 0 || cols % 32) {
+        set_error("Q4 mat_vec needs a positive multiple of 32 columns");
+        return 1;
+    }
+    const uint32_t groups = cols / 32;
+    for (uint32_t r = 0; r < rows; ++r) {
+        float lanes[32] = {0};
+        for (uint32_t c = 0; c < cols; ++c) {
+            uint32_t g = c / 32, local = c % 32;
+            uint8_t byte = packed[(size_t)r * (cols / 2) + (size_t)g * 16 + local / 2];
+            uint32_t code = (byte >> ((local % 2) * 4)) & 0xfu;
+            float value = (float)((int)code - 7) * qxo_f16_to_f32(scales[(size_t)r * groups + g]);
+            lanes[c % 32] = fmaf(value, input[c], lanes[c % 32]);
+        }
+        out[r] = reduce_simd32(lanes) * multiplier;
+    }
+    return 0;
+}
+
+/* rms_norm_simd: crates/qx-runtime/src/lib.rs:2416-2432 (cpu_rms_norm_simd,
+ * crates/qx-runtime-v2/src/lib.rs:4922-4944; the reduction of
+ * qx_v2_rmsnorm_scalar, kernels/v2_decode.metal:105-125, and of
+ * qx_residual_rms_scalar, kernels/q4_dense.metal:24-48).  256 threads each
+ * fold x[t], x[t+256], x[t+512], x[t+768] with fma; threads 32k..32k+31 take
+ * the 32-lane tree; the 8 group sums, padded with zeros, take one more.
+ * Writes the sum of squares to *total and the inverse RMS to *inverse; `out`
+ * (optional) receives x * scale * weight. */
+QXO_EXPORT int qxo_granite_rms_norm_simd(const float* input, const float* weight, float* out, float* total,
+                                         float* inverse) {
+    float threads[256] = {0};
+    for (int tid = 0; tid < 256; ++tid)
+        for (int i = tid; i < G_HIDDEN; i += 256) threads[tid] = fmaf(input[i], input[i], threads[tid]);
+    float groups[32] = {0};
+    for (int group = 0; group < 8; ++group) groups[group] = reduce_simd32(threads + group * 32);
+    float sum = reduce_simd32(groups);
+    float scale;
+    if (qxo_rsqrt_f32(sum / (float)G_HIDDEN + kRmsEpsilon, &scale)) {
+        set_error("positive finite RMS input");
+        return 1;
+    }
+    if (total) *total = sum;
+    if (inverse) *inverse = scale;
+    if (out)
+        for (int i = 0; i < G_HIDDEN; ++i) out[i] = input[i] * scale * weight[i];
+    return 0;
+}
+
+/* The attention half of granite_attention_decode_with_profile(hierarchical =
+ * true), crates/qx-runtime/src/lib.rs:476-549: the normalizer is summed by 256
+ * threads (positions t, t+256, ...) then 8 fixed 32-lane trees and a left
+ * fold; the P.V sum is formed per 32-position chunk (fma in position order)
+ * and the chunk partials are summed in order.  The reference holds 16
+ * partials, so lengths above 512 are rejected, as its slice bound does. */
+QXO_EXPORT int qxo_granite_attend_simd(const float* query, qxo_kv_cache* c, uint32_t length, float* output) {
+    if (length == 0 || length > c->length || length > 512) {
+        set_error("hierarchical attend length outside the committed cache or above 512");
+        return 1;
+    }
+    float exponentials[512];
+    for (int i = 0; i < G_HIDDEN; ++i) output[i] = 0.0f;
+    const int groups = G_QH / G_KVH;
+    for (int qh = 0; qh < G_QH; ++qh) {
+        int kvh = qh / groups;
+        const float* q = query + qh * G_D;
+        for (uint32_t p = 0; p < length; ++p) {
+            const float* k = c->keys + ((size_t)p * G_KVH + kvh) * G_D;
+            float score = 0.0f;
+            for (int d = 0; d < G_D; ++d) score = fmaf(q[d], k[d], score);
+            c->scores[p] = score * kAttentionMultiplier;
+        }
+        float max_score = -INFINITY;
+        for (uint32_t p = 0; p < length; ++p) max_score = fmaxf(max_score, c->scores[p]);
+        for (uint32_t p = 0; p < length; ++p) {
+            if (qxo_exp_f32(c->scores[p] - max_score, &exponentials[p])) {
+                set_error("non-finite model exp input");
+                return 1;
+            }
+        }
+        float threads[256] = {0};
+        for (int tid = 0; tid < 256; ++tid)
+            for (uint32_t p = (uint32_t)tid; p < length; p += 256) threads[tid] += exponentials[p];
+        float normalizer = 0.0f;
+        for (int group = 0; group < 8; ++group) normalizer += reduce_simd32(threads + group * 32);
+        for (uint32_t p = 0; p < length; ++p) c->scores[p] = exponentials[p] / normalizer;
+        float* out = output + qh * G_D;
+        const uint32_t chunks = (length + 31) / 32;
+        for (int d = 0; d < G_D; ++d) {
+            float partials[16] = {0};
+            for (uint32_t chunk = 0; chunk < 16; ++chunk) {
+                uint32_t begin = chunk * 32, end = begin + 32 < length ? begin + 32 : length;
+                for (uint32_t p = begin; p < end; ++p)
+                    partials[chunk] = fmaf(c->scores[p], c->values[((size_t)p * G_KVH + kvh) * G_D + d], partials[chunk]);
+            }
+            float sum = 0.0f;
+            for (uint32_t chunk = 0; chunk < chunks; ++chunk) sum += partials[chunk];
+            out[d] = sum;
+        }
+    }
+    return 0;
+}
+
+/* Attention half of the Granite layer with group-32 Q4 projections: the V1
+ * `ordered` profile (crates/qx-runtime/src/lib.rs:847-929, with
+ * DenseMatrix::from_quantized :580-590 and simd32_dot :2286-2296), which is
+ * also CpuQ4Model::step's attention half (crates/qx-runtime-v2/src/lib.rs:
+ * 4686-4703) with the fma rotation of granite_rope_pair:
+ *   rms_norm_simd -> q/k/v mat_vec_simd32 -> RoPE + append -> attention
+ *   -> o mat_vec_simd32 -> fma(0.22, o, hidden)
+ * and the inverse RMS of the result, which qx_residual_rms_scalar
+ * (kernels/q4_dense.metal:24-48) hands to the router norm.  Attention is the
+ * hierarchical form up to 512 positions (where the reference's ordered
+ * profile stops) and granite_attention_decode beyond.  Optional outputs:
+ * rotated query [1024], attention [1024], inverse RMS. */
+QXO_EXPORT int qxo_granite_q4_attention_block(const float* hidden, const float* norm_weight,
+                                              const uint8_t* qp, const uint16_t* qs, const uint8_t* kp,
+                                              const uint16_t* ks, const uint8_t* vp, const uint16_t* vs,
+                                              const uint8_t* op, const uint16_t* os, uint32_t position,
+                                              qxo_kv_cache* c, float* after_attention, float* query_rotated,
+                                              float* attention, float* inverse_rms) {
+    float normalized[G_HIDDEN], q[G_HIDDEN], k[G_KVW], v[G_KVW], att[G_HIDDEN], proj[G_HIDDEN];
+    if (qxo_granite_rms_norm_simd(hidden, norm_weight, normalized, NULL, NULL)) return 1;
+    qxo_q4_mat_vec_simd32(qp, qs, G_HIDDEN, G_HIDDEN, normalized, 1.0f, q);
+    qxo_q4_mat_vec_simd32(kp, ks, G_KVW, G_HIDDEN, normalized, 1.0f, k);
+    qxo_q4_mat_vec_simd32(vp, vs, G_KVW, G_HIDDEN, normalized, 1.0f, v);
+    if (qxo_apply_granite_rope(q, k, position)) return 1;
+    if (qxo_kv_cache_append(c, position, k, v)) return 1;
+    int bad = c->length <= 512 ? qxo_granite_attend_simd(q, c, c->length, att) : qxo_granite_attend(q, c, c->length, att);
+    if (bad) return 1;
+    qxo_q4_mat_vec_simd32(op, os, G_HIDDEN, G_HIDDEN, att, 1.0f, proj);
+    for (int i = 0; i < G_HIDDEN; ++i) after_attention[i] = fmaf(kResidualMultiplier, proj[i], hidden[i]);
+    if (query_rotated) memcpy(query_rotated, q, sizeof q);
+    if (attention) memcpy(attention, att, sizeof att);
+    if (inverse_rms && qxo_granite_rms_norm_simd(after_attention, NULL, NULL, NULL, inverse_rms)) return 1;
+    return 0;
+}
+
+/* The residual of the attention half, crates/qx-runtime/src/lib.rs:917-923:
+ * after_attention[i] = fma(0.22, projection[i], hidden[i]). */
+QXO_EXPORT void qxo_granite_residual(const float* hidden, const float* projection, float* out) {
+    for (int i = 0; i < G_HIDDEN; ++i) out[i] = fmaf(kResidualMultiplier, projection[i], hidden[i]);
+}

@@ -58,6 +58,15 @@ class GraniteLayerWeights(ctypes.Structure):
                 ("o_proj", c_void_p)]
 
 
+class Q4Matrix(ctypes.Structure):
+    _fields_ = [("packed", c_void_p), ("scales", c_void_p), ("rows", c_uint32), ("cols", c_uint32)]
+
+
+class GraniteQ4LayerWeights(ctypes.Structure):
+    _fields_ = [("input_norm", c_void_p), ("q_proj", Q4Matrix), ("k_proj", Q4Matrix), ("v_proj", Q4Matrix),
+                ("o_proj", Q4Matrix)]
+
+
 # name -> (restype, argtypes); must cover every function of include/qx_hip.h
 SIGNATURES = {
     "qxh_abi_version": (c_int32, []),
@@ -112,6 +121,11 @@ SIGNATURES = {
     "qxh_encode_granite_attention_block": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32,
                                                      P(GraniteLayerWeights), c_void_p, c_void_p, c_void_p,
                                                      c_uint64]),
+    "qxh_encode_q4_gemv": (c_int32, [c_void_p, P(Q4Matrix), c_void_p, c_void_p, c_float]),
+    "qxh_encode_rms_inverse": (c_int32, [c_void_p, c_void_p, c_void_p]),
+    "qxh_encode_granite_attention_block_q4": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32,
+                                                        P(GraniteQ4LayerWeights), c_void_p, c_void_p, c_void_p,
+                                                        c_void_p, c_uint64]),
     "qxh_encode_fill_normal": (c_int32, [c_void_p, c_void_p, c_int32, c_uint64, c_uint64, c_float]),
     "qxh_encode_kv_fill_normal": (c_int32, [c_void_p, c_void_p, c_uint64, c_uint32]),
     "qxh_encode_consensus_conformance": (c_int32, [c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p,

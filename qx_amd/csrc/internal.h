@@ -106,4 +106,32 @@ struct GraniteBlockArgs {
 hipError_t launch_granite_qkv_rope(const ShapeDims& s, const KvLayer& kv, const GraniteBlockArgs& a, hipStream_t st);
 hipError_t launch_granite_out_residual(const GraniteBlockArgs& a, hipStream_t st);
 
+// Group-32 Q4 matrices in qx-quant's RowMajor layout (q4_projection.hip).
+struct Q4View {
+    const uint8_t* packed;    // rows * cols / 2 bytes, 16-byte aligned
+    const uint16_t* scales;   // rows * cols / 32 f16 bit patterns
+};
+struct Q4GemvArgs {
+    const uint8_t* packed;
+    const uint16_t* scales;
+    const float* input;       // [cols]
+    float* output;            // [rows]
+    uint32_t rows;
+    uint32_t cols;            // multiple of 32
+    float multiplier;
+};
+struct GraniteQ4Args {
+    const float* input_norm;
+    Q4View wq, wk, wv, wo;    // 1024x1024, 512x1024, 512x1024, 1024x1024
+    const float* hidden_in;
+    float* hidden_out;
+    float* query_rot;         // workspace [1024]
+    float* attention;         // workspace [1024]
+    uint32_t position;
+};
+hipError_t launch_q4_gemv(const Q4GemvArgs& a, hipStream_t st);
+hipError_t launch_rms_inverse(const float* input, float* inverse, hipStream_t st);
+hipError_t launch_granite_q4_qkv_rope(const KvLayer& kv, const GraniteQ4Args& a, hipStream_t st);
+hipError_t launch_granite_q4_out_residual(const GraniteQ4Args& a, hipStream_t st);
+
 }  // namespace qxh

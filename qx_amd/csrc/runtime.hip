@@ -832,6 +832,111 @@ extern "C" int32_t qxh_encode_granite_attention_block(qxh_graph* g, qxh_kv_cache
     return QXH_OK;
 }
 
+static bool ranges_overlap(const void* a, uint64_t abytes, const void* b, uint64_t bbytes) {
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return x < y + bbytes && y < x + abytes;
+}
+
+static int32_t check_q4(const qxh_q4_matrix& m, uint32_t rows, uint32_t cols, const char* what) {
+    QXH_REQUIRE(m.packed && m.scales, QXH_ERR_INVALID_ARGUMENT, "%s: null Q4 packed codes or scales", what);
+    QXH_REQUIRE(m.rows == rows && m.cols == cols, QXH_ERR_INVALID_ARGUMENT, "%s: Q4 matrix is %ux%u, needs %ux%u",
+                what, m.rows, m.cols, rows, cols);
+    QXH_REQUIRE(((uintptr_t)m.packed & 15) == 0 && ((uintptr_t)m.scales & 1) == 0, QXH_ERR_INVALID_ARGUMENT,
+                "%s: Q4 codes must be 16-byte and scales 2-byte aligned", what);
+    return QXH_OK;
+}
+
+constexpr uint32_t kQ4MaxColumns = 65536;
+
+extern "C" int32_t qxh_encode_q4_gemv(qxh_graph* g, const qxh_q4_matrix* m, const float* input, float* output,
+                                      float multiplier) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    QXH_REQUIRE(m && input && output, QXH_ERR_INVALID_ARGUMENT, "q4_gemv: null argument");
+    QXH_REQUIRE(m->rows > 0, QXH_ERR_INVALID_ARGUMENT, "q4_gemv: empty matrix");
+    QXH_REQUIRE(m->cols > 0 && m->cols % 32 == 0 && m->cols <= kQ4MaxColumns, QXH_ERR_INVALID_ARGUMENT,
+                "q4_gemv: %u columns; needs a positive multiple of 32 up to %u", m->cols, kQ4MaxColumns);
+    if ((r = check_q4(*m, m->rows, m->cols, "q4_gemv"))) return r;
+    QXH_REQUIRE(((uintptr_t)input & 15) == 0 && ((uintptr_t)output & 3) == 0, QXH_ERR_INVALID_ARGUMENT,
+                "q4_gemv: input must be 16-byte and output 4-byte aligned");
+    QXH_REQUIRE(!ranges_overlap(input, (uint64_t)m->cols * 4, output, (uint64_t)m->rows * 4),
+                QXH_ERR_INVALID_ARGUMENT, "q4_gemv: input and output overlap");
+    Q4GemvArgs a{m->packed, m->scales, input, output, m->rows, m->cols, multiplier};
+    hipError_t e = launch_q4_gemv(a, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "q4_gemv launch");
+    g->dispatches += 1;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_encode_rms_inverse(qxh_graph* g, const float* input, float* inverse_rms) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    QXH_REQUIRE(input && inverse_rms, QXH_ERR_INVALID_ARGUMENT, "rms_inverse: null argument");
+    hipError_t e = launch_rms_inverse(input, inverse_rms, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "rms_inverse launch");
+    g->dispatches += 1;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_encode_granite_attention_block_q4(qxh_graph* g, qxh_kv_cache* c, uint32_t layer,
+                                                         uint32_t position, const qxh_granite_q4_layer_weights* w,
+                                                         const float* hidden_in, float* hidden_out,
+                                                         float* inverse_rms, void* workspace,
+                                                         uint64_t workspace_bytes) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    if ((r = check_range(c, layer, 0, 1))) return r;
+    QXH_REQUIRE(c->desc.shape == QXH_SHAPE_GRANITE, QXH_ERR_INVALID_ARGUMENT, "Granite block needs a Granite cache");
+    QXH_REQUIRE(w && w->input_norm, QXH_ERR_INVALID_ARGUMENT, "granite q4 block: null weights or input norm");
+    if ((r = check_q4(w->q_proj, 1024, 1024, "granite q4 block q_proj"))) return r;
+    if ((r = check_q4(w->k_proj, 512, 1024, "granite q4 block k_proj"))) return r;
+    if ((r = check_q4(w->v_proj, 512, 1024, "granite q4 block v_proj"))) return r;
+    if ((r = check_q4(w->o_proj, 1024, 1024, "granite q4 block o_proj"))) return r;
+    QXH_REQUIRE(hidden_in && hidden_out && hidden_in != hidden_out, QXH_ERR_INVALID_ARGUMENT,
+                "granite q4 block: hidden_in and hidden_out must be distinct non-null buffers");
+    QXH_REQUIRE(c->desc.key_dtype == c->desc.value_dtype, QXH_ERR_UNSUPPORTED,
+                "decode attention needs equal K and V dtypes");
+    if ((r = check_append(c, layer, 0, 1, position, 1))) return r;
+    QXH_REQUIRE(position <= 4096, QXH_ERR_INVALID_ARGUMENT, "unregistered Granite RoPE coordinate %u", position);
+    const uint32_t length = position + 1;
+    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, 1, length);
+    const uint64_t need = 2 * 1024 * sizeof(float) + align256(p.workspace_bytes);
+    QXH_REQUIRE(workspace && workspace_bytes >= need, QXH_ERR_INVALID_ARGUMENT,
+                "granite q4 block workspace holds %llu bytes, needs %llu", (unsigned long long)workspace_bytes,
+                (unsigned long long)need);
+    QXH_REQUIRE(((uintptr_t)workspace & 15) == 0, QXH_ERR_INVALID_ARGUMENT,
+                "granite q4 block workspace must be 16-byte aligned");
+    GraniteQ4Args a{};
+    a.input_norm = w->input_norm;
+    a.wq = {w->q_proj.packed, w->q_proj.scales};
+    a.wk = {w->k_proj.packed, w->k_proj.scales};
+    a.wv = {w->v_proj.packed, w->v_proj.scales};
+    a.wo = {w->o_proj.packed, w->o_proj.scales};
+    a.hidden_in = hidden_in;
+    a.hidden_out = hidden_out;
+    a.query_rot = reinterpret_cast<float*>(workspace);
+    a.attention = a.query_rot + 1024;
+    a.position = position;
+    void* attn_ws = reinterpret_cast<char*>(workspace) + 2 * 1024 * sizeof(float);
+    const KvLayer kv = kv_layer(c, layer, 0);
+    hipError_t e = launch_granite_q4_qkv_rope(kv, a, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "granite q4 qkv launch");
+    int dispatches = 0;
+    e = launch_decode_attention(c->dims, kv, p, 1, length, a.query_rot, QXH_F32, a.attention, QXH_F32, attn_ws,
+                                g->stream, &dispatches);
+    if (e != hipSuccess) return hip_fail(e, "granite q4 attention launch");
+    e = launch_granite_q4_out_residual(a, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "granite q4 output launch");
+    g->dispatches += 2 + dispatches;
+    if (inverse_rms) {
+        e = launch_rms_inverse(hidden_out, inverse_rms, g->stream);
+        if (e != hipSuccess) return hip_fail(e, "granite q4 residual rms launch");
+        g->dispatches += 1;
+    }
+    advance(c, layer, 0, 1, 1);
+    return QXH_OK;
+}
+
 extern "C" int32_t qxh_encode_fill_normal(qxh_graph* g, void* data, int32_t dtype, uint64_t count, uint64_t seed,
                                           float stddev) {
     int32_t r = check_graph(g);

@@ -377,6 +377,55 @@ def granite_attention_block(graph: Graph, cache: KvArena, layer: int, position: 
         _ptr(hidden_out), _ptr(workspace), workspace.numel()))
 
 
+class Q4Matrix:
+    """A group-32 Q4 matrix on the device in qx-quant's RowMajor layout
+    (crates/qx-quant/src/lib.rs:313-360): `packed` uint8 [rows, cols/2] and
+    `scales` f16 bit patterns [rows, cols/32] (int16 or uint8 tensors)."""
+
+    def __init__(self, packed, scales, rows: int, cols: int):
+        self.tensors = (packed, scales)
+        self.rows, self.cols = rows, cols
+        self.struct = abi.Q4Matrix(packed.data_ptr(), scales.data_ptr(), rows, cols)
+
+
+def q4_gemv(graph: Graph, matrix: Q4Matrix, vector, out=None, multiplier: float = 1.0):
+    """encode_prepared_q4_dense_simd_scaled (crates/qx-metal/src/lib.rs:2655-2736):
+    out = (matrix . vector) * multiplier in mat_vec_simd32's order."""
+    if out is None:
+        out = torch.empty(matrix.rows, dtype=torch.float32, device=vector.device)
+    check(lib().qxh_encode_q4_gemv(graph.handle, ctypes.byref(matrix.struct), _ptr(vector), _ptr(out),
+                                   float(multiplier)))
+    return out
+
+
+def rms_inverse(graph: Graph, vector, out=None):
+    """encode_rmsnorm_scalar (crates/qx-metal/src/lib.rs:7777-7810): the inverse
+    RMS of a 1024-wide fp32 vector in rms_norm_simd's order."""
+    if out is None:
+        out = torch.empty(1, dtype=torch.float32, device=vector.device)
+    check(lib().qxh_encode_rms_inverse(graph.handle, _ptr(vector), _ptr(out)))
+    return out
+
+
+class GraniteQ4Layer:
+    """Q4 weights of one Granite attention block: fp32 input norm [1024] and
+    Q4Matrix q (1024x1024), k, v (512x1024), o (1024x1024)."""
+
+    def __init__(self, input_norm, q_proj: Q4Matrix, k_proj: Q4Matrix, v_proj: Q4Matrix, o_proj: Q4Matrix):
+        self.tensors = (input_norm, q_proj, k_proj, v_proj, o_proj)
+        self.struct = abi.GraniteQ4LayerWeights(input_norm.data_ptr(), q_proj.struct, k_proj.struct, v_proj.struct,
+                                                o_proj.struct)
+
+
+def granite_attention_block_q4(graph: Graph, cache: KvArena, layer: int, position: int, weights: GraniteQ4Layer,
+                               hidden_in, hidden_out, workspace, inverse_rms=None):
+    """The Q4 attention half of encode_attention_layer_with_plan
+    (crates/qx-runtime-v2/src/lib.rs:6890-6994)."""
+    check(lib().qxh_encode_granite_attention_block_q4(
+        graph.handle, cache.handle, layer, position, ctypes.byref(weights.struct), _ptr(hidden_in),
+        _ptr(hidden_out), None if inverse_rms is None else _ptr(inverse_rms), _ptr(workspace), workspace.numel()))
+
+
 def consensus_conformance(graph: Graph, inputs, coords):
     n = inputs.numel()
     outs = [torch.empty(n, dtype=torch.int32, device=inputs.device) for _ in range(4)]
