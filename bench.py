@@ -144,23 +144,38 @@ def bench_cfg1(ctx, steps, warmup):
 
 
 # ---------------------------------------------------------------------------
-# cfg2: Granite 24-layer attention-only stack at ctx 4096 (fp32)
+# cfg2: Granite 24-layer attention-only stack at ctx 4096 (fp32 KV); fp32
+# dense weights, or (cfg2q4) group-32 Q4 weights
 # ---------------------------------------------------------------------------
-def bench_cfg2(ctx, steps, warmup):
+def bench_cfg2(ctx, steps, warmup, q4=False):
     import torch
     from qx_amd import abi
     from qx_amd import runtime as rt
 
     LAYERS, POS = 24, 4095
     stream = torch.cuda.current_stream()
+    gen = torch.Generator(device="cuda:0")
     sets = []
-    for s in range(2):  # two independent weight+cache sets (705 MB each) so the 256 MB MALL cannot hold a token
+    for s in range(2):  # two independent weight+cache sets so the 256 MB MALL cannot hold a token
         arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, LAYERS, 1, 4096, abi.F32)
         layers = []
         with rt.Graph(ctx, stream) as g:
             arena.fill_normal(g, seed=10 + s, length=POS)
             for layer in range(LAYERS):
                 norm = torch.ones(1024, device="cuda:0")
+                if q4:
+                    # uniform random codes, scales 0.02 / 7 (f16): the weight values
+                    # do not change the work
+                    gen.manual_seed(1000 * s + layer)
+                    mats = []
+                    for rows in (1024, 512, 512, 1024):
+                        codes = torch.randint(0, 256, (rows, 512), dtype=torch.uint8, device="cuda:0",
+                                              generator=gen)
+                        scales = torch.full((rows, 32), 0.02 / 7, dtype=torch.float16,
+                                            device="cuda:0").view(torch.int16)
+                        mats.append(rt.Q4Matrix(codes, scales, rows, 1024))
+                    layers.append(rt.GraniteQ4Layer(norm, *mats))
+                    continue
                 wq = torch.empty((1024, 1024), device="cuda:0")
                 wk = torch.empty((512, 1024), device="cuda:0")
                 wv = torch.empty((512, 1024), device="cuda:0")
@@ -169,16 +184,21 @@ def bench_cfg2(ctx, steps, warmup):
                     rt.fill_normal(g, w, seed=1000 * s + 10 * layer + i, stddev=0.02)
                 layers.append(rt.GraniteLayer(norm, wq, wk, wv, wo))
         hidden = [torch.empty(1024, device="cuda:0") for _ in range(LAYERS + 1)]
+        inv = torch.empty(LAYERS, device="cuda:0")
         with rt.Graph(ctx, stream) as g:
             rt.fill_normal(g, hidden[0], seed=77 + s)
         ws = torch.empty(rt.granite_block_workspace_bytes(arena, POS + 1), dtype=torch.uint8, device="cuda:0")
         g = rt.Graph(ctx, stream)
         g.capture_begin()
         for layer in range(LAYERS):
-            rt.granite_attention_block(g, arena, layer, POS, layers[layer], hidden[layer], hidden[layer + 1], ws)
+            if q4:
+                rt.granite_attention_block_q4(g, arena, layer, POS, layers[layer], hidden[layer], hidden[layer + 1],
+                                              ws, inv[layer:layer + 1])
+            else:
+                rt.granite_attention_block(g, arena, layer, POS, layers[layer], hidden[layer], hidden[layer + 1], ws)
         replay = g.capture_end()
         g.discard()
-        sets.append((arena, layers, hidden, ws, replay))
+        sets.append((arena, layers, hidden, ws, replay, inv))
     it = [0]
 
     def step():
@@ -186,12 +206,19 @@ def bench_cfg2(ctx, steps, warmup):
         it[0] += 1
 
     ms = timed(step, steps, warmup, stream)
-    weights = LAYERS * (1024 * 1024 * 2 + 512 * 1024 * 2) * 4
+    if q4:
+        # codes (rows x 512 B) + f16 scales (rows x 64 B) for q, k, v, o
+        weights = LAYERS * (1024 + 512 + 512 + 1024) * (512 + 64)
+        note = ("24 x (norm+Q4 QKV+RoPE+append, decode attention, Q4 O+residual, residual inverse RMS) per token, "
+                "group-32 Q4 weights (random codes), HIP-graph replay, 2 rotated weight/cache sets; roofline is "
+                "for the whole token")
+    else:
+        weights = LAYERS * (1024 * 1024 * 2 + 512 * 1024 * 2) * 4
+        note = ("24 x (norm+QKV+RoPE+append, decode attention, O+residual) per token, HIP-graph replay, "
+                "2 rotated weight/cache sets; roofline is for the whole token")
     kv = LAYERS * 4096 * 8 * 64 * 4 * 2
     return {"us_per_token": ms * 1000.0, "bytes_per_token": weights + kv,
-            "roofline": roofline_hbm(weights + kv, ms, None),
-            "note": "24 x (norm+QKV+RoPE+append, decode attention, O+residual) per token, HIP-graph replay, "
-                    "2 rotated weight/cache sets; roofline is for the whole token"}
+            "roofline": roofline_hbm(weights + kv, ms, None), "note": note}
 
 
 # ---------------------------------------------------------------------------
@@ -408,7 +435,9 @@ def run(ctx, args):
     if head:
         log("cfg4", json.dumps(head))
     if not args.no_detail:
-        for name, fn in (("cfg1", bench_cfg1), ("cfg2", bench_cfg2), ("cfg3", lambda c, k, w: bench_prefill(c, k, w, "cfg3")),
+        for name, fn in (("cfg1", bench_cfg1), ("cfg2", bench_cfg2),
+                         ("cfg2q4", lambda c, k, w: bench_cfg2(c, k, w, q4=True)),
+                         ("cfg3", lambda c, k, w: bench_prefill(c, k, w, "cfg3")),
                          ("cfg5a", bench_cfg5a), ("cfg5b", lambda c, k, w: bench_prefill(c, k, w, "cfg5b")),
                          ("kvhash", bench_kv_hash)):
             if only and name not in only:

@@ -491,14 +491,14 @@ def verification_hashes(residuals: bytes, residual_stride: int, key_rows, value_
                         interval: int) -> bytes:
     """Per-token digests of kernels/verification_hash.metal:349-522: (layers + 1) x 64 bytes."""
     L = lib()
-    row_bytes = len(key_rows[0])
     kb = [_bytes_arg(r) for r in key_rows]
     vb = [_bytes_arg(r) for r in value_rows]
     kp = (ctypes.POINTER(ctypes.c_uint8) * layers)(*[ctypes.cast(b, _u8p) for b in kb])
     vp = (ctypes.POINTER(ctypes.c_uint8) * layers)(*[ctypes.cast(b, _u8p) for b in vb])
     out = (ctypes.c_uint8 * (64 * (layers + 1)))()
     if L.qxo_verification_hashes(_bytes_arg(residuals), ctypes.c_size_t(residual_stride), kp, vp,
-                                 ctypes.c_size_t(row_bytes), ctypes.c_uint32(token), ctypes.c_uint32(layers),
+                                 ctypes.c_size_t(len(key_rows[0])), ctypes.c_size_t(len(value_rows[0])),
+                                 ctypes.c_uint32(token), ctypes.c_uint32(layers),
                                  ctypes.c_uint32(interval), out) != 0:
         raise RuntimeError("oracle verification hashes: input rejected")
     return bytes(out)

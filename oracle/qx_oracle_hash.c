@@ -203,11 +203,13 @@ QXO_EXPORT int qxo_kv_leaf_hash_v1(uint16_t layer, uint32_t token, const uint8_t
 /* residual snapshot 0, then 32 zero bytes.  p >= 1 (layer p-1): the state   */
 /* root of snapshot p when the layer is a checkpoint ((layer+1) % interval   */
 /* == 0 or the last layer) else 32 zero bytes, then kv_leaf_hash_v1(layer,  */
-/* token, key row, value row).                                               */
+/* token, key row, value row).  K and V rows have their own sizes, as the    */
+/* kernel's per-layer key/value size arrays allow (a KV plan with fp32 K and */
+/* fp16 V, crates/qx-runtime-v2/src/lib.rs:2194-2213).                      */
 /* ------------------------------------------------------------------------ */
 QXO_EXPORT int qxo_verification_hashes(const uint8_t* residuals, size_t residual_stride, const uint8_t* const* key_rows,
-                                       const uint8_t* const* value_rows, size_t row_bytes, uint32_t token,
-                                       uint32_t layers, uint32_t interval, uint8_t* out) {
+                                       const uint8_t* const* value_rows, size_t key_bytes, size_t value_bytes,
+                                       uint32_t token, uint32_t layers, uint32_t interval, uint8_t* out) {
     if (layers == 0 || interval == 0 || interval > layers) return -1;
     for (uint32_t p = 0; p <= layers; ++p) {
         uint8_t* o = out + (size_t)p * 64;
@@ -221,8 +223,8 @@ QXO_EXPORT int qxo_verification_hashes(const uint8_t* residuals, size_t residual
         }
         if (genesis) {
             memset(o + 32, 0, 32);
-        } else if (qxo_kv_leaf_hash_v1((uint16_t)layer, token, key_rows[layer], row_bytes, value_rows[layer], row_bytes,
-                                       o + 32)) {
+        } else if (qxo_kv_leaf_hash_v1((uint16_t)layer, token, key_rows[layer], key_bytes, value_rows[layer],
+                                       value_bytes, o + 32)) {
             return -1;
         }
     }

@@ -39,9 +39,64 @@ struct DecodeArgs {
     int query_dtype;
     int out_dtype;
     float qscale;          // softmax scale * log2(e)
+    // causal rows (VALU kernel only): when set, blockIdx.z is query row t of
+    // one sequence (seq_stride 0) and row t attends [0, min(length, causal_start + t + 1))
+    uint32_t causal;
+    uint32_t causal_start;
 };
 
 constexpr float kNegBig = -1.0e30f;
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <bool NT> __device__ __forceinline__ u32x2 load8(const void* p) {
+    const u32x2* q = reinterpret_cast<const u32x2*>(p);
+    if constexpr (NT) return __builtin_nontemporal_load(q);
+    else return *q;
+}
+
+// N consecutive row elements of dtype DT as raw 32-bit words (8, 16 or 32
+// bytes), loaded ahead of use and widened to fp32 by unpack().  K and V may
+// have different dtypes (KvPrecision Fp32KFp16V / Fp16KFp32V,
+// crates/qx-format/src/lib.rs:136-141); the lane layout follows K, so a V
+// slice is the same N elements in V's width.
+template <int DT, int N> struct RowSlice {
+    static constexpr int W = N * Elem<DT>::bytes / 4;
+    static_assert(W == 2 || W == 4 || W == 8, "8, 16 or 32 bytes per lane");
+    uint32_t w[W];
+    template <bool NT> __device__ __forceinline__ void load(const char* p) {
+        if constexpr (W == 2) {
+            const u32x2 v = load8<NT>(p);
+            w[0] = v[0];
+            w[1] = v[1];
+        } else {
+#pragma unroll
+            for (int c = 0; c < W / 4; ++c) {
+                const u32x4 v = load16<NT>(p + 16 * c);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w[4 * c + j] = v[j];
+            }
+        }
+    }
+    __device__ __forceinline__ void unpack(float (&out)[N]) const {
+        if constexpr (DT == F32) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) out[i] = __uint_as_float(w[i]);
+        } else if constexpr (DT == F16) {
+#pragma unroll
+            for (int i = 0; i < N / 2; ++i) {
+                out[2 * i] = (float)__builtin_bit_cast(half_t, (uint16_t)(w[i] & 0xffffu));
+                out[2 * i + 1] = (float)__builtin_bit_cast(half_t, (uint16_t)(w[i] >> 16));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < N / 2; ++i) {
+                out[2 * i] = __uint_as_float(w[i] << 16);
+                out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+            }
+        }
+    }
+};
 
 template <int MASK> __device__ __forceinline__ float xchg(float v) {
     if constexpr (MASK == 1) return dpp_quad_xor1(v);
@@ -73,9 +128,10 @@ __device__ __forceinline__ void merge_step(float (&m)[G], float (&l)[G], float (
     }
 }
 
-template <int D, int G, int KDT, int WAVES, int UNROLL, bool NT>
+template <int D, int G, int KDT, int VDT, int WAVES, int UNROLL, bool NT>
 __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs a) {
     constexpr int EB = Elem<KDT>::bytes;
+    constexpr int VEB = Elem<VDT>::bytes;
     constexpr int EPL = 16 / EB;
     constexpr int LPR = D / EPL;
     constexpr int RPW = 64 / LPR;
@@ -93,8 +149,9 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
     const uint32_t split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
     const uint32_t hkv = gridDim.y;
 
+    const uint32_t length = a.causal ? min(a.length, a.causal_start + seq + 1) : a.length;
     const uint32_t r0 = split * a.chunk;
-    const uint32_t r1 = min(a.length, r0 + a.chunk);
+    const uint32_t r1 = min(length, r0 + a.chunk);
     const uint32_t span = r1 > r0 ? r1 - r0 : 0u;
     const uint32_t wspan = ((span + WAVES - 1) / WAVES + RPW - 1) / RPW * RPW;
     const uint32_t w0 = r0 + wave * wspan;
@@ -102,7 +159,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
 
     const size_t head_off = (size_t)seq * a.seq_stride + (size_t)kvh * a.head_stride;
     const char* kb = reinterpret_cast<const char*>(a.keys) + head_off * EB;
-    const char* vb = reinterpret_cast<const char*>(a.values) + head_off * EB;
+    const char* vb = reinterpret_cast<const char*>(a.values) + head_off * VEB;
 
     float q[G][EPL];
 #pragma unroll
@@ -122,19 +179,20 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
     }
 
     for (uint32_t base = w0; base < w1; base += STEP) {
-        u32x4 kr[UNROLL], vr[UNROLL];
+        RowSlice<KDT, EPL> kr[UNROLL];
+        RowSlice<VDT, EPL> vr[UNROLL];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
             const uint32_t row = base + u * RPW + lrow;
             const uint32_t rc = row < w1 ? row : w1 - 1;
-            kr[u] = load16<NT>(kb + ((size_t)rc * D + lcol) * EB);
-            vr[u] = load16<NT>(vb + ((size_t)rc * D + lcol) * EB);
+            kr[u].template load<NT>(kb + ((size_t)rc * D + lcol) * EB);
+            vr[u].template load<NT>(vb + ((size_t)rc * D + lcol) * VEB);
         }
         float s[UNROLL][G];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
             float kf[EPL];
-            Unpack<KDT>::run(kr[u], kf);
+            kr[u].unpack(kf);
             const bool valid = base + u * RPW + lrow < w1;
 #pragma unroll
             for (int g = 0; g < G; ++g) {
@@ -160,7 +218,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
             float vf[EPL];
-            Unpack<KDT>::run(vr[u], vf);
+            vr[u].unpack(vf);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 const float p = fast_exp2(s[u][g] - m[g]);
@@ -247,9 +305,10 @@ template <int KDT> __device__ __forceinline__ float round_to(float v) {
     else return v;
 }
 
-template <int D, int G, int KDT, int WAVES>
+template <int D, int G, int KDT, int VDT, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs a) {
     constexpr int EB = Elem<KDT>::bytes;
+    constexpr int VEB = Elem<VDT>::bytes;
     constexpr int EPL = 16 / EB;
     constexpr int LPR = D / EPL;
     constexpr int RPW = 64 / LPR;
@@ -290,7 +349,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs 
             if (row < G) sm_q[row][d] = r;
             else sm_k[d] = round_to<KDT>(r);
         } else {
-            sm_v[d] = round_to<KDT>(a.value[(size_t)kvh * D + d]);
+            sm_v[d] = round_to<VDT>(a.value[(size_t)kvh * D + d]);
         }
     }
     __syncthreads();  // every raw q/k/v read is done before query_out (may alias query) is written
@@ -301,7 +360,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs 
         } else if (row == G) {
             store_any(reinterpret_cast<char*>(a.keys) + (head_off + (size_t)pos * D) * EB, d, sm_k[d], KDT);
         } else {
-            store_any(reinterpret_cast<char*>(a.values) + (head_off + (size_t)pos * D) * EB, d, sm_v[d], KDT);
+            store_any(reinterpret_cast<char*>(a.values) + (head_off + (size_t)pos * D) * VEB, d, sm_v[d], VDT);
         }
     }
     float q[G][EPL], kp[EPL], vp[EPL];
@@ -318,7 +377,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs 
     const uint32_t w0 = wave * wspan;
     const uint32_t w1 = min(pos, w0 + wspan);
     const char* kb = reinterpret_cast<const char*>(a.keys) + head_off * EB;
-    const char* vb = reinterpret_cast<const char*>(a.values) + head_off * EB;
+    const char* vb = reinterpret_cast<const char*>(a.values) + head_off * VEB;
 
     float m[G], l[G], acc[G][EPL];
 #pragma unroll
@@ -329,19 +388,20 @@ __global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs 
         for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
     }
     for (uint32_t base = w0; base < w1; base += STEP) {
-        u32x4 kr[UNROLL], vr[UNROLL];
+        RowSlice<KDT, EPL> kr[UNROLL];
+        RowSlice<VDT, EPL> vr[UNROLL];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
             const uint32_t row = base + u * RPW + lrow;
             const uint32_t rc = row < w1 ? row : w1 - 1;
-            kr[u] = load16<false>(kb + ((size_t)rc * D + lcol) * EB);
-            vr[u] = load16<false>(vb + ((size_t)rc * D + lcol) * EB);
+            kr[u].template load<false>(kb + ((size_t)rc * D + lcol) * EB);
+            vr[u].template load<false>(vb + ((size_t)rc * D + lcol) * VEB);
         }
         float sc[UNROLL][G];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
             float kf[EPL];
-            Unpack<KDT>::run(kr[u], kf);
+            kr[u].unpack(kf);
             const bool valid = base + u * RPW + lrow < w1;
 #pragma unroll
             for (int g = 0; g < G; ++g) {
@@ -367,7 +427,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs 
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
             float vf[EPL];
-            Unpack<KDT>::run(vr[u], vf);
+            vr[u].unpack(vf);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 const float p = fast_exp2(sc[u][g] - m[g]);
@@ -722,22 +782,33 @@ static int rows_per_wave_load(int head_dim, int key_dtype) {
     return 64 / lpr;
 }
 
-DecodePlan plan_decode(const ShapeDims& s, int key_dtype, uint32_t sequences, uint32_t length) {
+// The VALU kernel serves fp32 keys and every mixed K/V pair; equal 16-bit
+// dtypes take the MFMA kernel.
+static bool valu_path(int key_dtype, int value_dtype) { return key_dtype == F32 || key_dtype != value_dtype; }
+
+bool decode_dtypes_supported(const ShapeDims& s, int key_dtype, int value_dtype) {
+    if (key_dtype == value_dtype) return true;
+    // mixed pairs are the Granite KV plans Fp32KFp16V / Fp16KFp32V (and their bf16 twins)
+    return s.head_dim == 64 && s.group == 2 && (key_dtype == F32 || value_dtype == F32);
+}
+
+DecodePlan plan_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t sequences, uint32_t length) {
     DecodePlan p{};
     p.waves = kWaves;
+    const bool valu = valu_path(key_dtype, value_dtype);
     const uint32_t rpw = (uint32_t)rows_per_wave_load(s.head_dim, key_dtype);
     const uint32_t step = rpw * kUnroll;
     const uint32_t units = sequences * (uint32_t)s.kv_heads;
     const uint32_t target_wgs = 2048;
-    // VALU kernel (fp32): keep the (m, l, acc) partial small next to the KV
-    // bytes it summarises; MFMA kernel (16-bit): one 32-position tile per wave
-    uint32_t min_chunk = key_dtype == F32 ? kWaves * step : kWaves * 32;
+    // VALU kernel: keep the (m, l, acc) partial small next to the KV bytes it
+    // summarises; MFMA kernel (16-bit): one 32-position tile per wave
+    uint32_t min_chunk = valu ? kWaves * step : kWaves * 32;
     if (s.group >= 8 && min_chunk < 256) min_chunk = 256;
     uint32_t want = (target_wgs + units - 1) / units;
     uint32_t cap = (length + min_chunk - 1) / min_chunk;
     uint32_t splits = want < cap ? want : cap;
     if (splits < 1) splits = 1;
-    const uint32_t gran = key_dtype == F32 ? kWaves * rpw : kWaves * 32;
+    const uint32_t gran = valu ? kWaves * rpw : kWaves * 32;
     uint32_t chunk = (length + splits - 1) / splits;
     chunk = (chunk + gran - 1) / gran * gran;
     splits = (length + chunk - 1) / chunk;
@@ -753,13 +824,18 @@ DecodePlan plan_decode(const ShapeDims& s, int key_dtype, uint32_t sequences, ui
     return p;
 }
 
-template <int D, int G, int KDT>
-static void launch_typed(const DecodeArgs& a, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL((decode_attention_kernel<D, G, KDT, kWaves, kUnroll, true>), grid, dim3(64 * kWaves), 0, st,
-                       a);
+template <int D, int G, int KDT, int VDT>
+static void launch_valu(const DecodeArgs& a, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL((decode_attention_kernel<D, G, KDT, VDT, kWaves, kUnroll, true>), grid, dim3(64 * kWaves), 0,
+                       st, a);
 }
 
 constexpr int kStepWaves = 16;
+
+template <int KDT, int VDT>
+static void launch_step(const DecodeStepArgs& a, dim3 grid, dim3 block, hipStream_t st) {
+    hipLaunchKernelGGL((decode_step_kernel<64, 2, KDT, VDT, kStepWaves>), grid, block, 0, st, a);
+}
 
 hipError_t launch_decode_step(const ShapeDims& s, const KvLayer& kv, const float* query, const float* key,
                               const float* value, float* query_out, uint32_t position, void* out, int out_dtype,
@@ -777,15 +853,56 @@ hipError_t launch_decode_step(const ShapeDims& s, const KvLayer& kv, const float
     a.out_dtype = out_dtype;
     a.qscale = s.scale * kLog2e;
     const dim3 grid(s.kv_heads), block(64 * kStepWaves);
-    if (kv.key_dtype == F32) hipLaunchKernelGGL((decode_step_kernel<64, 2, F32, kStepWaves>), grid, block, 0, st, a);
-    else if (kv.key_dtype == F16) hipLaunchKernelGGL((decode_step_kernel<64, 2, F16, kStepWaves>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((decode_step_kernel<64, 2, BF16, kStepWaves>), grid, block, 0, st, a);
+    const int kd = kv.key_dtype, vd = kv.value_dtype;
+    if (kd == vd) {
+        if (kd == F32) launch_step<F32, F32>(a, grid, block, st);
+        else if (kd == F16) launch_step<F16, F16>(a, grid, block, st);
+        else launch_step<BF16, BF16>(a, grid, block, st);
+    } else if (kd == F32 && vd == F16) launch_step<F32, F16>(a, grid, block, st);
+    else if (kd == F32 && vd == BF16) launch_step<F32, BF16>(a, grid, block, st);
+    else if (kd == F16 && vd == F32) launch_step<F16, F32>(a, grid, block, st);
+    else if (kd == BF16 && vd == F32) launch_step<BF16, F32>(a, grid, block, st);
+    else return hipErrorNotSupported;
     return hipGetLastError();
 }
 
-hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t sequences,
-                                   uint32_t length, const void* query, int query_dtype, void* out, int out_dtype,
-                                   void* workspace, hipStream_t st, int* dispatches) {
+static hipError_t launch_decode_impl(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, DecodeArgs& a,
+                                     uint32_t units_z, void* workspace, hipStream_t st, int* dispatches) {
+    if (p.splits > 1) {
+        const uint64_t parts = (uint64_t)units_z * s.kv_heads * p.splits * s.group;
+        a.ws_ml = reinterpret_cast<float*>(workspace);
+        a.ws_acc = a.ws_ml + 2 * parts;
+    }
+    const dim3 grid(p.splits, s.kv_heads, units_z);
+    const int kd = kv.key_dtype, vd = kv.value_dtype;
+    const dim3 block(64 * kWaves);
+    if (!decode_dtypes_supported(s, kd, vd)) return hipErrorNotSupported;
+    if (a.causal && !valu_path(kd, vd)) return hipErrorNotSupported;
+    if (s.head_dim == 64 && s.group == 2) {
+        if (kd == vd && kd == F32) launch_valu<64, 2, F32, F32>(a, grid, st);
+        else if (kd == vd && kd == F16) hipLaunchKernelGGL((decode_mfma_kernel<64, 2, F16, kWaves>), grid, block, 0, st, a);
+        else if (kd == vd) hipLaunchKernelGGL((decode_mfma_kernel<64, 2, BF16, kWaves>), grid, block, 0, st, a);
+        else if (kd == F32 && vd == F16) launch_valu<64, 2, F32, F16>(a, grid, st);
+        else if (kd == F32 && vd == BF16) launch_valu<64, 2, F32, BF16>(a, grid, st);
+        else if (kd == F16 && vd == F32) launch_valu<64, 2, F16, F32>(a, grid, st);
+        else launch_valu<64, 2, BF16, F32>(a, grid, st);
+        if (p.splits > 1)
+            hipLaunchKernelGGL((decode_combine_kernel<64, 2>), dim3(s.q_heads * (64 / kCombineDims), units_z), dim3(kCombineThreads), 0, st, a);
+    } else if (s.head_dim == 128 && s.group == 8) {
+        if (kd == F32) launch_valu<128, 8, F32, F32>(a, grid, st);
+        else if (kd == F16) hipLaunchKernelGGL((decode_mfma_kernel<128, 8, F16, kWaves>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((decode_mfma_kernel<128, 8, BF16, kWaves>), grid, block, 0, st, a);
+        if (p.splits > 1)
+            hipLaunchKernelGGL((decode_combine_kernel<128, 8>), dim3(s.q_heads * (128 / kCombineDims), units_z), dim3(kCombineThreads), 0, st, a);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    *dispatches = p.splits > 1 ? 2 : 1;
+    return hipGetLastError();
+}
+
+static DecodeArgs decode_args(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t length,
+                              const void* query, int query_dtype, void* out, int out_dtype) {
     DecodeArgs a{};
     a.keys = kv.keys;
     a.values = kv.values;
@@ -799,31 +916,47 @@ hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const 
     a.query_dtype = query_dtype;
     a.out_dtype = out_dtype;
     a.qscale = s.scale * kLog2e;
-    if (p.splits > 1) {
-        const uint64_t parts = (uint64_t)sequences * s.kv_heads * p.splits * s.group;
-        a.ws_ml = reinterpret_cast<float*>(workspace);
-        a.ws_acc = a.ws_ml + 2 * parts;
-    }
-    dim3 grid(p.splits, s.kv_heads, sequences);
-    const int kd = kv.key_dtype;
-    const dim3 block(64 * kWaves);
-    if (s.head_dim == 64 && s.group == 2) {
-        if (kd == F32) launch_typed<64, 2, F32>(a, grid, st);
-        else if (kd == F16) hipLaunchKernelGGL((decode_mfma_kernel<64, 2, F16, kWaves>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((decode_mfma_kernel<64, 2, BF16, kWaves>), grid, block, 0, st, a);
-        if (p.splits > 1)
-            hipLaunchKernelGGL((decode_combine_kernel<64, 2>), dim3(s.q_heads * (64 / kCombineDims), sequences), dim3(kCombineThreads), 0, st, a);
-    } else if (s.head_dim == 128 && s.group == 8) {
-        if (kd == F32) launch_typed<128, 8, F32>(a, grid, st);
-        else if (kd == F16) hipLaunchKernelGGL((decode_mfma_kernel<128, 8, F16, kWaves>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((decode_mfma_kernel<128, 8, BF16, kWaves>), grid, block, 0, st, a);
-        if (p.splits > 1)
-            hipLaunchKernelGGL((decode_combine_kernel<128, 8>), dim3(s.q_heads * (128 / kCombineDims), sequences), dim3(kCombineThreads), 0, st, a);
-    } else {
-        return hipErrorInvalidValue;
-    }
-    *dispatches = p.splits > 1 ? 2 : 1;
-    return hipGetLastError();
+    return a;
+}
+
+hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t sequences,
+                                   uint32_t length, const void* query, int query_dtype, void* out, int out_dtype,
+                                   void* workspace, hipStream_t st, int* dispatches) {
+    DecodeArgs a = decode_args(s, kv, p, length, query, query_dtype, out, out_dtype);
+    return launch_decode_impl(s, kv, p, a, sequences, workspace, st, dispatches);
+}
+
+DecodePlan plan_decode_causal(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t start, uint32_t tokens) {
+    return plan_decode(s, key_dtype, value_dtype, tokens, start + tokens);
+}
+
+// Workspace that covers plan_decode_causal for every start with
+// start + tokens <= capacity: the split count never exceeds the pre-rounding
+// count min(want, ceil(length / min_chunk)), which grows with the length.
+uint64_t decode_causal_workspace_bound(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t capacity,
+                                       uint32_t tokens) {
+    const DecodePlan p = plan_decode(s, key_dtype, value_dtype, tokens, capacity);
+    const uint32_t units = tokens * (uint32_t)s.kv_heads;
+    const bool valu = valu_path(key_dtype, value_dtype);
+    const uint32_t rpw = (uint32_t)rows_per_wave_load(s.head_dim, key_dtype);
+    uint32_t min_chunk = valu ? kWaves * rpw * kUnroll : kWaves * 32;
+    if (s.group >= 8 && min_chunk < 256) min_chunk = 256;
+    const uint32_t want = (2048 + units - 1) / units;
+    const uint32_t cap = (capacity + min_chunk - 1) / min_chunk;
+    uint32_t bound = want < cap ? want : cap;
+    if (bound > (uint32_t)kMaxSplits) bound = kMaxSplits;
+    if (bound < p.splits) bound = p.splits;
+    return bound > 1 ? (uint64_t)units * bound * s.group * (s.head_dim + 2) * sizeof(float) : 0;
+}
+
+hipError_t launch_decode_causal_rows(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t start,
+                                     uint32_t tokens, const void* query, int query_dtype, void* out, int out_dtype,
+                                     void* workspace, hipStream_t st, int* dispatches) {
+    DecodeArgs a = decode_args(s, kv, p, start + tokens, query, query_dtype, out, out_dtype);
+    a.seq_stride = 0;  // every row reads the one sequence of `kv`
+    a.causal = 1;
+    a.causal_start = start;
+    return launch_decode_impl(s, kv, p, a, tokens, workspace, st, dispatches);
 }
 
 }  // namespace qxh

@@ -74,12 +74,24 @@ struct DecodePlan {
     int waves;              // waves per workgroup
 };
 
-DecodePlan plan_decode(const ShapeDims& s, int key_dtype, uint32_t sequences, uint32_t length);
+// K/V dtype pairs decode attention serves: equal dtypes for every shape;
+// fp32 with a 16-bit partner (the Granite KV plans) for the Granite shape.
+bool decode_dtypes_supported(const ShapeDims& s, int key_dtype, int value_dtype);
+DecodePlan plan_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t sequences, uint32_t length);
 hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t sequences,
                                    uint32_t length, const void* query, int query_dtype, void* out, int out_dtype,
                                    void* workspace, hipStream_t st, int* dispatches);
+// Causal rows on the decode kernels (fp32 or mixed K/V caches): query row t of
+// `tokens` attends positions [0, start + t] of the one sequence of `kv`.
+DecodePlan plan_decode_causal(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t start, uint32_t tokens);
+uint64_t decode_causal_workspace_bound(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t capacity,
+                                       uint32_t tokens);
+hipError_t launch_decode_causal_rows(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t start,
+                                     uint32_t tokens, const void* query, int query_dtype, void* out, int out_dtype,
+                                     void* workspace, hipStream_t st, int* dispatches);
 
-uint64_t prefill_workspace_bytes(const ShapeDims& s, int kv_dtype, uint32_t capacity, uint32_t tokens);
+uint64_t prefill_workspace_bytes(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t capacity,
+                                 uint32_t tokens);
 // pipelined path (prefill_pipelined.hip): V^T pre-pass + pipelined MFMA kernel
 bool prefill_pipe_supported(const ShapeDims& s, uint32_t tokens);
 uint32_t prefill_pipe_vt_tiles(uint32_t capacity);

@@ -287,9 +287,12 @@ __device__ __forceinline__ void store_digest(uint8_t* dst, const uint32_t (&d)[8
 struct KvLeafArgs {
     const char* keys;            // layer base of the first sequence
     const char* values;
-    uint64_t head_stride_bytes;
-    uint64_t seq_stride_bytes;
-    uint32_t head_shift;         // log2(head_dim * element bytes)
+    uint64_t head_stride_bytes_k;
+    uint64_t head_stride_bytes_v;
+    uint64_t seq_stride_bytes_k;
+    uint64_t seq_stride_bytes_v;
+    uint32_t head_shift_k;       // log2(head_dim * element bytes)
+    uint32_t head_shift_v;
     uint32_t token_begin;
     uint32_t count;
     uint32_t sequences;
@@ -309,15 +312,15 @@ __global__ __launch_bounds__(256, 3) void kv_leaf_hash_kernel(KvLeafArgs a) {
     const uint64_t lf = live ? leaf : total - 1;  // spare lanes repeat the last leaf and store nothing
     const uint32_t s = (uint32_t)(lf / a.count), i = (uint32_t)(lf % a.count);
     const uint32_t tok = a.token_begin + i;
-    const uint64_t row_off = (uint64_t)tok << a.head_shift;
-    const char* kb = a.keys + s * a.seq_stride_bytes;
-    const char* vb = a.values + s * a.seq_stride_bytes;
+    const uint64_t row_off = (uint64_t)tok << a.head_shift_k;
+    const char* kb = a.keys + s * a.seq_stride_bytes_k;
+    const char* vb = a.values + s * a.seq_stride_bytes_v;
     uint32_t kd[8], vd[8], node[8], d[8];
     chunk_leaf<KeyChunkDomain>((uint32_t)gl, [&](int i) {
-        return *reinterpret_cast<const u32x4*>(row_byte(kb, a.head_stride_bytes, a.head_shift, row_off, 256u * gl + 16u * i));
+        return *reinterpret_cast<const u32x4*>(row_byte(kb, a.head_stride_bytes_k, a.head_shift_k, row_off, 256u * gl + 16u * i));
     }, kd);
     chunk_leaf<ValueChunkDomain>((uint32_t)gl, [&](int i) {
-        return *reinterpret_cast<const u32x4*>(row_byte(vb, a.head_stride_bytes, a.head_shift, row_off, 256u * gl + 16u * i));
+        return *reinterpret_cast<const u32x4*>(row_byte(vb, a.head_stride_bytes_v, a.head_shift_v, row_off, 256u * gl + 16u * i));
     }, vd);
     kv_roots<CH>(kd, vd, lane, gl, node);
     // lane 0 of the group: key root; lane CH/2: value root
@@ -325,6 +328,39 @@ __global__ __launch_bounds__(256, 3) void kv_leaf_hash_kernel(KvLeafArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) vr[i] = (uint32_t)__shfl((int)node[i], lane - gl + CH / 2);
     kv_leaf(a.layer, tok, node, vr, d);
+    if (live && gl == 0) store_digest(a.out + leaf * 32, d);
+}
+
+// K and V rows of different sizes (KvPrecision Fp32KFp16V / Fp16KFp32V,
+// crates/qx-format/src/lib.rs:136-141): a group of CH = max(CHK, CHV) lanes
+// per leaf; lane c hashes K chunk c (c < CHK) and V chunk c (c < CHV), spare
+// lanes repeat chunk 0, and the two trees reduce separately.
+template <int CHK, int CHV>
+__global__ __launch_bounds__(256, 3) void kv_leaf_hash_mixed_kernel(KvLeafArgs a) {
+    constexpr int CH = CHK > CHV ? CHK : CHV;
+    constexpr int LPW = 64 / CH;
+    const int lane = threadIdx.x & 63;
+    const int gl = lane % CH;
+    const uint64_t total = (uint64_t)a.sequences * a.count;
+    const uint64_t leaf = ((uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * LPW + lane / CH;
+    const bool live = leaf < total;
+    const uint64_t lf = live ? leaf : total - 1;
+    const uint32_t s = (uint32_t)(lf / a.count), i = (uint32_t)(lf % a.count);
+    const uint32_t tok = a.token_begin + i;
+    const char* kb = a.keys + s * a.seq_stride_bytes_k;
+    const char* vb = a.values + s * a.seq_stride_bytes_v;
+    const uint64_t koff = (uint64_t)tok << a.head_shift_k, voff = (uint64_t)tok << a.head_shift_v;
+    const uint32_t ck = gl < CHK ? (uint32_t)gl : 0u, cv = gl < CHV ? (uint32_t)gl : 0u;
+    uint32_t kd[8], vd[8], d[8];
+    chunk_leaf<KeyChunkDomain>(ck, [&](int i) {
+        return *reinterpret_cast<const u32x4*>(row_byte(kb, a.head_stride_bytes_k, a.head_shift_k, koff, 256u * ck + 16u * i));
+    }, kd);
+    chunk_leaf<ValueChunkDomain>(cv, [&](int i) {
+        return *reinterpret_cast<const u32x4*>(row_byte(vb, a.head_stride_bytes_v, a.head_shift_v, voff, 256u * cv + 16u * i));
+    }, vd);
+    group_tree(kd, gl, CHK);
+    group_tree(vd, gl, CHV);
+    kv_leaf(a.layer, tok, kd, vd, d);
     if (live && gl == 0) store_digest(a.out + leaf * 32, d);
 }
 
@@ -343,7 +379,8 @@ struct VerifyArgs {
     uint64_t head_stride_bytes_v;
     uint32_t head_shift_k;
     uint32_t head_shift_v;
-    uint32_t kv_chunks;          // chunks per K (and V) row
+    uint32_t k_chunks;           // chunks per K row
+    uint32_t v_chunks;           // chunks per V row
     uint32_t residual_stride;
     uint32_t state_chunks;
     uint32_t token;
@@ -373,7 +410,8 @@ __global__ __launch_bounds__(192) void verification_hash_kernel(VerifyArgs a) {
         }
     } else if (!genesis) {
         const bool key = wave == 1;
-        const uint32_t gl = (uint32_t)lane < a.kv_chunks ? (uint32_t)lane : 0u;
+        const uint32_t chunks = key ? a.k_chunks : a.v_chunks;
+        const uint32_t gl = (uint32_t)lane < chunks ? (uint32_t)lane : 0u;
         const uint32_t shift = key ? a.head_shift_k : a.head_shift_v;
         const char* base = key ? a.keys + layer * a.layer_stride_bytes_k : a.values + layer * a.layer_stride_bytes_v;
         const uint64_t hs = key ? a.head_stride_bytes_k : a.head_stride_bytes_v;
@@ -383,7 +421,7 @@ __global__ __launch_bounds__(192) void verification_hash_kernel(VerifyArgs a) {
         };
         if (key) chunk_leaf<KeyChunkDomain>(gl, load, d);
         else chunk_leaf<ValueChunkDomain>(gl, load, d);
-        group_tree(d, lane, (int)a.kv_chunks);
+        group_tree(d, lane, (int)chunks);
     }
     if (lane == 0 && (wave == 0 || !genesis)) {
 #pragma unroll
@@ -421,26 +459,32 @@ static uint32_t log2u(uint64_t v) {
 
 hipError_t launch_kv_leaf_hashes(const ShapeDims& s, const KvLayer& kv, uint32_t layer, uint32_t sequences,
                                  uint32_t token_begin, uint32_t count, void* out, hipStream_t st) {
-    const uint32_t eb = kv.key_dtype == F32 ? 4u : 2u;
-    const uint64_t head_bytes = (uint64_t)s.head_dim * eb;
-    const uint64_t row_bytes = head_bytes * s.kv_heads;
+    const uint32_t ebk = kv.key_dtype == F32 ? 4u : 2u, ebv = kv.value_dtype == F32 ? 4u : 2u;
     KvLeafArgs a{};
     a.keys = reinterpret_cast<const char*>(kv.keys);
     a.values = reinterpret_cast<const char*>(kv.values);
-    a.head_stride_bytes = kv.head_stride * eb;
-    a.seq_stride_bytes = kv.sequence_stride * eb;
-    a.head_shift = log2u(head_bytes);
+    a.head_stride_bytes_k = kv.head_stride * ebk;
+    a.head_stride_bytes_v = kv.head_stride * ebv;
+    a.seq_stride_bytes_k = kv.sequence_stride * ebk;
+    a.seq_stride_bytes_v = kv.sequence_stride * ebv;
+    a.head_shift_k = log2u((uint64_t)s.head_dim * ebk);
+    a.head_shift_v = log2u((uint64_t)s.head_dim * ebv);
     a.token_begin = token_begin;
     a.count = count;
     a.sequences = sequences;
     a.layer = layer;
     a.out = reinterpret_cast<uint8_t*>(out);
     const uint64_t leaves = (uint64_t)sequences * count;
-    const uint32_t ch = (uint32_t)(row_bytes / 256);
+    const uint32_t chk = (uint32_t)((uint64_t)s.head_dim * ebk * s.kv_heads / 256);
+    const uint32_t chv = (uint32_t)((uint64_t)s.head_dim * ebv * s.kv_heads / 256);
+    const uint32_t ch = chk > chv ? chk : chv;
     const uint64_t per_block = 4ull * (64 / ch);
     const dim3 grid((uint32_t)((leaves + per_block - 1) / per_block));
-    if (ch == 4) hipLaunchKernelGGL(kv_leaf_hash_kernel<4>, grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(kv_leaf_hash_kernel<8>, grid, dim3(256), 0, st, a);
+    if (chk == 4 && chv == 4) hipLaunchKernelGGL(kv_leaf_hash_kernel<4>, grid, dim3(256), 0, st, a);
+    else if (chk == 8 && chv == 8) hipLaunchKernelGGL(kv_leaf_hash_kernel<8>, grid, dim3(256), 0, st, a);
+    else if (chk == 8 && chv == 4) hipLaunchKernelGGL((kv_leaf_hash_mixed_kernel<8, 4>), grid, dim3(256), 0, st, a);
+    else if (chk == 4 && chv == 8) hipLaunchKernelGGL((kv_leaf_hash_mixed_kernel<4, 8>), grid, dim3(256), 0, st, a);
+    else return hipErrorNotSupported;
     return hipGetLastError();
 }
 
@@ -458,7 +502,8 @@ hipError_t launch_verification_hashes(const ShapeDims& s, const KvLayer& kv0, ui
     a.head_stride_bytes_v = kv0.head_stride * ebv;
     a.head_shift_k = log2u((uint64_t)s.head_dim * ebk);
     a.head_shift_v = log2u((uint64_t)s.head_dim * ebv);
-    a.kv_chunks = (uint32_t)((uint64_t)s.head_dim * ebk * s.kv_heads / 256);
+    a.k_chunks = (uint32_t)((uint64_t)s.head_dim * ebk * s.kv_heads / 256);
+    a.v_chunks = (uint32_t)((uint64_t)s.head_dim * ebv * s.kv_heads / 256);
     a.residual_stride = residual_stride;
     a.state_chunks = residual_stride / 256;
     a.token = token;

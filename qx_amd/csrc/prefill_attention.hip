@@ -414,8 +414,16 @@ __global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a
     }
 }
 
-uint64_t prefill_workspace_bytes(const ShapeDims& s, int kv_dtype, uint32_t capacity, uint32_t tokens) {
-    if (kv_dtype == F32) return 0;
+// fp32 and mixed K/V caches run causal rows on the decode kernels (every query
+// row streams its own prefix: fine for the K <= 4 verifier rows, quadratic in
+// bytes for long prefills); equal 16-bit dtypes take the MFMA prefill.
+static bool prefill_on_decode(const KvLayer& kv) { return kv.key_dtype == F32 || kv.key_dtype != kv.value_dtype; }
+
+uint64_t prefill_workspace_bytes(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t capacity,
+                                 uint32_t tokens) {
+    if (key_dtype == F32 || key_dtype != value_dtype)
+        return decode_causal_workspace_bound(s, key_dtype, value_dtype, capacity, tokens);
+    const int kv_dtype = key_dtype;
     if (prefill_pipe_supported(s, tokens)) return prefill_pipe_workspace_bytes(s, capacity, tokens);
     if (kv_dtype != BF16) return 0;
     const uint32_t qb = s.head_dim == 64 ? (tokens + 127) / 128 : (tokens + 31) / 32;
@@ -426,8 +434,12 @@ hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint3
                                     const void* query, int query_dtype, void* out, int out_dtype, void* workspace,
                                     hipStream_t st, int* dispatches) {
     *dispatches = 0;
-    if (kv.key_dtype != kv.value_dtype || kv.key_dtype != query_dtype || kv.key_dtype == F32)
-        return hipErrorNotSupported;
+    if (prefill_on_decode(kv)) {
+        const DecodePlan p = plan_decode_causal(s, kv.key_dtype, kv.value_dtype, start_position, tokens);
+        return launch_decode_causal_rows(s, kv, p, start_position, tokens, query, query_dtype, out, out_dtype, workspace,
+                                         st, dispatches);
+    }
+    if (kv.key_dtype != query_dtype) return hipErrorNotSupported;
     const bool pp = prefill_pipe_supported(s, tokens);
     if (pp) {
         hipError_t e = launch_prefill_pipe(s, kv, start_position, tokens, query, query_dtype, out, out_dtype, workspace,

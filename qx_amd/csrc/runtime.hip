@@ -558,8 +558,9 @@ extern "C" int32_t qxh_encode_decode_step_for_layer(qxh_graph* g, qxh_kv_cache* 
                 "decode_step is the Granite single-token entry point");
     QXH_REQUIRE(query && key && value && output, QXH_ERR_INVALID_ARGUMENT, "decode_step: null argument");
     QXH_REQUIRE(valid_dtype(output_dtype), QXH_ERR_INVALID_ARGUMENT, "decode_step: invalid dtype %d", output_dtype);
-    QXH_REQUIRE(c->desc.key_dtype == c->desc.value_dtype, QXH_ERR_UNSUPPORTED,
-                "decode attention needs equal K and V dtypes");
+    QXH_REQUIRE(decode_dtypes_supported(c->dims, c->desc.key_dtype, c->desc.value_dtype), QXH_ERR_UNSUPPORTED,
+                "decode attention does not serve K dtype %d with V dtype %d for this shape", c->desc.key_dtype,
+                c->desc.value_dtype);
     QXH_REQUIRE(position <= 4096, QXH_ERR_INVALID_ARGUMENT, "unregistered Granite RoPE coordinate %u", position);
     if ((r = check_append(c, layer, 0, 1, position, 1))) return r;
     const uint32_t length = position + 1;
@@ -567,7 +568,7 @@ extern "C" int32_t qxh_encode_decode_step_for_layer(qxh_graph* g, qxh_kv_cache* 
         // long context: the two-call path (append, then split-K attention)
         QXH_REQUIRE(query_output, QXH_ERR_INVALID_ARGUMENT,
                     "decode_step beyond %u positions needs query_output for the rotated query", kDecodeStepMaxLength);
-        const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, 1, length);
+        const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, c->desc.value_dtype, 1, length);
         QXH_REQUIRE(workspace_bytes >= p.workspace_bytes && (p.workspace_bytes == 0 || workspace),
                     QXH_ERR_INVALID_ARGUMENT, "decode_step workspace holds %llu bytes, needs %llu",
                     (unsigned long long)workspace_bytes, (unsigned long long)p.workspace_bytes);
@@ -628,7 +629,7 @@ extern "C" int32_t qxh_attention_workspace_bytes(const qxh_kv_cache* c, uint32_t
                                                  uint64_t* bytes) {
     QXH_REQUIRE(c && bytes, QXH_ERR_INVALID_ARGUMENT, "attention_workspace_bytes: null argument");
     QXH_REQUIRE(length > 0 && sequences > 0, QXH_ERR_INVALID_ARGUMENT, "empty attention");
-    *bytes = plan_decode(c->dims, c->desc.key_dtype, sequences, length).workspace_bytes;
+    *bytes = plan_decode(c->dims, c->desc.key_dtype, c->desc.value_dtype, sequences, length).workspace_bytes;
     return QXH_OK;
 }
 
@@ -646,9 +647,10 @@ extern "C" int32_t qxh_encode_attention_for_layer(qxh_graph* g, qxh_kv_cache* c,
     for (uint32_t s = first; s < first + count; ++s)
         QXH_REQUIRE(length <= c->at(layer, s), QXH_ERR_KV_POSITION,
                     "attention length %u exceeds committed length %u (sequence %u)", length, c->at(layer, s), s);
-    QXH_REQUIRE(c->desc.key_dtype == c->desc.value_dtype, QXH_ERR_UNSUPPORTED,
-                "decode attention needs equal K and V dtypes (got %d, %d)", c->desc.key_dtype, c->desc.value_dtype);
-    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, count, length);
+    QXH_REQUIRE(decode_dtypes_supported(c->dims, c->desc.key_dtype, c->desc.value_dtype), QXH_ERR_UNSUPPORTED,
+                "decode attention does not serve K dtype %d with V dtype %d for this shape", c->desc.key_dtype,
+                c->desc.value_dtype);
+    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, c->desc.value_dtype, count, length);
     QXH_REQUIRE(workspace_bytes >= p.workspace_bytes && (p.workspace_bytes == 0 || workspace),
                 QXH_ERR_INVALID_ARGUMENT, "attention workspace holds %llu bytes, needs %llu",
                 (unsigned long long)workspace_bytes, (unsigned long long)p.workspace_bytes);
@@ -663,7 +665,7 @@ extern "C" int32_t qxh_encode_attention_for_layer(qxh_graph* g, qxh_kv_cache* c,
 extern "C" int32_t qxh_prefill_workspace_bytes(const qxh_kv_cache* c, uint32_t tokens, uint64_t* bytes) {
     QXH_REQUIRE(c && bytes, QXH_ERR_INVALID_ARGUMENT, "prefill_workspace_bytes: null argument");
     QXH_REQUIRE(tokens > 0, QXH_ERR_INVALID_ARGUMENT, "prefill of zero tokens");
-    *bytes = prefill_workspace_bytes(c->dims, c->desc.key_dtype, c->desc.capacity, tokens);
+    *bytes = prefill_workspace_bytes(c->dims, c->desc.key_dtype, c->desc.value_dtype, c->desc.capacity, tokens);
     return QXH_OK;
 }
 
@@ -681,7 +683,7 @@ extern "C" int32_t qxh_encode_prefill_attention(qxh_graph* g, qxh_kv_cache* c, u
     QXH_REQUIRE((uint64_t)start + tokens <= c->at(layer, seq), QXH_ERR_KV_POSITION,
                 "prefill rows end at %llu beyond committed length %u", (unsigned long long)start + tokens,
                 c->at(layer, seq));
-    const uint64_t need = prefill_workspace_bytes(c->dims, c->desc.key_dtype, c->desc.capacity, tokens);
+    const uint64_t need = prefill_workspace_bytes(c->dims, c->desc.key_dtype, c->desc.value_dtype, c->desc.capacity, tokens);
     QXH_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), QXH_ERR_INVALID_ARGUMENT,
                 "prefill workspace holds %llu bytes, needs %llu", (unsigned long long)workspace_bytes,
                 (unsigned long long)need);
@@ -720,8 +722,6 @@ extern "C" int32_t qxh_encode_kv_leaf_hashes(qxh_graph* g, const qxh_kv_cache* c
     if ((r = check_range(c, layer, first_seq, sequences))) return r;
     QXH_REQUIRE(count > 0, QXH_ERR_INVALID_ARGUMENT, "kv leaf hashes of zero rows");
     QXH_REQUIRE(out, QXH_ERR_INVALID_ARGUMENT, "kv leaf hashes: null output");
-    QXH_REQUIRE(c->desc.key_dtype == c->desc.value_dtype, QXH_ERR_UNSUPPORTED,
-                "kv leaf hashes need equal K and V dtypes");
     QXH_REQUIRE(out_bytes >= (uint64_t)sequences * count * 32, QXH_ERR_INVALID_ARGUMENT,
                 "kv leaf hash output of %llu bytes is smaller than %llu", (unsigned long long)out_bytes,
                 (unsigned long long)sequences * count * 32);
@@ -732,6 +732,8 @@ extern "C" int32_t qxh_encode_kv_leaf_hashes(qxh_graph* g, const qxh_kv_cache* c
     }
     hipError_t e = launch_kv_leaf_hashes(c->dims, kv_layer(c, layer, first_seq), layer, sequences, begin, count, out,
                                          g->stream);
+    if (e == hipErrorNotSupported)
+        return fail(QXH_ERR_UNSUPPORTED, "kv leaf hashes: K or V row is not 1024 or 2048 bytes");
     if (e != hipSuccess) return hip_fail(e, "kv leaf hash launch");
     g->dispatches += 1;
     return QXH_OK;
@@ -757,13 +759,13 @@ extern "C" int32_t qxh_encode_verification_hashes(qxh_graph* g, const qxh_kv_cac
     QXH_REQUIRE(residual_stride % 256 == 0 && chunks >= 1 && chunks <= 64 && (chunks & (chunks - 1)) == 0,
                 QXH_ERR_INVALID_ARGUMENT, "verification residual size %u is not a power-of-two multiple of 256 (<= 64 chunks)",
                 residual_stride);
-    QXH_REQUIRE(c->desc.key_dtype == c->desc.value_dtype, QXH_ERR_UNSUPPORTED,
-                "verification hashes need equal K and V dtypes");
-    const uint64_t row = (uint64_t)c->dims.kv_heads * c->dims.head_dim * dtype_bytes(c->desc.key_dtype);
-    const uint64_t kv_chunks = row / 256;
-    QXH_REQUIRE(row % 256 == 0 && kv_chunks <= 8 && (kv_chunks & (kv_chunks - 1)) == 0, QXH_ERR_UNSUPPORTED,
-                "verification KV row of %llu bytes is not a power-of-two multiple of 256 (<= 8 chunks)",
-                (unsigned long long)row);
+    for (int32_t dt : {c->desc.key_dtype, c->desc.value_dtype}) {
+        const uint64_t row = (uint64_t)c->dims.kv_heads * c->dims.head_dim * dtype_bytes(dt);
+        const uint64_t kv_chunks = row / 256;
+        QXH_REQUIRE(row % 256 == 0 && kv_chunks <= 8 && (kv_chunks & (kv_chunks - 1)) == 0, QXH_ERR_UNSUPPORTED,
+                    "verification KV row of %llu bytes is not a power-of-two multiple of 256 (<= 8 chunks)",
+                    (unsigned long long)row);
+    }
     for (uint32_t l = 0; l < layers; ++l) {
         const uint32_t len = c->cursor[(size_t)l * c->desc.sequences + seq];
         QXH_REQUIRE(token < len, QXH_ERR_KV_POSITION, "verification token %u is outside layer %u's committed length %u",
@@ -780,7 +782,7 @@ extern "C" int32_t qxh_granite_block_workspace_bytes(const qxh_kv_cache* c, uint
     QXH_REQUIRE(c && bytes, QXH_ERR_INVALID_ARGUMENT, "granite_block_workspace_bytes: null argument");
     QXH_REQUIRE(c->desc.shape == QXH_SHAPE_GRANITE, QXH_ERR_INVALID_ARGUMENT, "Granite block needs a Granite cache");
     QXH_REQUIRE(length > 0, QXH_ERR_INVALID_ARGUMENT, "empty attention");
-    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, 1, length);
+    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, c->desc.value_dtype, 1, length);
     *bytes = 2 * 1024 * sizeof(float) + align256(p.workspace_bytes);
     return QXH_OK;
 }
@@ -796,12 +798,13 @@ extern "C" int32_t qxh_encode_granite_attention_block(qxh_graph* g, qxh_kv_cache
                 "granite block: null weight");
     QXH_REQUIRE(hidden_in && hidden_out && hidden_in != hidden_out, QXH_ERR_INVALID_ARGUMENT,
                 "granite block: hidden_in and hidden_out must be distinct non-null buffers");
-    QXH_REQUIRE(c->desc.key_dtype == c->desc.value_dtype, QXH_ERR_UNSUPPORTED,
-                "decode attention needs equal K and V dtypes");
+    QXH_REQUIRE(decode_dtypes_supported(c->dims, c->desc.key_dtype, c->desc.value_dtype), QXH_ERR_UNSUPPORTED,
+                "decode attention does not serve K dtype %d with V dtype %d for this shape", c->desc.key_dtype,
+                c->desc.value_dtype);
     if ((r = check_append(c, layer, 0, 1, position, 1))) return r;
     QXH_REQUIRE(position <= 4096, QXH_ERR_INVALID_ARGUMENT, "unregistered Granite RoPE coordinate %u", position);
     const uint32_t length = position + 1;
-    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, 1, length);
+    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, c->desc.value_dtype, 1, length);
     const uint64_t need = 2 * 1024 * sizeof(float) + align256(p.workspace_bytes);
     QXH_REQUIRE(workspace && workspace_bytes >= need, QXH_ERR_INVALID_ARGUMENT,
                 "granite block workspace holds %llu bytes, needs %llu", (unsigned long long)workspace_bytes,
@@ -894,12 +897,13 @@ extern "C" int32_t qxh_encode_granite_attention_block_q4(qxh_graph* g, qxh_kv_ca
     if ((r = check_q4(w->o_proj, 1024, 1024, "granite q4 block o_proj"))) return r;
     QXH_REQUIRE(hidden_in && hidden_out && hidden_in != hidden_out, QXH_ERR_INVALID_ARGUMENT,
                 "granite q4 block: hidden_in and hidden_out must be distinct non-null buffers");
-    QXH_REQUIRE(c->desc.key_dtype == c->desc.value_dtype, QXH_ERR_UNSUPPORTED,
-                "decode attention needs equal K and V dtypes");
+    QXH_REQUIRE(decode_dtypes_supported(c->dims, c->desc.key_dtype, c->desc.value_dtype), QXH_ERR_UNSUPPORTED,
+                "decode attention does not serve K dtype %d with V dtype %d for this shape", c->desc.key_dtype,
+                c->desc.value_dtype);
     if ((r = check_append(c, layer, 0, 1, position, 1))) return r;
     QXH_REQUIRE(position <= 4096, QXH_ERR_INVALID_ARGUMENT, "unregistered Granite RoPE coordinate %u", position);
     const uint32_t length = position + 1;
-    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, 1, length);
+    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, c->desc.value_dtype, 1, length);
     const uint64_t need = 2 * 1024 * sizeof(float) + align256(p.workspace_bytes);
     QXH_REQUIRE(workspace && workspace_bytes >= need, QXH_ERR_INVALID_ARGUMENT,
                 "granite q4 block workspace holds %llu bytes, needs %llu", (unsigned long long)workspace_bytes,

@@ -162,18 +162,16 @@ def test_bf16_values_outside_f16_range_take_the_exact_pass(ctx, shape):
     assert e <= TOL_16
 
 
-def test_prefill_rejects_rows_beyond_cursor_and_fp32(ctx):
+def test_prefill_rejects_rows_beyond_cursor_and_a_query_dtype_the_mfma_path_lacks(ctx):
     arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, 64, abi.F16)
     arena.set_len(10)
     q = torch.zeros((11, 16, 64), dtype=torch.float16, device="cuda:0")
     with rt.Graph(ctx) as g:
         with pytest.raises(abi.QxhError, match="beyond committed length"):
             rt.prefill_attention(g, arena, 0, 0, q)
-    a32 = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, 64, abi.F32)
-    a32.set_len(10)
-    with rt.Graph(ctx) as g:
+        # 16-bit caches take the MFMA prefill, whose query is the cache dtype
         with pytest.raises(abi.QxhError) as ei:
-            rt.prefill_attention(g, a32, 0, 0, torch.zeros((10, 16, 64), device="cuda:0"))
+            rt.prefill_attention(g, arena, 0, 0, torch.zeros((10, 16, 64), device="cuda:0"))
         assert ei.value.code == abi.QXH_ERR_UNSUPPORTED
 
 
