@@ -17,6 +17,7 @@
 //
 // The kernel is HBM-bound: the algorithmic traffic per launch is the KV
 // bytes of `length` positions per (sequence, kv head) plus q and the output.
+#include "block_merge.h"
 #include "common.h"
 #include "consensus_math.h"
 #include "internal.h"
@@ -924,6 +925,59 @@ hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const 
                                    void* workspace, hipStream_t st, int* dispatches) {
     DecodeArgs a = decode_args(s, kv, p, length, query, query_dtype, out, out_dtype);
     return launch_decode_impl(s, kv, p, a, sequences, workspace, st, dispatches);
+}
+
+// Granite attention block, fp32 and mixed caches: at most 16 splits of 16
+// waves each, so the o-projection kernels can merge the partials themselves
+// (16 x 16 heads x 66 floats = 67 KB at most, read by each of 64
+// workgroups).  Measured at ctx 4096: 32 splits of 8 waves speed the
+// attention up by ~1 us but double the merge's reads, a net loss.
+constexpr int kBlockWaves = 16;
+constexpr uint32_t kBlockMaxSplits = kBlockMergeMaxSplits;  // what the o kernels' merge unrolls
+
+bool block_decode_fused(int key_dtype, int value_dtype) { return valu_path(key_dtype, value_dtype); }
+
+DecodePlan plan_block_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t length) {
+    DecodePlan p{};
+    p.waves = kBlockWaves;
+    const uint32_t gran = kBlockWaves * (uint32_t)rows_per_wave_load(s.head_dim, key_dtype);
+    const uint32_t min_chunk = gran * kUnroll;
+    uint32_t splits = (length + min_chunk - 1) / min_chunk;
+    if (splits > kBlockMaxSplits) splits = kBlockMaxSplits;
+    if (splits < 1) splits = 1;
+    uint32_t chunk = (length + splits - 1) / splits;
+    chunk = (chunk + gran - 1) / gran * gran;
+    splits = (length + chunk - 1) / chunk;
+    p.splits = splits;
+    p.chunk = chunk;
+    p.workspace_bytes = splits > 1 ? (uint64_t)s.kv_heads * splits * s.group * (s.head_dim + 2) * sizeof(float) : 0;
+    (void)value_dtype;
+    return p;
+}
+
+template <int KDT, int VDT>
+static void launch_block_valu(const DecodeArgs& a, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL((decode_attention_kernel<64, 2, KDT, VDT, kBlockWaves, kUnroll, true>), grid,
+                       dim3(64 * kBlockWaves), 0, st, a);
+}
+
+hipError_t launch_block_decode_attention(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t length,
+                                         const float* query, float* out, void* workspace, hipStream_t st) {
+    if (s.head_dim != 64 || s.group != 2 || !valu_path(kv.key_dtype, kv.value_dtype)) return hipErrorNotSupported;
+    DecodeArgs a = decode_args(s, kv, p, length, query, F32, out, F32);
+    if (p.splits > 1) {
+        a.ws_ml = reinterpret_cast<float*>(workspace);
+        a.ws_acc = a.ws_ml + 2 * (uint64_t)s.kv_heads * p.splits * s.group;
+    }
+    const dim3 grid(p.splits, s.kv_heads, 1);
+    const int kd = kv.key_dtype, vd = kv.value_dtype;
+    if (kd == F32 && vd == F32) launch_block_valu<F32, F32>(a, grid, st);
+    else if (kd == F32 && vd == F16) launch_block_valu<F32, F16>(a, grid, st);
+    else if (kd == F32 && vd == BF16) launch_block_valu<F32, BF16>(a, grid, st);
+    else if (kd == F16 && vd == F32) launch_block_valu<F16, F32>(a, grid, st);
+    else if (kd == BF16 && vd == F32) launch_block_valu<BF16, F32>(a, grid, st);
+    else return hipErrorNotSupported;
+    return hipGetLastError();
 }
 
 DecodePlan plan_decode_causal(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t start, uint32_t tokens) {

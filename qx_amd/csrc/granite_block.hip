@@ -11,6 +11,7 @@
 // 1024-wide row and of the normalised input, so no LDS is needed.  In
 // kernel 1 a wave owns the row pair (p, p+32) of one head, so the rotation
 // (fma(-y, s, x*c), fma(y, c, x*s)) happens in registers.
+#include "block_merge.h"
 #include "common.h"
 #include "consensus_math.h"
 #include "internal.h"
@@ -50,16 +51,20 @@ __device__ __forceinline__ void normalize_slices(const float* hidden, const floa
     }
 }
 
-__device__ __forceinline__ float row_dot(const float* row, const f32x4 (&n)[4], int lane) {
-    f32x4 w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = ldg4_nt(row + 256 * i + 4 * lane);
+__device__ __forceinline__ float row_dot_loaded(const f32x4 (&w)[4], const f32x4 (&n)[4]) {
     float d = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int c = 0; c < 4; ++c) d = __builtin_fmaf(w[i][c], n[i][c], d);
     return group_sum<64>(d);
+}
+
+__device__ __forceinline__ float row_dot(const float* row, const f32x4 (&n)[4], int lane) {
+    f32x4 w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = ldg4_nt(row + 256 * i + 4 * lane);
+    return row_dot_loaded(w, n);
 }
 
 // grid 256 workgroups x 4 waves.  Workgroup b: head block hb = b / 8 (0-15 q,
@@ -114,6 +119,41 @@ __global__ __launch_bounds__(256) void granite_out_residual_kernel(GraniteBlockA
     for (int i = 0; i < 4; ++i) n[i] = ldg4(a.attention + 256 * i + 4 * lane);
     const float proj = row_dot(a.wo + (size_t)row * kHidden, n, lane);
     if (lane == 0) a.hidden_out[row] = __builtin_fmaf(kResidual, proj, a.hidden_in[row]);
+}
+
+// fp32 and mixed caches: the attention launch left split partials; every
+// workgroup merges them (block_merge.h) before its rows.  grid 64 workgroups
+// x 4 waves, wave w of workgroup b owns rows 16 b + 4 w .. + 3; its weights
+// are requested before the merge so the two latencies overlap.
+__global__ __launch_bounds__(256) void granite_out_merge_residual_kernel(GraniteBlockArgs a) {
+    __shared__ __attribute__((aligned(16))) float s_att[kHidden];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row0 = blockIdx.x * 16 + wave * 4;
+    f32x4 w[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[r][i] = ldg4_nt(a.wo + (size_t)(row0 + r) * kHidden + 256 * i + 4 * lane);
+    const float resid = lane < 4 ? a.hidden_in[row0 + lane] : 0.0f;
+    merge_granite_attention(a.parts.ml, a.parts.acc, a.parts.splits, a.attention, s_att);
+    __syncthreads();
+    if (blockIdx.x == 0 && a.parts.splits > 1)
+        for (int o = threadIdx.x; o < kHidden; o += 256) a.attention[o] = s_att[o];
+    f32x4 n[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) n[i] = *reinterpret_cast<const f32x4*>(s_att + 256 * i + 4 * lane);
+    float out[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out[r] = row_dot_loaded(w[r], n);
+    if (lane < 4) {
+        const float proj = lane == 0 ? out[0] : lane == 1 ? out[1] : lane == 2 ? out[2] : out[3];
+        a.hidden_out[row0 + lane] = __builtin_fmaf(kResidual, proj, resid);
+    }
+}
+
+hipError_t launch_granite_out_merge_residual(const GraniteBlockArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL(granite_out_merge_residual_kernel, dim3(kHidden / 16), dim3(256), 0, st, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_granite_qkv_rope(const ShapeDims& s, const KvLayer& kv, const GraniteBlockArgs& a, hipStream_t st) {

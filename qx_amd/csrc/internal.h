@@ -92,6 +92,12 @@ hipError_t launch_decode_causal_rows(const ShapeDims& s, const KvLayer& kv, cons
 
 uint64_t prefill_workspace_bytes(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t capacity,
                                  uint32_t tokens);
+// Granite attention block on fp32 / mixed caches: split-K attention with at
+// most 16 splits whose partials the o-projection kernel merges (block_merge.h).
+bool block_decode_fused(int key_dtype, int value_dtype);
+DecodePlan plan_block_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t length);
+hipError_t launch_block_decode_attention(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t length,
+                                         const float* query, float* out, void* workspace, hipStream_t st);
 // pipelined path (prefill_pipelined.hip): V^T pre-pass + pipelined MFMA kernel
 bool prefill_pipe_supported(const ShapeDims& s, uint32_t tokens);
 uint32_t prefill_pipe_vt_tiles(uint32_t capacity);
@@ -103,6 +109,13 @@ hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint3
                                     hipStream_t st, int* dispatches);
 
 // Granite attention block (fp32 dense weights).
+// Split partials of the block's attention launch for the merging o kernels.
+struct BlockPartials {
+    const float* ml;      // [Hkv][splits][2][2] (m, l)
+    const float* acc;     // [Hkv][splits][2][64]
+    uint32_t splits;      // 1: the attention output is already in `attention`
+};
+
 struct GraniteBlockArgs {
     const float* input_norm;
     const float* wq;
@@ -114,9 +127,11 @@ struct GraniteBlockArgs {
     float* query_rot;   // workspace [1024]
     float* attention;   // workspace [1024]
     uint32_t position;
+    BlockPartials parts;
 };
 hipError_t launch_granite_qkv_rope(const ShapeDims& s, const KvLayer& kv, const GraniteBlockArgs& a, hipStream_t st);
 hipError_t launch_granite_out_residual(const GraniteBlockArgs& a, hipStream_t st);
+hipError_t launch_granite_out_merge_residual(const GraniteBlockArgs& a, hipStream_t st);
 
 // Group-32 Q4 matrices in qx-quant's RowMajor layout (q4_projection.hip).
 struct Q4View {
@@ -140,10 +155,12 @@ struct GraniteQ4Args {
     float* query_rot;         // workspace [1024]
     float* attention;         // workspace [1024]
     uint32_t position;
+    BlockPartials parts;
 };
 hipError_t launch_q4_gemv(const Q4GemvArgs& a, hipStream_t st);
 hipError_t launch_rms_inverse(const float* input, float* inverse, hipStream_t st);
 hipError_t launch_granite_q4_qkv_rope(const KvLayer& kv, const GraniteQ4Args& a, hipStream_t st);
 hipError_t launch_granite_q4_out_residual(const GraniteQ4Args& a, hipStream_t st);
+hipError_t launch_granite_q4_out_merge_residual(const GraniteQ4Args& a, hipStream_t st);
 
 }  // namespace qxh

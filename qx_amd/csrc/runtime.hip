@@ -778,12 +778,48 @@ extern "C" int32_t qxh_encode_verification_hashes(qxh_graph* g, const qxh_kv_cac
     return QXH_OK;
 }
 
+// Attention inside the Granite blocks.  fp32 and mixed caches: at most 16
+// splits whose partials the o-projection kernel merges (no combine dispatch);
+// 16-bit caches: the split-K MFMA kernel and its combine.
+struct BlockAttention {
+    DecodePlan plan;
+    bool fused;
+};
+
+static BlockAttention block_attention_plan(const qxh_kv_cache* c, uint32_t length) {
+    BlockAttention b{};
+    const int kd = c->desc.key_dtype, vd = c->desc.value_dtype;
+    b.fused = block_decode_fused(kd, vd);
+    b.plan = b.fused ? plan_block_decode(c->dims, kd, vd, length) : plan_decode(c->dims, kd, vd, 1, length);
+    return b;
+}
+
+static uint64_t block_workspace_bytes(const BlockAttention& b) {
+    return 2 * 1024 * sizeof(float) + align256(b.plan.workspace_bytes);
+}
+
+// Launches the attention of a block; `parts` tells the o kernel where the
+// partials are when the merge is fused.
+static hipError_t launch_block_attention(const qxh_kv_cache* c, const KvLayer& kv, const BlockAttention& b,
+                                         uint32_t length, const float* query, float* attention, void* ws,
+                                         hipStream_t st, int* dispatches, BlockPartials* parts) {
+    if (b.fused) {
+        *dispatches = 1;
+        parts->splits = b.plan.splits;
+        parts->ml = reinterpret_cast<const float*>(ws);
+        parts->acc = parts->ml + 2 * (uint64_t)c->dims.kv_heads * b.plan.splits * c->dims.group;
+        return launch_block_decode_attention(c->dims, kv, b.plan, length, query, attention, ws, st);
+    }
+    parts->splits = 0;
+    return launch_decode_attention(c->dims, kv, b.plan, 1, length, query, QXH_F32, attention, QXH_F32, ws, st,
+                                   dispatches);
+}
+
 extern "C" int32_t qxh_granite_block_workspace_bytes(const qxh_kv_cache* c, uint32_t length, uint64_t* bytes) {
     QXH_REQUIRE(c && bytes, QXH_ERR_INVALID_ARGUMENT, "granite_block_workspace_bytes: null argument");
     QXH_REQUIRE(c->desc.shape == QXH_SHAPE_GRANITE, QXH_ERR_INVALID_ARGUMENT, "Granite block needs a Granite cache");
     QXH_REQUIRE(length > 0, QXH_ERR_INVALID_ARGUMENT, "empty attention");
-    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, c->desc.value_dtype, 1, length);
-    *bytes = 2 * 1024 * sizeof(float) + align256(p.workspace_bytes);
+    *bytes = block_workspace_bytes(block_attention_plan(c, length));
     return QXH_OK;
 }
 
@@ -804,8 +840,8 @@ extern "C" int32_t qxh_encode_granite_attention_block(qxh_graph* g, qxh_kv_cache
     if ((r = check_append(c, layer, 0, 1, position, 1))) return r;
     QXH_REQUIRE(position <= 4096, QXH_ERR_INVALID_ARGUMENT, "unregistered Granite RoPE coordinate %u", position);
     const uint32_t length = position + 1;
-    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, c->desc.value_dtype, 1, length);
-    const uint64_t need = 2 * 1024 * sizeof(float) + align256(p.workspace_bytes);
+    const BlockAttention b = block_attention_plan(c, length);
+    const uint64_t need = block_workspace_bytes(b);
     QXH_REQUIRE(workspace && workspace_bytes >= need, QXH_ERR_INVALID_ARGUMENT,
                 "granite block workspace holds %llu bytes, needs %llu", (unsigned long long)workspace_bytes,
                 (unsigned long long)need);
@@ -825,10 +861,9 @@ extern "C" int32_t qxh_encode_granite_attention_block(qxh_graph* g, qxh_kv_cache
     hipError_t e = launch_granite_qkv_rope(c->dims, kv, a, g->stream);
     if (e != hipSuccess) return hip_fail(e, "granite qkv launch");
     int dispatches = 0;
-    e = launch_decode_attention(c->dims, kv, p, 1, length, a.query_rot, QXH_F32, a.attention, QXH_F32, attn_ws,
-                                g->stream, &dispatches);
+    e = launch_block_attention(c, kv, b, length, a.query_rot, a.attention, attn_ws, g->stream, &dispatches, &a.parts);
     if (e != hipSuccess) return hip_fail(e, "granite attention launch");
-    e = launch_granite_out_residual(a, g->stream);
+    e = b.fused ? launch_granite_out_merge_residual(a, g->stream) : launch_granite_out_residual(a, g->stream);
     if (e != hipSuccess) return hip_fail(e, "granite output launch");
     g->dispatches += 2 + dispatches;
     advance(c, layer, 0, 1, 1);
@@ -903,8 +938,8 @@ extern "C" int32_t qxh_encode_granite_attention_block_q4(qxh_graph* g, qxh_kv_ca
     if ((r = check_append(c, layer, 0, 1, position, 1))) return r;
     QXH_REQUIRE(position <= 4096, QXH_ERR_INVALID_ARGUMENT, "unregistered Granite RoPE coordinate %u", position);
     const uint32_t length = position + 1;
-    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, c->desc.value_dtype, 1, length);
-    const uint64_t need = 2 * 1024 * sizeof(float) + align256(p.workspace_bytes);
+    const BlockAttention b = block_attention_plan(c, length);
+    const uint64_t need = block_workspace_bytes(b);
     QXH_REQUIRE(workspace && workspace_bytes >= need, QXH_ERR_INVALID_ARGUMENT,
                 "granite q4 block workspace holds %llu bytes, needs %llu", (unsigned long long)workspace_bytes,
                 (unsigned long long)need);
@@ -926,10 +961,9 @@ extern "C" int32_t qxh_encode_granite_attention_block_q4(qxh_graph* g, qxh_kv_ca
     hipError_t e = launch_granite_q4_qkv_rope(kv, a, g->stream);
     if (e != hipSuccess) return hip_fail(e, "granite q4 qkv launch");
     int dispatches = 0;
-    e = launch_decode_attention(c->dims, kv, p, 1, length, a.query_rot, QXH_F32, a.attention, QXH_F32, attn_ws,
-                                g->stream, &dispatches);
+    e = launch_block_attention(c, kv, b, length, a.query_rot, a.attention, attn_ws, g->stream, &dispatches, &a.parts);
     if (e != hipSuccess) return hip_fail(e, "granite q4 attention launch");
-    e = launch_granite_q4_out_residual(a, g->stream);
+    e = b.fused ? launch_granite_q4_out_merge_residual(a, g->stream) : launch_granite_q4_out_residual(a, g->stream);
     if (e != hipSuccess) return hip_fail(e, "granite q4 output launch");
     g->dispatches += 2 + dispatches;
     if (inverse_rms) {
