@@ -222,6 +222,53 @@ def bench_cfg2(ctx, steps, warmup, q4=False):
 
 
 # ---------------------------------------------------------------------------
+# Qwen attention half (Q4 projections) for 48 layers at ctx 32768, f16 KV
+# ---------------------------------------------------------------------------
+def bench_qwen_block(ctx, steps, warmup):
+    import torch
+    from qx_amd import abi
+    from qx_amd import runtime as rt
+
+    LAYERS, POS = 48, 32767
+    stream = torch.cuda.current_stream()
+    gen = torch.Generator(device="cuda:0")
+    arena = rt.KvArena(ctx, abi.SHAPE_QWEN3, LAYERS, 1, POS + 1, abi.F16)
+    layers = []
+    with rt.Graph(ctx, stream) as g:
+        arena.fill_normal(g, seed=21, length=POS)
+    for layer in range(LAYERS):
+        gen.manual_seed(5000 + layer)
+        mats = []
+        for rows, cols in ((4096, 2048), (512, 2048), (512, 2048), (2048, 4096)):
+            codes = torch.randint(0, 256, (rows, cols // 2), dtype=torch.uint8, device="cuda:0", generator=gen)
+            scales = torch.full((rows, cols // 32), 0.02 / 7, dtype=torch.float16, device="cuda:0").view(torch.int16)
+            mats.append(rt.Q4Matrix(codes, scales, rows, cols))
+        ones = lambda n: torch.ones(n, device="cuda:0")
+        layers.append(rt.QwenQ4Layer(ones(2048), mats[0], mats[1], mats[2], ones(128), ones(128), mats[3],
+                                     ones(2048)))
+    hidden = [torch.empty(2048, dtype=torch.float16, device="cuda:0") for _ in range(LAYERS + 1)]
+    moe = torch.empty(2048, dtype=torch.float16, device="cuda:0")
+    with rt.Graph(ctx, stream) as g:
+        rt.fill_normal(g, hidden[0], seed=78)
+    ws = torch.empty(rt.qwen_block_workspace_bytes(arena, POS + 1), dtype=torch.uint8, device="cuda:0")
+    g = rt.Graph(ctx, stream)
+    g.capture_begin()
+    for layer in range(LAYERS):
+        rt.qwen_attention_block(g, arena, layer, POS, layers[layer], hidden[layer], hidden[layer + 1], moe, ws)
+    replay = g.capture_end()
+    g.discard()
+    ms = timed(lambda: replay.launch(stream), steps, warmup, stream)
+    weights = (4096 + 512 + 512) * (1024 + 128) + 2048 * (2048 + 256)  # Q4 codes + f16 scales
+    kv = (POS + 1) * 4 * 128 * 2 * 2
+    per_token = LAYERS * (weights + kv)
+    return {"us_per_token": ms * 1000.0, "us_per_layer": ms * 1000.0 / LAYERS, "bytes_per_token": per_token,
+            "roofline": roofline_hbm(per_token, ms, None),
+            "note": "48 x Qwen attention half (norm + Q4 q/k/v, q/k head norm + RoPE + append, split-K attention "
+                    "over 32768 f16 positions, Q4 o, residual + post-attention norm) per token, random Q4 codes, "
+                    "HIP-graph replay; roofline is for the whole token"}
+
+
+# ---------------------------------------------------------------------------
 # cfg5a: Qwen decode at ctx 32768, bf16 KV, 48 layers' caches rotated
 # ---------------------------------------------------------------------------
 def bench_cfg5a(ctx, steps, warmup):
@@ -438,7 +485,7 @@ def run(ctx, args):
         for name, fn in (("cfg1", bench_cfg1), ("cfg2", bench_cfg2),
                          ("cfg2q4", lambda c, k, w: bench_cfg2(c, k, w, q4=True)),
                          ("cfg3", lambda c, k, w: bench_prefill(c, k, w, "cfg3")),
-                         ("cfg5a", bench_cfg5a), ("cfg5b", lambda c, k, w: bench_prefill(c, k, w, "cfg5b")),
+                         ("cfg5a", bench_cfg5a), ("qwenblock", bench_qwen_block), ("cfg5b", lambda c, k, w: bench_prefill(c, k, w, "cfg5b")),
                          ("kvhash", bench_kv_hash)):
             if only and name not in only:
                 continue

@@ -401,6 +401,39 @@ QXH_API int32_t qxh_encode_granite_attention_block_q4(qxh_graph* graph, qxh_kv_c
                                                       const float* hidden_in, float* hidden_out, float* inverse_rms,
                                                       void* workspace, uint64_t workspace_bytes);
 
+/* ---- Qwen attention half with Q4 projections ----------------------------------
+ * PreparedQwenLayer::encode_with_expert_cache up to the router input
+ * (crates/qx-runtime-v2/src/lib.rs:904-973): encode_qwen_rms_norm,
+ * encode_prepared_qwen_q4_stage for q, k and v (crates/qx-metal/src/lib.rs:
+ * 1862-1916), encode_qwen_qk_norm_rope + encode_qwen_store_kv,
+ * encode_qwen_gqa_attention over position + 1 positions, the o stage and
+ * encode_qwen_residual_rms_norm (kernels/qwen_attention.metal:31-58).
+ * Activations are f16 bit patterns: hidden [2048] in; hidden_after_attention
+ * = f16(hidden + o) and moe_input = f16(rms_norm(hidden_after_attention) *
+ * post_attention_norm) out.  The K/V rows of `position` are appended to
+ * `layer` of sequence 0 (any KV dtype pair decode serves on the Qwen shape).
+ * Matches the reference's CPU stages (tools/qx-qwen-parity/src/main.rs:
+ * 124-240) to the 16-bit tolerance.  Workspace: qxh_qwen_block_workspace_bytes.
+ * Errors: a non-Qwen cache, matrix shapes other than q 4096x2048, k and v
+ * 512x2048, o 2048x4096, null norms, hidden aliasing an output, an append not
+ * at the cursor, a short workspace. */
+typedef struct {
+    const float* input_norm;          /* [2048] */
+    qxh_q4_matrix q_proj;             /* 4096 x 2048 */
+    qxh_q4_matrix k_proj;             /* 512 x 2048 */
+    qxh_q4_matrix v_proj;             /* 512 x 2048 */
+    const float* query_norm;          /* [128] */
+    const float* key_norm;            /* [128] */
+    qxh_q4_matrix o_proj;             /* 2048 x 4096 */
+    const float* post_attention_norm; /* [2048] */
+} qxh_qwen_q4_layer_weights;
+
+QXH_API int32_t qxh_qwen_block_workspace_bytes(const qxh_kv_cache* cache, uint32_t length, uint64_t* bytes);
+QXH_API int32_t qxh_encode_qwen_attention_block(qxh_graph* graph, qxh_kv_cache* cache, uint32_t layer,
+                                                uint32_t position, const qxh_qwen_q4_layer_weights* weights,
+                                                const uint16_t* hidden, uint16_t* hidden_after_attention,
+                                                uint16_t* moe_input, void* workspace, uint64_t workspace_bytes);
+
 /* ---- synthetic data (bench / tests) ------------------------------------------
  * Counter-based N(0, stddev^2) values (SplitMix64 -> Box-Muller), on device. */
 QXH_API int32_t qxh_encode_fill_normal(qxh_graph* graph, void* data, int32_t dtype, uint64_t count, uint64_t seed,

@@ -85,6 +85,9 @@ def lib():
         L.qxo_q4_mat_vec_simd32.argtypes = [_u8p, _u16p, ctypes.c_uint32, ctypes.c_uint32, _f32p,
                                             ctypes.c_float, _f32p]
         L.qxo_granite_rms_norm_simd.argtypes = [_f32p] * 5
+        L.qxo_q4_mat_vec.argtypes = [_u8p, _u16p, ctypes.c_uint32, ctypes.c_uint32, _f32p, _f32p]
+        L.qxo_qwen_rms_norm.argtypes = [_f32p, _f32p, ctypes.c_uint32, ctypes.c_float, _f32p]
+        L.qxo_qwen_rms_norm.restype = None
         L.qxo_granite_residual.argtypes = [_f32p, _f32p, _f32p]
         L.qxo_granite_residual.restype = None
         L.qxo_granite_attend_simd.argtypes = [_f32p, ctypes.c_void_p, ctypes.c_uint32, _f32p]
@@ -335,6 +338,15 @@ def q4_mat_vec_simd32(m: Q4Matrix, vector, multiplier: float = 1.0):
     return out
 
 
+def q4_mat_vec(m: Q4Matrix, vector):
+    """QuantizedTensor::mat_vec (Q4, RowMajor), crates/qx-quant/src/lib.rs:851-891:
+    one sequential fma chain per row."""
+    x = _f32(vector)
+    out = np.zeros(m.rows, np.float32)
+    _check(lib().qxo_q4_mat_vec(_p(m.packed, _u8p), _p(m.scales, _u16p), m.rows, m.cols, _p(x), _p(out)))
+    return out
+
+
 def granite_rms_norm_simd(hidden, weight=None):
     """rms_norm_simd, crates/qx-runtime/src/lib.rs:2416-2432.  Returns
     (normalized or None, sum of squares, inverse RMS)."""
@@ -396,6 +408,52 @@ def qwen_qk_norm_rope(query_bits, key_bits, query_norm, key_norm, position: int,
     lib().qxo_qwen_qk_norm_rope(_p(q, _u16p), _p(k, _u16p), _p(qn), _p(kn), position, fmt,
                                 _p(qo, _u16p), _p(ko, _u16p))
     return qo, ko
+
+
+def qwen_rms_norm(vector, weight, epsilon: float = 1e-6):
+    """rms_norm, tools/qx-qwen-parity/src/main.rs:1157-1168."""
+    x, w = _f32(vector), _f32(weight)
+    out = np.zeros(x.size, np.float32)
+    lib().qxo_qwen_rms_norm(_p(x), _p(w), x.size, float(epsilon), _p(out))
+    return out
+
+
+def _f16_round(a):
+    return np.asarray(a, np.float32).astype(np.float16)
+
+
+def qwen_attention_block(hidden_bits, input_norm, wq: "Q4Matrix", wk: "Q4Matrix", wv: "Q4Matrix", query_norm,
+                         key_norm, wo: "Q4Matrix", post_attention_norm, position: int, key_cache_bits,
+                         value_cache_bits):
+    """The attention half of a Qwen layer as the parity tool checks it stage by
+    stage (tools/qx-qwen-parity/src/main.rs:124-240; the GPU graph is
+    PreparedQwenLayer::encode_with_expert_cache, crates/qx-runtime-v2/src/lib.rs:
+    904-973): f16 rms_norm of the f16 hidden state, f16 Q4 q/k/v projections
+    (mat_vec), cpu_qk_norm_rope, K/V stored at `position`, cpu_gqa_attention,
+    f16 Q4 o projection, hidden_after = f16(hidden + projection) and
+    moe_input = f16(rms_norm(hidden_after)).  Caches are position-major f16
+    bits [ctx][4][128] holding positions [0, position); the new rows are
+    appended in a copy.  Returns a dict of every stage (f16 arrays)."""
+    h = np.asarray(hidden_bits, np.uint16).view(np.float16).astype(np.float32)
+    a = _f16_round(qwen_rms_norm(h, input_norm))
+    q = _f16_round(q4_mat_vec(wq, a.astype(np.float32)))
+    k = _f16_round(q4_mat_vec(wk, a.astype(np.float32)))
+    v = _f16_round(q4_mat_vec(wv, a.astype(np.float32)))
+    qr_bits, kr_bits = qwen_qk_norm_rope(q.view(np.uint16), k.view(np.uint16), query_norm, key_norm, position, F16)
+    kc = np.concatenate([np.asarray(key_cache_bits, np.uint16).reshape(-1, 512)[:position],
+                         np.asarray(kr_bits, np.uint16).reshape(1, 512)])
+    vc = np.concatenate([np.asarray(value_cache_bits, np.uint16).reshape(-1, 512)[:position],
+                         v.view(np.uint16).reshape(1, 512)])
+    att_bits = qwen_gqa_attention(qr_bits, kc, vc, F16)
+    att = np.asarray(att_bits, np.uint16).view(np.float16).astype(np.float32)
+    proj = _f16_round(q4_mat_vec(wo, att))
+    after = _f16_round(h + proj.astype(np.float32))
+    moe = _f16_round(qwen_rms_norm(after.astype(np.float32), post_attention_norm))
+    return {"attention_input": a, "query": q, "key": k, "value": v,
+            "query_rotated": np.asarray(qr_bits, np.uint16).view(np.float16),
+            "key_rotated": np.asarray(kr_bits, np.uint16).view(np.float16),
+            "attention": att.astype(np.float16), "projection": proj, "hidden_after_attention": after,
+            "moe_input": moe}
 
 
 def qwen_inverse_frequencies():

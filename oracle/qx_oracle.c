@@ -774,3 +774,37 @@ QXO_EXPORT int qxo_granite_q4_attention_block(const float* hidden, const float* 
 QXO_EXPORT void qxo_granite_residual(const float* hidden, const float* projection, float* out) {
     for (int i = 0; i < G_HIDDEN; ++i) out[i] = fmaf(kResidualMultiplier, projection[i], hidden[i]);
 }
+
+/* QuantizedTensor::mat_vec, crates/qx-quant/src/lib.rs:851-891, Q4 RowMajor:
+ * per row one fma chain over the columns in order, accumulator starting at 0. */
+QXO_EXPORT int qxo_q4_mat_vec(const uint8_t* packed, const uint16_t* scales, uint32_t rows, uint32_t cols,
+                              const float* input, float* out) {
+    if (cols == 0 || cols % 32) {
+        set_error("Q4 mat_vec needs a positive multiple of 32 columns");
+        return 1;
+    }
+    const uint32_t groups = cols / 32;
+    for (uint32_t r = 0; r < rows; ++r) {
+        float acc = 0.0f;
+        for (uint32_t c = 0; c < cols; ++c) {
+            uint32_t g = c / 32, local = c % 32;
+            uint8_t byte = packed[(size_t)r * (cols / 2) + (size_t)g * 16 + local / 2];
+            uint32_t code = (byte >> ((local % 2) * 4)) & 0xfu;
+            float value = (float)((int)code - 7) * qxo_f16_to_f32(scales[(size_t)r * groups + g]);
+            acc = fmaf(value, input[c], acc);
+        }
+        out[r] = acc;
+    }
+    return 0;
+}
+
+/* rms_norm of the Qwen parity tool, tools/qx-qwen-parity/src/main.rs:1157-1168:
+ * the sum of rounded squares as a left fold, divided by n, plus epsilon, then
+ * sqrt and reciprocal (std f32 sqrt is IEEE-correct, as sqrtf), and
+ * value * inverse * weight left to right. */
+QXO_EXPORT void qxo_qwen_rms_norm(const float* input, const float* weight, uint32_t n, float epsilon, float* out) {
+    float sum = 0.0f;
+    for (uint32_t i = 0; i < n; ++i) sum += input[i] * input[i];
+    float inverse = 1.0f / sqrtf(sum / (float)n + epsilon);
+    for (uint32_t i = 0; i < n; ++i) out[i] = input[i] * inverse * weight[i];
+}

@@ -67,6 +67,12 @@ class GraniteQ4LayerWeights(ctypes.Structure):
                 ("o_proj", Q4Matrix)]
 
 
+class QwenQ4LayerWeights(ctypes.Structure):
+    _fields_ = [("input_norm", c_void_p), ("q_proj", Q4Matrix), ("k_proj", Q4Matrix), ("v_proj", Q4Matrix),
+                ("query_norm", c_void_p), ("key_norm", c_void_p), ("o_proj", Q4Matrix),
+                ("post_attention_norm", c_void_p)]
+
+
 # name -> (restype, argtypes); must cover every function of include/qx_hip.h
 SIGNATURES = {
     "qxh_abi_version": (c_int32, []),
@@ -126,6 +132,9 @@ SIGNATURES = {
     "qxh_encode_granite_attention_block_q4": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32,
                                                         P(GraniteQ4LayerWeights), c_void_p, c_void_p, c_void_p,
                                                         c_void_p, c_uint64]),
+    "qxh_qwen_block_workspace_bytes": (c_int32, [c_void_p, c_uint32, P(c_uint64)]),
+    "qxh_encode_qwen_attention_block": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32, P(QwenQ4LayerWeights),
+                                                  c_void_p, c_void_p, c_void_p, c_void_p, c_uint64]),
     "qxh_encode_fill_normal": (c_int32, [c_void_p, c_void_p, c_int32, c_uint64, c_uint64, c_float]),
     "qxh_encode_kv_fill_normal": (c_int32, [c_void_p, c_void_p, c_uint64, c_uint32]),
     "qxh_encode_consensus_conformance": (c_int32, [c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p,

@@ -157,6 +157,24 @@ struct GraniteQ4Args {
     uint32_t position;
     BlockPartials parts;
 };
+// Qwen attention half with Q4 projections (qwen_block.hip); f16 activations.
+struct QwenBlockArgs {
+    const float* input_norm;    // [2048]
+    Q4View wq, wk, wv, wo;      // 4096x2048, 512x2048, 512x2048, 2048x4096
+    const float* post_norm;     // [2048]
+    const uint16_t* hidden;     // f16 [2048]
+    uint16_t* query;            // workspace f16 [4096], before RoPE
+    uint16_t* key;              // workspace f16 [512]
+    uint16_t* value;            // workspace f16 [512]
+    const uint16_t* attention;  // workspace f16 [4096]
+    uint16_t* projection;       // workspace f16 [2048]
+    uint16_t* hidden_after;     // f16 [2048]
+    uint16_t* moe_input;        // f16 [2048]
+};
+hipError_t launch_qwen_norm_qkv(const QwenBlockArgs& a, hipStream_t st);
+hipError_t launch_qwen_out(const QwenBlockArgs& a, hipStream_t st);
+hipError_t launch_qwen_residual_norm(const QwenBlockArgs& a, hipStream_t st);
+
 hipError_t launch_q4_gemv(const Q4GemvArgs& a, hipStream_t st);
 hipError_t launch_rms_inverse(const float* input, float* inverse, hipStream_t st);
 hipError_t launch_granite_q4_qkv_rope(const KvLayer& kv, const GraniteQ4Args& a, hipStream_t st);

@@ -25,6 +25,7 @@
 #include "common.h"
 #include "consensus_math.h"
 #include "internal.h"
+#include "q4_common.h"
 
 namespace qxh {
 
@@ -34,29 +35,6 @@ constexpr int kHidden = 1024;
 constexpr float kRmsEps = 1e-6f;    // qx_model::RMS_EPSILON
 constexpr float kResidual = 0.22f;  // qx_model::RESIDUAL_MULTIPLIER
 constexpr int kChunkGroups = 32;    // groups staged per pass (1024 columns)
-
-// The reference's 32-lane tree (reduce_simd32, crates/qx-runtime/src/lib.rs:
-// 2298-2305; qx_ordered_simd_sum, kernels/q4_dense.metal:6-13) as an xor
-// butterfly with the same offsets in the same order.  At offset o, lane i with
-// bit o clear forms v[i] + v[i + o], exactly the tree's step; its partner
-// forms v[i + o] + v[i], the same bits, so every lane of the 32-lane group
-// ends with lane 0's tree value.
-__device__ __forceinline__ float ordered_sum32(float v) {
-    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));  // xor 16
-    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x201F));  // xor 8
-    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x101F));  // xor 4
-    v += dpp_quad_xor2(v);
-    v += dpp_quad_xor1(v);
-    return v;
-}
-
-__device__ __forceinline__ float readlane_f(float v, int lane) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
-
-__device__ __forceinline__ float f16_bits_to_float(uint16_t b) {
-    return (float)__builtin_bit_cast(_Float16, b);
-}
 
 // Sum of squares of a 1024-wide vector in the 256-thread order of
 // rms_norm_simd (crates/qx-runtime/src/lib.rs:2416-2432), run by a 256-thread
@@ -78,34 +56,6 @@ __device__ __forceinline__ float square_sum_256(const float (&x)[4], float* grou
 
 __device__ __forceinline__ float inverse_rms(float total) {
     return consensus_rsqrt(total / (float)kHidden + kRmsEps);
-}
-
-// The lane's fold over `groups` groups of its half-wave's row.  `codes` is
-// the half-wave's 32 staged groups in LDS (group g at byte 16 g), `scale` the
-// lane's own group scale (group l), `in` the staged input chunk.
-__device__ __forceinline__ float q4_fold(const uint8_t* codes, float scale, const float* in, int groups, int l,
-                                         float acc) {
-    const int shift = (l & 1) * 4;
-    for (int g = 0; g < groups; ++g) {
-        const uint32_t code = ((uint32_t)codes[g * 16 + (l >> 1)] >> shift) & 0xfu;
-        const float s = __shfl(scale, g, 32);
-        const float w = (float)((int)code - 7) * s;
-        acc = __builtin_fmaf(w, in[g * 32 + l], acc);
-    }
-    return acc;
-}
-
-// The 32-group case (a full 1024-column chunk) fully unrolled.
-__device__ __forceinline__ float q4_fold32(const uint8_t* codes, float scale, const float* in, int l, float acc) {
-    const int shift = (l & 1) * 4;
-#pragma unroll
-    for (int g = 0; g < 32; ++g) {
-        const uint32_t code = ((uint32_t)codes[g * 16 + (l >> 1)] >> shift) & 0xfu;
-        const float s = __shfl(scale, g, 32);
-        const float w = (float)((int)code - 7) * s;
-        acc = __builtin_fmaf(w, in[g * 32 + l], acc);
-    }
-    return acc;
 }
 
 // ---- general GEMV -----------------------------------------------------------

@@ -975,6 +975,99 @@ extern "C" int32_t qxh_encode_granite_attention_block_q4(qxh_graph* g, qxh_kv_ca
     return QXH_OK;
 }
 
+// Qwen block workspace: f16 query, key, value, rotated query, attention and
+// o projection, then the decode split partials.
+constexpr uint64_t kQwenBlockScratch = 2 * (4096 + 512 + 512 + 4096 + 4096 + 2048);
+
+extern "C" int32_t qxh_qwen_block_workspace_bytes(const qxh_kv_cache* c, uint32_t length, uint64_t* bytes) {
+    QXH_REQUIRE(c && bytes, QXH_ERR_INVALID_ARGUMENT, "qwen_block_workspace_bytes: null argument");
+    QXH_REQUIRE(c->desc.shape == QXH_SHAPE_QWEN3, QXH_ERR_INVALID_ARGUMENT, "Qwen block needs a Qwen cache");
+    QXH_REQUIRE(length > 0, QXH_ERR_INVALID_ARGUMENT, "empty attention");
+    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, c->desc.value_dtype, 1, length);
+    *bytes = align256(kQwenBlockScratch) + align256(p.workspace_bytes);
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_encode_qwen_attention_block(qxh_graph* g, qxh_kv_cache* c, uint32_t layer, uint32_t position,
+                                                   const qxh_qwen_q4_layer_weights* w, const uint16_t* hidden,
+                                                   uint16_t* hidden_after, uint16_t* moe_input, void* workspace,
+                                                   uint64_t workspace_bytes) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    if ((r = check_range(c, layer, 0, 1))) return r;
+    QXH_REQUIRE(c->desc.shape == QXH_SHAPE_QWEN3, QXH_ERR_INVALID_ARGUMENT, "Qwen block needs a Qwen cache");
+    QXH_REQUIRE(w && w->input_norm && w->query_norm && w->key_norm && w->post_attention_norm,
+                QXH_ERR_INVALID_ARGUMENT, "qwen block: null weights or norm");
+    if ((r = check_q4(w->q_proj, 4096, 2048, "qwen block q_proj"))) return r;
+    if ((r = check_q4(w->k_proj, 512, 2048, "qwen block k_proj"))) return r;
+    if ((r = check_q4(w->v_proj, 512, 2048, "qwen block v_proj"))) return r;
+    if ((r = check_q4(w->o_proj, 2048, 4096, "qwen block o_proj"))) return r;
+    QXH_REQUIRE(hidden && hidden_after && moe_input, QXH_ERR_INVALID_ARGUMENT, "qwen block: null activation");
+    QXH_REQUIRE(!ranges_overlap(hidden, 4096, hidden_after, 4096) && !ranges_overlap(hidden, 4096, moe_input, 4096) &&
+                    !ranges_overlap(hidden_after, 4096, moe_input, 4096),
+                QXH_ERR_INVALID_ARGUMENT, "qwen block: hidden, hidden_after_attention and moe_input must not overlap");
+    QXH_REQUIRE(decode_dtypes_supported(c->dims, c->desc.key_dtype, c->desc.value_dtype), QXH_ERR_UNSUPPORTED,
+                "decode attention does not serve K dtype %d with V dtype %d for this shape", c->desc.key_dtype,
+                c->desc.value_dtype);
+    if ((r = check_append(c, layer, 0, 1, position, 1))) return r;
+    const uint32_t length = position + 1;
+    const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, c->desc.value_dtype, 1, length);
+    const uint64_t need = align256(kQwenBlockScratch) + align256(p.workspace_bytes);
+    QXH_REQUIRE(workspace && workspace_bytes >= need, QXH_ERR_INVALID_ARGUMENT,
+                "qwen block workspace holds %llu bytes, needs %llu", (unsigned long long)workspace_bytes,
+                (unsigned long long)need);
+    QXH_REQUIRE(((uintptr_t)workspace & 15) == 0, QXH_ERR_INVALID_ARGUMENT, "qwen block workspace must be 16-byte aligned");
+    uint16_t* ws16 = reinterpret_cast<uint16_t*>(workspace);
+    QwenBlockArgs a{};
+    a.input_norm = w->input_norm;
+    a.wq = {w->q_proj.packed, w->q_proj.scales};
+    a.wk = {w->k_proj.packed, w->k_proj.scales};
+    a.wv = {w->v_proj.packed, w->v_proj.scales};
+    a.wo = {w->o_proj.packed, w->o_proj.scales};
+    a.post_norm = w->post_attention_norm;
+    a.hidden = hidden;
+    a.query = ws16;
+    a.key = a.query + 4096;
+    a.value = a.key + 512;
+    uint16_t* query_rot = a.value + 512;
+    uint16_t* attention = query_rot + 4096;
+    a.attention = attention;
+    a.projection = attention + 4096;
+    a.hidden_after = hidden_after;
+    a.moe_input = moe_input;
+    void* attn_ws = reinterpret_cast<char*>(workspace) + align256(kQwenBlockScratch);
+    const KvLayer kv = kv_layer(c, layer, 0);
+    hipError_t e = launch_qwen_norm_qkv(a, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "qwen norm + qkv launch");
+    RopeAppendArgs ra{};
+    ra.query = a.query;
+    ra.key = a.key;
+    ra.value = a.value;
+    ra.query_out = query_rot;
+    ra.query_norm = w->query_norm;
+    ra.key_norm = w->key_norm;
+    ra.input_dtype = QXH_F16;
+    ra.output_dtype = QXH_F16;
+    ra.start_position = position;
+    ra.tokens = 1;
+    ra.sequences = 1;
+    ra.mode = 1;
+    qwen_inverse_frequencies(ra.qwen_inv_freq);
+    e = launch_rope_append(c->dims, kv, ra, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "qwen rope + append launch");
+    int dispatches = 0;
+    e = launch_decode_attention(c->dims, kv, p, 1, length, query_rot, QXH_F16, attention, QXH_F16, attn_ws, g->stream,
+                                &dispatches);
+    if (e != hipSuccess) return hip_fail(e, "qwen attention launch");
+    e = launch_qwen_out(a, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "qwen o projection launch");
+    e = launch_qwen_residual_norm(a, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "qwen residual norm launch");
+    g->dispatches += 4 + dispatches;
+    advance(c, layer, 0, 1, 1);
+    return QXH_OK;
+}
+
 extern "C" int32_t qxh_encode_fill_normal(qxh_graph* g, void* data, int32_t dtype, uint64_t count, uint64_t seed,
                                           float stddev) {
     int32_t r = check_graph(g);

@@ -426,6 +426,35 @@ def granite_attention_block_q4(graph: Graph, cache: KvArena, layer: int, positio
         _ptr(hidden_out), None if inverse_rms is None else _ptr(inverse_rms), _ptr(workspace), workspace.numel()))
 
 
+class QwenQ4Layer:
+    """Q4 weights of one Qwen attention half: fp32 input norm [2048], Q4Matrix
+    q (4096x2048), k, v (512x2048), fp32 q/k head norms [128], Q4Matrix o
+    (2048x4096), fp32 post-attention norm [2048]."""
+
+    def __init__(self, input_norm, q_proj: Q4Matrix, k_proj: Q4Matrix, v_proj: Q4Matrix, query_norm, key_norm,
+                 o_proj: Q4Matrix, post_attention_norm):
+        self.tensors = (input_norm, q_proj, k_proj, v_proj, query_norm, key_norm, o_proj, post_attention_norm)
+        self.struct = abi.QwenQ4LayerWeights(input_norm.data_ptr(), q_proj.struct, k_proj.struct, v_proj.struct,
+                                             query_norm.data_ptr(), key_norm.data_ptr(), o_proj.struct,
+                                             post_attention_norm.data_ptr())
+
+
+def qwen_block_workspace_bytes(cache: KvArena, length: int) -> int:
+    n = ctypes.c_uint64()
+    check(lib().qxh_qwen_block_workspace_bytes(cache.handle, length, ctypes.byref(n)))
+    return n.value
+
+
+def qwen_attention_block(graph: Graph, cache: KvArena, layer: int, position: int, weights: QwenQ4Layer, hidden,
+                         hidden_after, moe_input, workspace):
+    """The attention half of PreparedQwenLayer::encode_with_expert_cache
+    (crates/qx-runtime-v2/src/lib.rs:904-973); f16 hidden in, f16
+    hidden_after_attention and moe_input out."""
+    check(lib().qxh_encode_qwen_attention_block(
+        graph.handle, cache.handle, layer, position, ctypes.byref(weights.struct), _ptr(hidden), _ptr(hidden_after),
+        _ptr(moe_input), _ptr(workspace), workspace.numel()))
+
+
 def consensus_conformance(graph: Graph, inputs, coords):
     n = inputs.numel()
     outs = [torch.empty(n, dtype=torch.int32, device=inputs.device) for _ in range(4)]
