@@ -65,6 +65,39 @@ def roofline_hbm(bytes_per_launch, ms_per_launch, traffic=None):
 
 
 # ---------------------------------------------------------------------------
+# Achievable HBM on this box: a plain streaming read (a torch reduction over
+# 2 GiB, far beyond the 256 MB MALL) and a 1 GiB copy, timed like the rest,
+# so the decode rooflines can be read against the measured ceiling as well as
+# the 8 TB/s specification.
+# ---------------------------------------------------------------------------
+def bench_hbm_probe(ctx, steps, warmup):
+    import torch
+    from qx_amd import runtime as rt
+    stream = torch.cuda.current_stream()
+    nbytes = 2 << 30
+    x = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0")
+    with rt.Graph(ctx, stream) as g:
+        rt.fill_normal(g, x.view(torch.float32), seed=3)
+    best = None
+    for blocks in (1024, 2048, 4096):
+        sink = torch.empty(blocks, dtype=torch.int32, device="cuda:0")
+        g = rt.Graph(ctx, stream)
+
+        def step():
+            rt.hbm_read_probe(g, x, sink, blocks)
+
+        ms = timed(step, steps, warmup, stream)
+        g.finish()
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        if best is None or gbs > best[1]:
+            best = (blocks, gbs)
+    return {"read_gb_per_s": round(best[1], 1), "read_frac_of_peak": round(best[1] / HBM_PEAK_GBS, 4),
+            "blocks": best[0],
+            "note": "one streaming read of 2 GiB (16-byte nontemporal loads, best of 1024/2048/4096 workgroups; "
+                    "qxh_encode_hbm_read_probe): the HBM rate a plain streaming kernel reaches on this box"}
+
+
+# ---------------------------------------------------------------------------
 # cfg4: batched fp16 decode, 256 x 4096, 24 layers of independent caches
 # ---------------------------------------------------------------------------
 def bench_cfg4(ctx, steps, warmup):
@@ -482,7 +515,7 @@ def run(ctx, args):
     if head:
         log("cfg4", json.dumps(head))
     if not args.no_detail:
-        for name, fn in (("cfg1", bench_cfg1), ("cfg2", bench_cfg2),
+        for name, fn in (("hbm_probe", bench_hbm_probe), ("cfg1", bench_cfg1), ("cfg2", bench_cfg2),
                          ("cfg2q4", lambda c, k, w: bench_cfg2(c, k, w, q4=True)),
                          ("cfg3", lambda c, k, w: bench_prefill(c, k, w, "cfg3")),
                          ("cfg5a", bench_cfg5a), ("qwenblock", bench_qwen_block), ("cfg5b", lambda c, k, w: bench_prefill(c, k, w, "cfg5b")),
@@ -496,6 +529,8 @@ def run(ctx, args):
                 detail[name] = {"error": str(e)}
                 log(name, "error", e)
             torch.cuda.empty_cache()
+    if head and isinstance(detail.get("hbm_probe"), dict) and "read_gb_per_s" in detail["hbm_probe"]:
+        head["frac_of_hbm_probe"] = round(head["roofline"]["achieved"] / detail["hbm_probe"]["read_gb_per_s"], 4)
     cpu = None if args.no_cpu else cpu_baseline()
     if head is None:
         print(json.dumps({"detail": detail, "cpu_baseline": cpu}))

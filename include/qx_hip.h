@@ -438,6 +438,12 @@ QXH_API int32_t qxh_encode_qwen_attention_block(qxh_graph* graph, qxh_kv_cache* 
  * Counter-based N(0, stddev^2) values (SplitMix64 -> Box-Muller), on device. */
 QXH_API int32_t qxh_encode_fill_normal(qxh_graph* graph, void* data, int32_t dtype, uint64_t count, uint64_t seed,
                                float stddev);
+/* Achievable-HBM probe: one streaming read of `bytes` (a positive multiple of
+ * 16, 16-byte aligned) with 16-byte nontemporal loads over `blocks`
+ * workgroups of 256 threads (0: 2048).  `sink` (4 * blocks bytes) is never
+ * written for real data; it keeps the loads from being optimised away. */
+QXH_API int32_t qxh_encode_hbm_read_probe(qxh_graph* graph, const void* data, uint64_t bytes, uint32_t* sink,
+                                          uint32_t blocks);
 /* Fill rows [0, length) of every (layer, sequence, kv_head) cache with
  * N(0,1) values and set every cursor to `length`. */
 QXH_API int32_t qxh_encode_kv_fill_normal(qxh_graph* graph, qxh_kv_cache* cache, uint64_t seed, uint32_t length);

@@ -51,6 +51,8 @@ hipError_t launch_qwen_qk_norm_rope(void* q, void* k, const float* qn, const flo
 hipError_t launch_kv_gather(const ShapeDims& s, const KvLayer& kv, uint32_t pos_begin, uint32_t count, void* keys_out,
                             void* values_out, hipStream_t st);
 hipError_t launch_fill_normal(void* data, int dtype, uint64_t count, uint64_t seed, float stddev, hipStream_t st);
+// probe.hip: plain streaming read of `bytes` (a multiple of 16) over `blocks` workgroups
+hipError_t launch_hbm_read_probe(const void* data, uint64_t bytes, uint32_t* sink, uint32_t blocks, hipStream_t st);
 // decode_attention.hip: Granite RoPE + append + attention of one token, one dispatch
 hipError_t launch_decode_step(const ShapeDims& s, const KvLayer& kv, const float* query, const float* key,
                               const float* value, float* query_out, uint32_t position, void* out, int out_dtype,

@@ -1080,6 +1080,20 @@ extern "C" int32_t qxh_encode_fill_normal(qxh_graph* g, void* data, int32_t dtyp
     return QXH_OK;
 }
 
+extern "C" int32_t qxh_encode_hbm_read_probe(qxh_graph* g, const void* data, uint64_t bytes, uint32_t* sink,
+                                             uint32_t blocks) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    QXH_REQUIRE(data && sink, QXH_ERR_INVALID_ARGUMENT, "hbm_read_probe: null argument");
+    QXH_REQUIRE(bytes > 0 && bytes % 16 == 0 && ((uintptr_t)data & 15) == 0, QXH_ERR_INVALID_ARGUMENT,
+                "hbm_read_probe: bytes must be a positive multiple of 16 at a 16-byte aligned address");
+    if (blocks == 0) blocks = 2048;
+    hipError_t e = launch_hbm_read_probe(data, bytes, sink, blocks, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "hbm_read_probe launch");
+    g->dispatches += 1;
+    return QXH_OK;
+}
+
 extern "C" int32_t qxh_encode_kv_fill_normal(qxh_graph* g, qxh_kv_cache* c, uint64_t seed, uint32_t length) {
     int32_t r = check_graph(g);
     if (r) return r;

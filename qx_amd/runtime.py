@@ -426,6 +426,12 @@ def granite_attention_block_q4(graph: Graph, cache: KvArena, layer: int, positio
         _ptr(hidden_out), None if inverse_rms is None else _ptr(inverse_rms), _ptr(workspace), workspace.numel()))
 
 
+def hbm_read_probe(graph: Graph, data, sink, blocks: int = 0):
+    """One plain streaming read of `data` (the bench's achievable-HBM probe)."""
+    check(lib().qxh_encode_hbm_read_probe(graph.handle, _ptr(data), data.numel() * data.element_size(), _ptr(sink),
+                                          blocks))
+
+
 class QwenQ4Layer:
     """Q4 weights of one Qwen attention half: fp32 input norm [2048], Q4Matrix
     q (4096x2048), k, v (512x2048), fp32 q/k head norms [128], Q4Matrix o
