@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define QXH_ABI_VERSION 1
+#define QXH_ABI_VERSION 2
 
 #if defined(__GNUC__)
 #define QXH_API __attribute__((visibility("default")))
@@ -56,8 +56,16 @@ enum {
 };
 
 /* Element types.  QXH_F16 is IEEE binary16, QXH_BF16 is bfloat16; both are
- * rounded to nearest even on store. */
-typedef enum { QXH_F32 = 0, QXH_F16 = 1, QXH_BF16 = 2 } qxh_dtype;
+ * rounded to nearest even on store.
+ * QXH_I8_TIERED is a value-cache format only (the tiered value cache that
+ * docs/qx-structural-memory-2026-08-25.md:69-74 proposes and the reference
+ * does not implement): the newest `value_window` positions of each
+ * (sequence, kv head) are held in binary16, older positions as INT8 codes in
+ * blocks of 32 elements with one binary16 scale per block,
+ * scale = f16(max|v| / 127), code = clamp(rint(v / scale), -127, 127), value
+ * = code * scale; v is the binary16 value, so a row quantises to the same
+ * bytes whether it leaves the window later or is appended past it. */
+typedef enum { QXH_F32 = 0, QXH_F16 = 1, QXH_BF16 = 2, QXH_I8_TIERED = 3 } qxh_dtype;
 
 /* Model attention shapes.
  * GRANITE: crates/qx-model/src/lib.rs:20-36 (16 q heads, 8 KV heads, d 64,
@@ -157,6 +165,8 @@ typedef struct {
     uint32_t layers;
     uint32_t sequences;
     uint32_t capacity;    /* positions per cache */
+    uint32_t value_window; /* QXH_I8_TIERED: binary16 positions per (sequence, kv head), a power of
+                              two in [32, 65536]; 0 for every other value dtype */
 } qxh_kv_desc;
 
 typedef struct {
@@ -166,7 +176,14 @@ typedef struct {
     uint64_t sequence_stride;   /* elements between sequences of one layer */
     uint64_t layer_stride;      /* elements between layers */
     uint32_t key_elem_bytes;
-    uint32_t value_elem_bytes;
+    uint32_t value_elem_bytes;  /* 1 for QXH_I8_TIERED (the INT8 codes at `values`) */
+    /* QXH_I8_TIERED only (NULL / 0 otherwise): one binary16 scale per 32
+     * elements at element offset / 32, and the binary16 window, where position
+     * p of a (sequence, kv head) sits in slot p % value_window of a
+     * value_window x head_dim block; blocks ordered [layer][sequence][kv head]. */
+    void* value_scales;
+    void* value_ring;
+    uint32_t value_window;
 } qxh_kv_layout;
 
 /* Bytes of arena a descriptor needs (ExecutionPlan::kv_bytes counterpart). */
@@ -189,6 +206,16 @@ QXH_API int32_t qxh_kv_cache_rollback(qxh_kv_cache* cache, uint32_t sequence, ui
 QXH_API int32_t qxh_kv_cache_set_len(qxh_kv_cache* cache, uint32_t sequence, uint32_t length);
 QXH_API int32_t qxh_kv_cache_layout(const qxh_kv_cache* cache, qxh_kv_layout* out);
 QXH_API int32_t qxh_kv_cache_desc(const qxh_kv_cache* cache, qxh_kv_desc* out);
+/* QXH_I8_TIERED: positions [0, boundary) of (layer, sequence) are INT8, the
+ * rest of the committed positions binary16 (no counterpart in the reference,
+ * which only proposes the format).  An append of `tokens` at cursor s moves
+ * the boundary to max(boundary, s + tokens - value_window); a rollback to L
+ * lowers it to min(boundary, L); reset clears it; set_len puts it at
+ * max(0, length - value_window).  Launches over several sequences of a tiered
+ * cache need equal boundaries (QXH_ERR_UNSUPPORTED otherwise).  Returns 0 for
+ * other value dtypes. */
+QXH_API int32_t qxh_kv_cache_value_tier(const qxh_kv_cache* cache, uint32_t layer, uint32_t sequence,
+                                        uint32_t* boundary);
 
 /* ---- encoders (enqueue on graph) --------------------------------------------- */
 

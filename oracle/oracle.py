@@ -560,3 +560,114 @@ def verification_hashes(residuals: bytes, residual_stride: int, key_rows, value_
                                  ctypes.c_uint32(interval), out) != 0:
         raise RuntimeError("oracle verification hashes: input rejected")
     return bytes(out)
+
+
+# --- tiered value cache ------------------------------------------------------
+# The reference proposes a tiered value cache (recent V in fp16, older V in
+# block-scaled INT8; docs/qx-structural-memory-2026-08-25.md:69-74) and does
+# not implement it, so there is no reference code or golden vector to follow:
+# this build defines the format (include/qx_hip.h, QXH_I8_TIERED) and these
+# functions restate that definition.  Parity is pinned by mathematics in
+# tests/test_oracle_tiered_v.py: exactly representable blocks, brute-force
+# nearest codes, the clamp and zero-scale cases, and the invariants of the
+# tier boundary under appends and rollbacks.
+
+TIER_BLOCK = 32
+
+
+def tiered_quantize(values_f16):
+    """Rows of binary16 values [..., d] (d a multiple of 32) -> (int8 codes
+    [..., d], binary16 scales [..., d / 32]): per block of 32, scale =
+    f16(f32(max|v|) / 127), code = clamp(rint(v / scale), -127, 127) in f32
+    arithmetic, and code 0 where the scale is 0."""
+    v = np.asarray(values_f16, dtype=np.float16).astype(np.float32)
+    blocks = v.reshape(v.shape[:-1] + (v.shape[-1] // TIER_BLOCK, TIER_BLOCK))
+    amax = np.max(np.abs(blocks), axis=-1)
+    scale16 = (amax / np.float32(127.0)).astype(np.float32).astype(np.float16)
+    s = scale16.astype(np.float32)[..., None]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = np.rint(blocks / s)
+    q = np.where(s > 0, np.clip(q, -127, 127), 0).astype(np.int8)
+    return q.reshape(v.shape), scale16
+
+
+def tiered_dequantize(codes, scales16):
+    """code * scale in f32 (exact: 8-bit code times 11-bit significand)."""
+    c = np.asarray(codes, dtype=np.int8).astype(np.float32)
+    blocks = c.reshape(c.shape[:-1] + (c.shape[-1] // TIER_BLOCK, TIER_BLOCK))
+    s = np.asarray(scales16, dtype=np.float16).astype(np.float32)[..., None]
+    return (blocks * s).reshape(c.shape)
+
+
+class TieredValueCache:
+    """Value rows of one sequence under the tiered format: position-major
+    [n][kv_heads][d] history with the boundary rule of qxh_kv_cache_value_tier.
+    `rows()` gives what the cache holds at each committed position as f32:
+    binary16 values at and after the boundary, dequantised INT8 before it."""
+
+    def __init__(self, window: int, kv_heads: int = GRANITE_KV_HEADS, head_dim: int = GRANITE_HEAD_DIM):
+        self.window, self.kv_heads, self.head_dim = window, kv_heads, head_dim
+        self.half = np.zeros((0, kv_heads, head_dim), np.float16)  # binary16 value per position
+        self.codes = np.zeros((0, kv_heads, head_dim), np.int8)
+        self.scales = np.zeros((0, kv_heads, head_dim // TIER_BLOCK), np.float16)
+        self.length = 0
+        self.boundary = 0
+
+    def _grow(self, n):
+        if n > len(self.half):
+            extra = n - len(self.half)
+            self.half = np.concatenate([self.half, np.zeros((extra,) + self.half.shape[1:], np.float16)])
+            self.codes = np.concatenate([self.codes, np.zeros((extra,) + self.codes.shape[1:], np.int8)])
+            self.scales = np.concatenate([self.scales, np.zeros((extra,) + self.scales.shape[1:], np.float16)])
+
+    def append(self, rows):
+        """Append value rows [t][kv_heads][d] (any float dtype; rounded to
+        binary16) at the cursor."""
+        rows = np.asarray(rows, dtype=np.float32).astype(np.float16)
+        s, t = self.length, rows.shape[0]
+        new_b = max(self.boundary, s + t - self.window)
+        self._grow(s + t)
+        self.half[s:s + t] = rows
+        lo = self.boundary
+        if new_b > lo:
+            self.codes[lo:new_b], self.scales[lo:new_b] = tiered_quantize(self.half[lo:new_b])
+        self.length, self.boundary = s + t, new_b
+
+    def rollback(self, length: int):
+        assert length <= self.length
+        self.length = length
+        self.boundary = min(self.boundary, length)
+
+    def set_len(self, length: int):
+        self.length = length
+        self.boundary = max(0, length - self.window)
+
+    def rows(self):
+        out = self.half[: self.length].astype(np.float32)
+        b = self.boundary
+        out[:b] = tiered_dequantize(self.codes[:b], self.scales[:b])
+        return out
+
+
+def _splitmix64(x):
+    x = (np.asarray(x, dtype=np.uint64) + np.uint64(0x9E3779B97F4A7C15))
+    x = (x ^ (x >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+    x = (x ^ (x >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return x ^ (x >> np.uint64(31))
+
+
+def tiered_fill_values(seed: int, block: int, capacity: int, length: int, head_dim: int = GRANITE_HEAD_DIM):
+    """f16 values [length][head_dim] that the library's synthetic fill of a
+    tiered value cache (qxh_encode_kv_fill_normal) gives (layer, sequence, kv
+    head) block `block` = (layer * sequences + sequence) * kv_heads + head:
+    element d of row p is the Irwin-Hall sum of the four 16-bit fields of
+    splitmix64(seed ^ 0x5DEECE66DA5A5A5A ^ splitmix64((block * capacity + p)
+    * head_dim + d)), centred, times 2^-15 (exact), rounded to f16.  A
+    test fixture generator of this library, not a reference function."""
+    with np.errstate(over="ignore"):
+        ctr = (np.uint64(block) * np.uint64(capacity) + np.arange(length, dtype=np.uint64)[:, None]) * \
+            np.uint64(head_dim) + np.arange(head_dim, dtype=np.uint64)[None, :]
+        h = _splitmix64(np.uint64(seed ^ 0x5DEECE66DA5A5A5A) ^ _splitmix64(ctr))
+    fields = [((h >> np.uint64(16 * i)) & np.uint64(0xFFFF)).astype(np.int64) for i in range(4)]
+    total = (fields[0] + fields[1] + fields[2] + fields[3] - 131070).astype(np.float32)
+    return (total * np.float32(2.0 ** -15)).astype(np.float16)

@@ -19,6 +19,7 @@ QXH_ERR_UNSUPPORTED = 4
 QXH_ERR_NO_DEVICE = 5
 
 F32, F16, BF16 = 0, 1, 2
+I8_TIERED = 3  # value dtype only: f16 window + INT8 blocks of 32 with f16 scales
 SHAPE_GRANITE, SHAPE_QWEN3 = 0, 1
 
 c_void_p = ctypes.c_void_p
@@ -45,12 +46,13 @@ class GraphMetrics(ctypes.Structure):
 
 class KvDesc(ctypes.Structure):
     _fields_ = [("shape", c_int32), ("key_dtype", c_int32), ("value_dtype", c_int32), ("layers", c_uint32),
-                ("sequences", c_uint32), ("capacity", c_uint32)]
+                ("sequences", c_uint32), ("capacity", c_uint32), ("value_window", c_uint32)]
 
 
 class KvLayout(ctypes.Structure):
     _fields_ = [("keys", c_void_p), ("values", c_void_p), ("head_stride", c_uint64), ("sequence_stride", c_uint64),
-                ("layer_stride", c_uint64), ("key_elem_bytes", c_uint32), ("value_elem_bytes", c_uint32)]
+                ("layer_stride", c_uint64), ("key_elem_bytes", c_uint32), ("value_elem_bytes", c_uint32),
+                ("value_scales", c_void_p), ("value_ring", c_void_p), ("value_window", c_uint32)]
 
 
 class GraniteLayerWeights(ctypes.Structure):
@@ -100,6 +102,7 @@ SIGNATURES = {
     "qxh_kv_cache_set_len": (c_int32, [c_void_p, c_uint32, c_uint32]),
     "qxh_kv_cache_layout": (c_int32, [c_void_p, P(KvLayout)]),
     "qxh_kv_cache_desc": (c_int32, [c_void_p, P(KvDesc)]),
+    "qxh_kv_cache_value_tier": (c_int32, [c_void_p, c_uint32, c_uint32, P(c_uint32)]),
     "qxh_encode_rope_kv_batch": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
                                            c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p,
                                            c_int32]),

@@ -11,7 +11,9 @@
 
 namespace qxh {
 
-enum DType : int { F32 = 0, F16 = 1, BF16 = 2 };
+// I8T: the tiered value format (INT8 codes + f16 block scales + f16 window),
+// a value-cache dtype only; tiered_v.h has its device side.
+enum DType : int { F32 = 0, F16 = 1, BF16 = 2, I8T = 3 };
 
 // bfloat16 storage (round-to-nearest-even on store, exact widening on load)
 struct bf16_t {
@@ -41,6 +43,10 @@ template <> struct Elem<F16> {
 template <> struct Elem<BF16> {
     typedef bf16_t T;
     static constexpr int bytes = 2;
+};
+template <> struct Elem<I8T> {  // the INT8 code region
+    typedef int8_t T;
+    static constexpr int bytes = 1;
 };
 
 __device__ __forceinline__ float to_f32(float x) { return x; }

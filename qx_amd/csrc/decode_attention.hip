@@ -22,6 +22,9 @@
 #include "consensus_math.h"
 #include "internal.h"
 #include "mfma.h"
+#include "tiered_v.h"
+
+#include <type_traits>
 
 namespace qxh {
 
@@ -44,6 +47,13 @@ struct DecodeArgs {
     // one sequence (seq_stride 0) and row t attends [0, min(length, causal_start + t + 1))
     uint32_t causal;
     uint32_t causal_start;
+    // tiered values (VALU kernel, VDT == I8T): `values` holds the INT8 codes
+    const void* value_scales;
+    const void* value_ring;
+    uint64_t ring_head_stride;  // elements
+    uint64_t ring_seq_stride;   // elements (0 for causal rows)
+    uint32_t window_mask;
+    uint32_t tier;
 };
 
 constexpr float kNegBig = -1.0e30f;
@@ -161,6 +171,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
     const size_t head_off = (size_t)seq * a.seq_stride + (size_t)kvh * a.head_stride;
     const char* kb = reinterpret_cast<const char*>(a.keys) + head_off * EB;
     const char* vb = reinterpret_cast<const char*>(a.values) + head_off * VEB;
+    // tiered values: the block scales and the f16 window of this (sequence, kv head)
+    const uint16_t* vsc = reinterpret_cast<const uint16_t*>(a.value_scales) + head_off / kTierBlock;
+    const uint16_t* vring = reinterpret_cast<const uint16_t*>(a.value_ring) + (size_t)seq * a.ring_seq_stride +
+                            (size_t)kvh * a.ring_head_stride;
 
     float q[G][EPL];
 #pragma unroll
@@ -181,13 +195,17 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
 
     for (uint32_t base = w0; base < w1; base += STEP) {
         RowSlice<KDT, EPL> kr[UNROLL];
-        RowSlice<VDT, EPL> vr[UNROLL];
+        typename std::conditional<VDT == I8T, TieredSlice<EPL>, RowSlice<VDT, EPL>>::type vr[UNROLL];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
             const uint32_t row = base + u * RPW + lrow;
             const uint32_t rc = row < w1 ? row : w1 - 1;
             kr[u].template load<NT>(kb + ((size_t)rc * D + lcol) * EB);
-            vr[u].template load<NT>(vb + ((size_t)rc * D + lcol) * VEB);
+            if constexpr (VDT == I8T)
+                vr[u].template load<NT>(reinterpret_cast<const int8_t*>(vb), vsc, vring, rc, a.tier, a.window_mask, D,
+                                        lcol);
+            else
+                vr[u].template load<NT>(vb + ((size_t)rc * D + lcol) * VEB);
         }
         float s[UNROLL][G];
 #pragma unroll
@@ -788,6 +806,8 @@ static int rows_per_wave_load(int head_dim, int key_dtype) {
 static bool valu_path(int key_dtype, int value_dtype) { return key_dtype == F32 || key_dtype != value_dtype; }
 
 bool decode_dtypes_supported(const ShapeDims& s, int key_dtype, int value_dtype) {
+    // tiered values: Granite with fp32 (the reference's proposal keeps K in fp32) or f16 keys
+    if (value_dtype == I8T) return s.head_dim == 64 && s.group == 2 && (key_dtype == F32 || key_dtype == F16);
     if (key_dtype == value_dtype) return true;
     // mixed pairs are the Granite KV plans Fp32KFp16V / Fp16KFp32V (and their bf16 twins)
     return s.head_dim == 64 && s.group == 2 && (key_dtype == F32 || value_dtype == F32);
@@ -886,6 +906,8 @@ static hipError_t launch_decode_impl(const ShapeDims& s, const KvLayer& kv, cons
         else if (kd == F32 && vd == F16) launch_valu<64, 2, F32, F16>(a, grid, st);
         else if (kd == F32 && vd == BF16) launch_valu<64, 2, F32, BF16>(a, grid, st);
         else if (kd == F16 && vd == F32) launch_valu<64, 2, F16, F32>(a, grid, st);
+        else if (kd == F32 && vd == I8T) launch_valu<64, 2, F32, I8T>(a, grid, st);
+        else if (kd == F16 && vd == I8T) launch_valu<64, 2, F16, I8T>(a, grid, st);
         else launch_valu<64, 2, BF16, F32>(a, grid, st);
         if (p.splits > 1)
             hipLaunchKernelGGL((decode_combine_kernel<64, 2>), dim3(s.q_heads * (64 / kCombineDims), units_z), dim3(kCombineThreads), 0, st, a);
@@ -917,6 +939,12 @@ static DecodeArgs decode_args(const ShapeDims& s, const KvLayer& kv, const Decod
     a.query_dtype = query_dtype;
     a.out_dtype = out_dtype;
     a.qscale = s.scale * kLog2e;
+    a.value_scales = kv.value_scales;
+    a.value_ring = kv.value_ring;
+    a.ring_head_stride = kv.ring_head_stride;
+    a.ring_seq_stride = kv.ring_sequence_stride;
+    a.window_mask = kv.window ? kv.window - 1 : 0;
+    a.tier = kv.tier;
     return a;
 }
 
@@ -1008,6 +1036,7 @@ hipError_t launch_decode_causal_rows(const ShapeDims& s, const KvLayer& kv, cons
                                      void* workspace, hipStream_t st, int* dispatches) {
     DecodeArgs a = decode_args(s, kv, p, start + tokens, query, query_dtype, out, out_dtype);
     a.seq_stride = 0;  // every row reads the one sequence of `kv`
+    a.ring_seq_stride = 0;
     a.causal = 1;
     a.causal_start = start;
     return launch_decode_impl(s, kv, p, a, tokens, workspace, st, dispatches);

@@ -27,6 +27,16 @@ struct KvLayer {
     int key_dtype;
     int value_dtype;
     uint32_t capacity;
+    // value_dtype == I8T: `values` holds the INT8 codes (element offsets as
+    // for any dtype); value_scales one f16 per 32 elements at element offset
+    // / 32; value_ring the f16 window, position p of a (sequence, kv head) in
+    // slot p & (window - 1).  Positions below `tier` are INT8.
+    void* value_scales;
+    void* value_ring;
+    uint64_t ring_head_stride;      // elements (window * head_dim)
+    uint64_t ring_sequence_stride;  // elements
+    uint32_t window;                // power of two
+    uint32_t tier;                  // INT8 / f16 boundary of the launch's sequences
 };
 
 struct RopeAppendArgs {
@@ -51,6 +61,20 @@ hipError_t launch_qwen_qk_norm_rope(void* q, void* k, const float* qn, const flo
 hipError_t launch_kv_gather(const ShapeDims& s, const KvLayer& kv, uint32_t pos_begin, uint32_t count, void* keys_out,
                             void* values_out, hipStream_t st);
 hipError_t launch_fill_normal(void* data, int dtype, uint64_t count, uint64_t seed, float stddev, hipStream_t st);
+// tiered_v.hip: value writes of an append of `tokens` rows at `start` to each
+// of `sequences` tiered caches whose boundary moves from kv.tier to new_tier
+// (rows [kv.tier, min(new_tier, start)) leave the window; new rows below
+// new_tier are quantised directly, the rest go to the window)
+hipError_t launch_tiered_value_append(const ShapeDims& s, const KvLayer& kv, uint32_t sequences, uint32_t start,
+                                      uint32_t tokens, uint32_t new_tier, const void* value, int input_dtype,
+                                      hipStream_t st);
+// dequantised f32 value rows [count][kv_heads][d] of one sequence
+hipError_t launch_tiered_value_gather(const ShapeDims& s, const KvLayer& kv, uint32_t pos_begin, uint32_t count,
+                                      float* values_out, hipStream_t st);
+// synthetic tiered values: the f16 values kv_fill_normal writes to an f16
+// cache with the same seed, quantised below max(0, length - window)
+hipError_t launch_tiered_value_fill(const ShapeDims& s, const KvLayer& kv_all_layers_seq0, uint32_t layers,
+                                    uint32_t sequences, uint32_t length, uint64_t seed, hipStream_t st);
 // probe.hip: plain streaming read of `bytes` (a multiple of 16) over `blocks` workgroups
 hipError_t launch_hbm_read_probe(const void* data, uint64_t bytes, uint32_t* sink, uint32_t blocks, hipStream_t st);
 // decode_attention.hip: Granite RoPE + append + attention of one token, one dispatch

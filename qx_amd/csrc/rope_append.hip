@@ -16,6 +16,7 @@
 #include "common.h"
 #include "consensus_math.h"
 #include "internal.h"
+#include "tiered_v.h"
 
 namespace qxh {
 
@@ -48,8 +49,10 @@ __global__ __launch_bounds__(256) void granite_rope_append_kernel(KvLayer kv, Ro
             const float y = load_any(a.key, src + P + pair, a.input_dtype);
             store_any(kv.keys, dst + pair, __builtin_fmaf(-y, sn, x * cs), kv.key_dtype);
             store_any(kv.keys, dst + P + pair, __builtin_fmaf(y, cs, x * sn), kv.key_dtype);
-            store_any(kv.values, dst + pair, load_any(a.value, src + pair, a.input_dtype), kv.value_dtype);
-            store_any(kv.values, dst + P + pair, load_any(a.value, src + P + pair, a.input_dtype), kv.value_dtype);
+            if (kv.values) {  // null: a tiered value cache, written by tiered_v.hip
+                store_any(kv.values, dst + pair, load_any(a.value, src + pair, a.input_dtype), kv.value_dtype);
+                store_any(kv.values, dst + P + pair, load_any(a.value, src + P + pair, a.input_dtype), kv.value_dtype);
+            }
         }
     }
 }
@@ -103,6 +106,7 @@ __global__ __launch_bounds__(256) void qwen_norm_rope_append_kernel(KvLayer kv, 
     const size_t dst = (size_t)s * kv.sequence_stride + (size_t)h * kv.head_stride + (size_t)pos * D;
     store_any(kv.keys, dst + lane, o_l, kv.key_dtype);
     store_any(kv.keys, dst + P + lane, o_r, kv.key_dtype);
+    if (!kv.values) return;  // a tiered value cache, written by tiered_v.hip
     store_any(kv.values, dst + lane, load_any(a.value, base + lane, a.input_dtype), kv.value_dtype);
     store_any(kv.values, dst + P + lane, load_any(a.value, base + P + lane, a.input_dtype), kv.value_dtype);
 }
@@ -120,7 +124,7 @@ __global__ __launch_bounds__(256) void store_kv_kernel(KvLayer kv, RopeAppendArg
         const size_t src = tok * n + i;
         const size_t dst = (size_t)s * kv.sequence_stride + (size_t)h * kv.head_stride + (size_t)pos * head_dim + d;
         store_any(kv.keys, dst, load_any(a.key, src, a.input_dtype), kv.key_dtype);
-        store_any(kv.values, dst, load_any(a.value, src, a.input_dtype), kv.value_dtype);
+        if (kv.values) store_any(kv.values, dst, load_any(a.value, src, a.input_dtype), kv.value_dtype);
     }
 }
 
@@ -152,6 +156,8 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
     x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
     return x ^ (x >> 31);
 }
+
+constexpr uint64_t kValueSeedMix = 0x5DEECE66DA5A5A5Aull;  // value stream of a KV fill
 
 __device__ __forceinline__ void normal_pair(uint64_t seed, uint64_t counter, float& z0, float& z1) {
     const uint64_t h = splitmix64(seed ^ splitmix64(counter));
@@ -193,9 +199,48 @@ __global__ __launch_bounds__(256) void kv_fill_normal_kernel(KvLayer kv, uint64_
         normal_pair(seed, ctr, a, b);
         store_any(kv.keys, off, a, kv.key_dtype);
         store_any(kv.keys, off + 1, b, kv.key_dtype);
-        normal_pair(seed ^ 0x5DEECE66DA5A5A5Aull, ctr, a, b);
+        if (!kv.values) continue;  // tiered values: tiered_fill_kernel
+        normal_pair(kValueSeedMix ^ seed, ctr, a, b);
         store_any(kv.values, off, a, kv.value_dtype);
         store_any(kv.values, off + 1, b, kv.value_dtype);
+    }
+}
+
+// Tiered value fill: one wave per (layer, sequence, kv head, row) with rows
+// below `length`.  Element d of row p of block hb takes the Irwin-Hall sum of
+// the four 16-bit fields of h = splitmix64(seed' ^ splitmix64((hb * capacity
+// + p) * D + d)), centred, times 2^-15 (exact in f32; standard deviation
+// 2 / sqrt(3)), rounded once to f16: integer work and one rounding, so a CPU
+// restates it bit for bit whichever instructions the compiler picks.  The
+// row is quantised when it is below max(0, length - window), else written to
+// its window slot.
+template <int D>
+__global__ __launch_bounds__(256) void tiered_fill_kernel(KvLayer kv, uint64_t rows_total, uint32_t length,
+                                                          uint64_t seed) {
+    constexpr int E = D / 64;
+    const int lane = threadIdx.x & 63;
+    const uint64_t r = blockIdx.x * 4ull + (threadIdx.x >> 6);
+    if (r >= rows_total) return;
+    const uint64_t hb = r / length;
+    const uint32_t row = (uint32_t)(r % length);
+    float v[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const uint64_t h = splitmix64((kValueSeedMix ^ seed) ^ splitmix64((hb * kv.capacity + row) * D + lane * E + e));
+        const int32_t sum = (int32_t)(h & 0xffff) + (int32_t)((h >> 16) & 0xffff) + (int32_t)((h >> 32) & 0xffff) +
+                            (int32_t)(h >> 48) - 131070;
+        v[e] = (float)(half_t)((float)sum * 0x1p-15f);
+    }
+    const uint32_t tier = length > kv.window ? length - kv.window : 0u;
+    if (row < tier) {
+        const size_t off = hb * kv.head_stride + (size_t)row * D;
+        tiered_quantize_row<D>(v, lane, reinterpret_cast<int8_t*>(kv.values) + off,
+                               reinterpret_cast<uint16_t*>(kv.value_scales) + off / kTierBlock);
+    } else {
+        uint16_t* ring = reinterpret_cast<uint16_t*>(kv.value_ring) + hb * kv.ring_head_stride +
+                         (size_t)(row & (kv.window - 1)) * D;
+#pragma unroll
+        for (int e = 0; e < E; ++e) ring[lane * E + e] = f32_to_half_bits(v[e]);
     }
 }
 
@@ -290,6 +335,20 @@ hipError_t launch_kv_fill_normal(const ShapeDims& s, const KvLayer& kv, uint32_t
     if (blocks == 0) blocks = 1;
     hipLaunchKernelGGL(kv_fill_normal_kernel, dim3((unsigned)blocks), dim3(256), 0, st, kv, blocks_hb, s.head_dim,
                        length, seed);
+    return hipGetLastError();
+}
+
+hipError_t launch_tiered_value_fill(const ShapeDims& s, const KvLayer& kv, uint32_t layers, uint32_t sequences,
+                                    uint32_t length, uint64_t seed, hipStream_t st) {
+    const uint64_t rows = (uint64_t)layers * sequences * s.kv_heads * length;
+    if (rows == 0) return hipSuccess;
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    if (s.head_dim == 64)
+        hipLaunchKernelGGL(tiered_fill_kernel<64>, grid, dim3(256), 0, st, kv, rows, length, seed);
+    else if (s.head_dim == 128)
+        hipLaunchKernelGGL(tiered_fill_kernel<128>, grid, dim3(256), 0, st, kv, rows, length, seed);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

@@ -79,8 +79,14 @@ struct qxh_kv_cache {
     bool owned;
     uint64_t head_stride, seq_stride, layer_stride;  // elements
     uint64_t key_region_bytes;
+    // tiered values: byte offsets of the scale and window regions from the
+    // arena base, and the INT8 / f16 boundary of every (layer, sequence)
+    uint64_t scales_offset, ring_offset;
     std::vector<uint32_t> cursor;  // [layer][sequence]
+    std::vector<uint32_t> tier;    // [layer][sequence]
     uint32_t& at(uint32_t layer, uint32_t seq) { return cursor[(size_t)layer * desc.sequences + seq]; }
+    uint32_t& tier_at(uint32_t layer, uint32_t seq) { return tier[(size_t)layer * desc.sequences + seq]; }
+    bool tiered() const { return desc.value_dtype == QXH_I8_TIERED; }
 };
 
 static bool shape_dims(int32_t shape, ShapeDims* d) {
@@ -96,7 +102,7 @@ static bool shape_dims(int32_t shape, ShapeDims* d) {
 }
 
 static bool valid_dtype(int32_t dt) { return dt == QXH_F32 || dt == QXH_F16 || dt == QXH_BF16; }
-static uint32_t dtype_bytes(int32_t dt) { return dt == QXH_F32 ? 4u : 2u; }
+static uint32_t dtype_bytes(int32_t dt) { return dt == QXH_F32 ? 4u : dt == QXH_I8_TIERED ? 1u : 2u; }
 static uint64_t align256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
 
 // Qwen RoPE inverse frequencies formed exactly as the reference CPU path does,
@@ -316,17 +322,37 @@ extern "C" int32_t qxh_replay_destroy(qxh_replay* r) {
 static int32_t check_desc(const qxh_kv_desc* d, ShapeDims* dims) {
     QXH_REQUIRE(d, QXH_ERR_INVALID_ARGUMENT, "null KV descriptor");
     QXH_REQUIRE(shape_dims(d->shape, dims), QXH_ERR_INVALID_ARGUMENT, "unknown shape %d", d->shape);
-    QXH_REQUIRE(valid_dtype(d->key_dtype) && valid_dtype(d->value_dtype), QXH_ERR_INVALID_ARGUMENT,
-                "invalid KV dtype (%d, %d)", d->key_dtype, d->value_dtype);
+    QXH_REQUIRE(valid_dtype(d->key_dtype) && (valid_dtype(d->value_dtype) || d->value_dtype == QXH_I8_TIERED),
+                QXH_ERR_INVALID_ARGUMENT, "invalid KV dtype (%d, %d)", d->key_dtype, d->value_dtype);
     QXH_REQUIRE(d->layers > 0 && d->sequences > 0 && d->capacity > 0, QXH_ERR_INVALID_ARGUMENT,
                 "KV layers, sequences and capacity must be positive");
+    if (d->value_dtype == QXH_I8_TIERED) {
+        const uint32_t w = d->value_window;
+        QXH_REQUIRE(w >= 32 && w <= 65536 && (w & (w - 1)) == 0, QXH_ERR_INVALID_ARGUMENT,
+                    "tiered value window %u is not a power of two in [32, 65536]", w);
+        QXH_REQUIRE(d->shape == QXH_SHAPE_GRANITE && (d->key_dtype == QXH_F32 || d->key_dtype == QXH_F16),
+                    QXH_ERR_UNSUPPORTED, "tiered values are built for the Granite shape with fp32 or f16 keys");
+    } else {
+        QXH_REQUIRE(d->value_window == 0, QXH_ERR_INVALID_ARGUMENT,
+                    "value_window %u is only meaningful for tiered values", d->value_window);
+    }
     return QXH_OK;
 }
 
-static void region_bytes(const qxh_kv_desc* d, const ShapeDims& s, uint64_t* kbytes, uint64_t* vbytes) {
+// Tiered values: INT8 codes (one byte per element), f16 scales (one per 32
+// elements), then the f16 windows [layer][sequence][kv head][window][d].
+static void region_bytes(const qxh_kv_desc* d, const ShapeDims& s, uint64_t* kbytes, uint64_t* vbytes,
+                         uint64_t* scale_bytes = nullptr) {
     const uint64_t elems = (uint64_t)d->layers * d->sequences * s.kv_heads * d->capacity * s.head_dim;
     *kbytes = align256(elems * dtype_bytes(d->key_dtype));
     *vbytes = align256(elems * dtype_bytes(d->value_dtype));
+    if (scale_bytes) *scale_bytes = 0;
+    if (d->value_dtype == QXH_I8_TIERED) {
+        const uint64_t sb = align256(elems / 32 * 2);
+        const uint64_t ring = align256((uint64_t)d->layers * d->sequences * s.kv_heads * d->value_window * s.head_dim * 2);
+        if (scale_bytes) *scale_bytes = sb;
+        *vbytes += sb + ring;
+    }
 }
 
 extern "C" int32_t qxh_kv_cache_bytes(const qxh_kv_desc* desc, uint64_t* bytes) {
@@ -347,8 +373,8 @@ extern "C" int32_t qxh_kv_cache_create(qxh_context* ctx, const qxh_kv_desc* desc
     ShapeDims s;
     int32_t r = check_desc(desc, &s);
     if (r) return r;
-    uint64_t kb, vb;
-    region_bytes(desc, s, &kb, &vb);
+    uint64_t kb, vb, sb;
+    region_bytes(desc, s, &kb, &vb, &sb);
     const uint64_t need = kb + vb;
     bool owned = false;
     if (arena) {
@@ -373,7 +399,11 @@ extern "C" int32_t qxh_kv_cache_create(qxh_context* ctx, const qxh_kv_desc* desc
     c->seq_stride = c->head_stride * s.kv_heads;
     c->layer_stride = c->seq_stride * desc->sequences;
     c->key_region_bytes = kb;
+    const uint64_t codes_bytes = align256((uint64_t)c->layer_stride * desc->layers);
+    c->scales_offset = c->tiered() ? kb + codes_bytes : 0;
+    c->ring_offset = c->tiered() ? kb + codes_bytes + sb : 0;
     c->cursor.assign((size_t)desc->layers * desc->sequences, 0u);
+    c->tier.assign((size_t)desc->layers * desc->sequences, 0u);
     *out = c;
     return QXH_OK;
 }
@@ -400,7 +430,13 @@ extern "C" int32_t qxh_kv_cache_len(const qxh_kv_cache* c, uint32_t layer, uint3
 extern "C" int32_t qxh_kv_cache_reset(qxh_kv_cache* c) {
     QXH_REQUIRE(c, QXH_ERR_INVALID_ARGUMENT, "kv_cache_reset: null cache");
     std::fill(c->cursor.begin(), c->cursor.end(), 0u);
+    std::fill(c->tier.begin(), c->tier.end(), 0u);
     return QXH_OK;
+}
+
+// Boundary after a bulk write of `length` rows (fill, set_len).
+static uint32_t settled_tier(const qxh_kv_cache* c, uint32_t length) {
+    return c->tiered() && length > c->desc.value_window ? length - c->desc.value_window : 0u;
 }
 
 extern "C" int32_t qxh_kv_cache_rollback(qxh_kv_cache* c, uint32_t seq, uint32_t length) {
@@ -409,7 +445,12 @@ extern "C" int32_t qxh_kv_cache_rollback(qxh_kv_cache* c, uint32_t seq, uint32_t
     for (uint32_t l = 0; l < c->desc.layers; ++l)
         QXH_REQUIRE(length <= c->at(l, seq), QXH_ERR_KV_POSITION,
                     "KV rollback checkpoint %u is outside current position %u (layer %u)", length, c->at(l, seq), l);
-    for (uint32_t l = 0; l < c->desc.layers; ++l) c->at(l, seq) = length;
+    for (uint32_t l = 0; l < c->desc.layers; ++l) {
+        c->at(l, seq) = length;
+        // rows [tier, length) keep their window slots: every row written after
+        // them lies less than a window past them
+        c->tier_at(l, seq) = std::min(c->tier_at(l, seq), length);
+    }
     return QXH_OK;
 }
 
@@ -421,7 +462,10 @@ extern "C" int32_t qxh_kv_cache_set_len(qxh_kv_cache* c, uint32_t seq, uint32_t 
                 c->desc.capacity);
     for (uint32_t l = 0; l < c->desc.layers; ++l)
         for (uint32_t s = 0; s < c->desc.sequences; ++s)
-            if (seq == UINT32_MAX || s == seq) c->at(l, s) = length;
+            if (seq == UINT32_MAX || s == seq) {
+                c->at(l, s) = length;
+                c->tier_at(l, s) = settled_tier(c, length);
+            }
     return QXH_OK;
 }
 
@@ -434,6 +478,17 @@ extern "C" int32_t qxh_kv_cache_layout(const qxh_kv_cache* c, qxh_kv_layout* out
     out->layer_stride = c->layer_stride;
     out->key_elem_bytes = dtype_bytes(c->desc.key_dtype);
     out->value_elem_bytes = dtype_bytes(c->desc.value_dtype);
+    out->value_scales = c->tiered() ? c->arena + c->scales_offset : nullptr;
+    out->value_ring = c->tiered() ? c->arena + c->ring_offset : nullptr;
+    out->value_window = c->desc.value_window;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_kv_cache_value_tier(const qxh_kv_cache* c, uint32_t layer, uint32_t seq, uint32_t* boundary) {
+    QXH_REQUIRE(c && boundary, QXH_ERR_INVALID_ARGUMENT, "kv_cache_value_tier: null argument");
+    QXH_REQUIRE(layer < c->desc.layers && seq < c->desc.sequences, QXH_ERR_INVALID_ARGUMENT,
+                "layer %u / sequence %u out of range", layer, seq);
+    *boundary = c->tier[(size_t)layer * c->desc.sequences + seq];
     return QXH_OK;
 }
 
@@ -453,7 +508,47 @@ static KvLayer kv_layer(const qxh_kv_cache* c, uint32_t layer, uint32_t first_se
     k.key_dtype = c->desc.key_dtype;
     k.value_dtype = c->desc.value_dtype;
     k.capacity = c->desc.capacity;
+    if (c->tiered()) {
+        const uint64_t ring_seq = (uint64_t)c->dims.kv_heads * c->desc.value_window * c->dims.head_dim;
+        k.value_scales = c->arena + c->scales_offset + off / 32 * 2;
+        k.value_ring = c->arena + c->ring_offset + ((uint64_t)layer * c->desc.sequences + first_seq) * ring_seq * 2;
+        k.ring_head_stride = (uint64_t)c->desc.value_window * c->dims.head_dim;
+        k.ring_sequence_stride = ring_seq;
+        k.window = c->desc.value_window;
+        k.tier = c->tier[(size_t)layer * c->desc.sequences + first_seq];
+    }
     return k;
+}
+
+// Launches over several sequences of a tiered cache read one boundary.
+static int32_t check_equal_tiers(const qxh_kv_cache* c, uint32_t layer, uint32_t first, uint32_t count) {
+    if (!c->tiered()) return QXH_OK;
+    const uint32_t t0 = c->tier[(size_t)layer * c->desc.sequences + first];
+    for (uint32_t s = first + 1; s < first + count; ++s)
+        QXH_REQUIRE(c->tier[(size_t)layer * c->desc.sequences + s] == t0, QXH_ERR_UNSUPPORTED,
+                    "tiered value boundaries differ across the sequences of one launch (%u at sequence %u, %u at %u)",
+                    t0, first, c->tier[(size_t)layer * c->desc.sequences + s], s);
+    return QXH_OK;
+}
+
+// Entry points whose kernels read or write values in one of the plain dtypes.
+static int32_t reject_tiered(const qxh_kv_cache* c, const char* what) {
+    QXH_REQUIRE(!c || !c->tiered(), QXH_ERR_UNSUPPORTED, "%s does not serve tiered value caches", what);
+    return QXH_OK;
+}
+
+// Value half of an append to a tiered cache, after the key half: moves the
+// boundary of every appended sequence to max(tier, start + tokens - window).
+static hipError_t append_tiered_values(qxh_kv_cache* c, uint32_t layer, uint32_t first, uint32_t count, uint32_t start,
+                                       uint32_t tokens, const void* value, int32_t input_dtype, hipStream_t st) {
+    const KvLayer kv = kv_layer(c, layer, first);
+    const uint64_t end = (uint64_t)start + tokens;
+    const uint32_t w = c->desc.value_window;
+    const uint32_t new_tier = std::max<uint32_t>(kv.tier, end > w ? (uint32_t)(end - w) : 0u);
+    hipError_t e = launch_tiered_value_append(c->dims, kv, count, start, tokens, new_tier, value, input_dtype, st);
+    if (e == hipSuccess)
+        for (uint32_t s = first; s < first + count; ++s) c->tier_at(layer, s) = new_tier;
+    return e;
 }
 
 // ---------------------------------------------------------------------------
@@ -526,9 +621,17 @@ extern "C" int32_t qxh_encode_rope_kv_batch(qxh_graph* g, qxh_kv_cache* c, uint3
     a.sequences = count;
     a.mode = granite ? 0 : 1;
     if (!granite) qwen_inverse_frequencies(a.qwen_inv_freq);
-    hipError_t e = launch_rope_append(c->dims, kv_layer(c, layer, first), a, g->stream);
+    if ((r = check_equal_tiers(c, layer, first, count))) return r;
+    KvLayer kv = kv_layer(c, layer, first);
+    if (c->tiered()) kv.values = nullptr;  // the value half is tiered_v.hip's
+    hipError_t e = launch_rope_append(c->dims, kv, a, g->stream);
     if (e != hipSuccess) return hip_fail(e, "rope_kv launch");
     g->dispatches += 1;
+    if (c->tiered()) {
+        e = append_tiered_values(c, layer, first, count, start, tokens, value, input_dtype, g->stream);
+        if (e != hipSuccess) return hip_fail(e, "tiered value append launch");
+        g->dispatches += 1;
+    }
     advance(c, layer, first, count, tokens);
     return QXH_OK;
 }
@@ -553,6 +656,7 @@ extern "C" int32_t qxh_encode_decode_step_for_layer(qxh_graph* g, qxh_kv_cache* 
                                                     int32_t output_dtype, void* workspace, uint64_t workspace_bytes) {
     int32_t r = check_graph(g);
     if (r) return r;
+    if ((r = reject_tiered(c, "the one-dispatch decode step"))) return r;
     if ((r = check_range(c, layer, 0, 1))) return r;
     QXH_REQUIRE(c->desc.shape == QXH_SHAPE_GRANITE, QXH_ERR_INVALID_ARGUMENT,
                 "decode_step is the Granite single-token entry point");
@@ -604,9 +708,17 @@ extern "C" int32_t qxh_encode_store_kv(qxh_graph* g, qxh_kv_cache* c, uint32_t l
     a.tokens = tokens;
     a.sequences = count;
     a.mode = 2;
-    hipError_t e = launch_rope_append(c->dims, kv_layer(c, layer, first), a, g->stream);
+    if ((r = check_equal_tiers(c, layer, first, count))) return r;
+    KvLayer kv = kv_layer(c, layer, first);
+    if (c->tiered()) kv.values = nullptr;
+    hipError_t e = launch_rope_append(c->dims, kv, a, g->stream);
     if (e != hipSuccess) return hip_fail(e, "store_kv launch");
     g->dispatches += 1;
+    if (c->tiered()) {
+        e = append_tiered_values(c, layer, first, count, start, tokens, value, input_dtype, g->stream);
+        if (e != hipSuccess) return hip_fail(e, "tiered value append launch");
+        g->dispatches += 1;
+    }
     advance(c, layer, first, count, tokens);
     return QXH_OK;
 }
@@ -650,6 +762,7 @@ extern "C" int32_t qxh_encode_attention_for_layer(qxh_graph* g, qxh_kv_cache* c,
     QXH_REQUIRE(decode_dtypes_supported(c->dims, c->desc.key_dtype, c->desc.value_dtype), QXH_ERR_UNSUPPORTED,
                 "decode attention does not serve K dtype %d with V dtype %d for this shape", c->desc.key_dtype,
                 c->desc.value_dtype);
+    if ((r = check_equal_tiers(c, layer, first, count))) return r;
     const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, c->desc.value_dtype, count, length);
     QXH_REQUIRE(workspace_bytes >= p.workspace_bytes && (p.workspace_bytes == 0 || workspace),
                 QXH_ERR_INVALID_ARGUMENT, "attention workspace holds %llu bytes, needs %llu",
@@ -707,9 +820,25 @@ extern "C" int32_t qxh_encode_kv_gather_token_rows(qxh_graph* g, const qxh_kv_ca
     const uint32_t len = c->cursor[(size_t)layer * c->desc.sequences + seq];
     QXH_REQUIRE((uint64_t)begin + count <= len, QXH_ERR_KV_POSITION,
                 "KV position %llu is outside committed length %u", (unsigned long long)begin + count - 1, len);
-    hipError_t e = launch_kv_gather(c->dims, kv_layer(c, layer, seq), begin, count, keys_out, values_out, g->stream);
-    if (e != hipSuccess) return hip_fail(e, "gather launch");
-    g->dispatches += 1;
+    const KvLayer kv = kv_layer(c, layer, seq);
+    hipError_t e = hipSuccess;
+    if (!c->tiered()) {
+        e = launch_kv_gather(c->dims, kv, begin, count, keys_out, values_out, g->stream);
+        if (e != hipSuccess) return hip_fail(e, "gather launch");
+        g->dispatches += 1;
+        return QXH_OK;
+    }
+    // tiered values come back as f32 (dequantised INT8 rows, widened f16 rows)
+    if (keys_out) {
+        e = launch_kv_gather(c->dims, kv, begin, count, keys_out, nullptr, g->stream);
+        if (e != hipSuccess) return hip_fail(e, "gather launch");
+        g->dispatches += 1;
+    }
+    if (values_out) {
+        e = launch_tiered_value_gather(c->dims, kv, begin, count, reinterpret_cast<float*>(values_out), g->stream);
+        if (e != hipSuccess) return hip_fail(e, "tiered value gather launch");
+        g->dispatches += 1;
+    }
     return QXH_OK;
 }
 
@@ -718,6 +847,7 @@ extern "C" int32_t qxh_encode_kv_leaf_hashes(qxh_graph* g, const qxh_kv_cache* c
                                              uint64_t out_bytes) {
     int32_t r = check_graph(g);
     if (r) return r;
+    if ((r = reject_tiered(c, "kv leaf hashing"))) return r;
     QXH_REQUIRE(sequences > 0, QXH_ERR_INVALID_ARGUMENT, "kv leaf hashes of zero sequences");
     if ((r = check_range(c, layer, first_seq, sequences))) return r;
     QXH_REQUIRE(count > 0, QXH_ERR_INVALID_ARGUMENT, "kv leaf hashes of zero rows");
@@ -745,6 +875,7 @@ extern "C" int32_t qxh_encode_verification_hashes(qxh_graph* g, const qxh_kv_cac
                                                   uint32_t interval, void* out, uint64_t out_bytes) {
     int32_t r = check_graph(g);
     if (r) return r;
+    if ((r = reject_tiered(c, "verification hashing"))) return r;
     QXH_REQUIRE(c && residuals && out, QXH_ERR_INVALID_ARGUMENT, "verification hashes: null argument");
     QXH_REQUIRE(layers >= 1 && layers <= c->desc.layers, QXH_ERR_INVALID_ARGUMENT,
                 "verification layer count %u is outside 1..=%u", layers, c->desc.layers);
@@ -828,6 +959,7 @@ extern "C" int32_t qxh_encode_granite_attention_block(qxh_graph* g, qxh_kv_cache
                                                       float* hidden_out, void* workspace, uint64_t workspace_bytes) {
     int32_t r = check_graph(g);
     if (r) return r;
+    if ((r = reject_tiered(c, "the Granite attention block"))) return r;
     if ((r = check_range(c, layer, 0, 1))) return r;
     QXH_REQUIRE(c->desc.shape == QXH_SHAPE_GRANITE, QXH_ERR_INVALID_ARGUMENT, "Granite block needs a Granite cache");
     QXH_REQUIRE(w && w->input_norm && w->q_proj && w->k_proj && w->v_proj && w->o_proj, QXH_ERR_INVALID_ARGUMENT,
@@ -923,6 +1055,7 @@ extern "C" int32_t qxh_encode_granite_attention_block_q4(qxh_graph* g, qxh_kv_ca
                                                          uint64_t workspace_bytes) {
     int32_t r = check_graph(g);
     if (r) return r;
+    if ((r = reject_tiered(c, "the Granite Q4 attention block"))) return r;
     if ((r = check_range(c, layer, 0, 1))) return r;
     QXH_REQUIRE(c->desc.shape == QXH_SHAPE_GRANITE, QXH_ERR_INVALID_ARGUMENT, "Granite block needs a Granite cache");
     QXH_REQUIRE(w && w->input_norm, QXH_ERR_INVALID_ARGUMENT, "granite q4 block: null weights or input norm");
@@ -994,6 +1127,7 @@ extern "C" int32_t qxh_encode_qwen_attention_block(qxh_graph* g, qxh_kv_cache* c
                                                    uint64_t workspace_bytes) {
     int32_t r = check_graph(g);
     if (r) return r;
+    if ((r = reject_tiered(c, "the Qwen attention block"))) return r;
     if ((r = check_range(c, layer, 0, 1))) return r;
     QXH_REQUIRE(c->desc.shape == QXH_SHAPE_QWEN3, QXH_ERR_INVALID_ARGUMENT, "Qwen block needs a Qwen cache");
     QXH_REQUIRE(w && w->input_norm && w->query_norm && w->key_norm && w->post_attention_norm,
@@ -1100,11 +1234,20 @@ extern "C" int32_t qxh_encode_kv_fill_normal(qxh_graph* g, qxh_kv_cache* c, uint
     QXH_REQUIRE(c, QXH_ERR_INVALID_ARGUMENT, "kv_fill_normal: null cache");
     QXH_REQUIRE(length > 0 && length <= c->desc.capacity, QXH_ERR_KV_POSITION, "KV length %u outside (0, %u]", length,
                 c->desc.capacity);
-    hipError_t e = launch_kv_fill_normal(c->dims, kv_layer(c, 0, 0), c->desc.layers, c->desc.sequences,
-                                         c->layer_stride, length, seed, g->stream);
+    KvLayer kv = kv_layer(c, 0, 0);
+    if (c->tiered()) kv.values = nullptr;  // keys here, values by the tiered fill below
+    hipError_t e = launch_kv_fill_normal(c->dims, kv, c->desc.layers, c->desc.sequences, c->layer_stride, length, seed,
+                                         g->stream);
     if (e != hipSuccess) return hip_fail(e, "kv_fill_normal launch");
     g->dispatches += 1;
+    if (c->tiered()) {
+        e = launch_tiered_value_fill(c->dims, kv_layer(c, 0, 0), c->desc.layers, c->desc.sequences, length, seed,
+                                     g->stream);
+        if (e != hipSuccess) return hip_fail(e, "tiered value fill launch");
+        g->dispatches += 1;
+    }
     std::fill(c->cursor.begin(), c->cursor.end(), length);
+    std::fill(c->tier.begin(), c->tier.end(), settled_tier(c, length));
     return QXH_OK;
 }
 

@@ -156,10 +156,10 @@ class KvArena:
     uint8 tensor handed to the library, so torch's allocator owns it."""
 
     def __init__(self, ctx: Context, shape: int, layers: int = 1, sequences: int = 1, capacity: int = 512,
-                 key_dtype: int = F32, value_dtype: int | None = None):
+                 key_dtype: int = F32, value_dtype: int | None = None, value_window: int = 0):
         self.ctx = ctx
         self.desc = abi.KvDesc(shape, key_dtype, key_dtype if value_dtype is None else value_dtype, layers,
-                               sequences, capacity)
+                               sequences, capacity, value_window)
         nbytes = ctypes.c_uint64()
         check(lib().qxh_kv_cache_bytes(ctypes.byref(self.desc), ctypes.byref(nbytes)))
         self.arena = torch.empty(nbytes.value + 256, dtype=torch.uint8, device=f"cuda:{ctx.device}")
@@ -199,12 +199,20 @@ class KvArena:
     def set_len(self, length: int, sequence: int = 0xFFFFFFFF):
         check(lib().qxh_kv_cache_set_len(self._h, sequence, length))
 
+    def value_tier(self, layer: int = 0, sequence: int = 0) -> int:
+        """Tiered values: positions below this boundary are INT8."""
+        n = ctypes.c_uint32()
+        check(lib().qxh_kv_cache_value_tier(self._h, layer, sequence, ctypes.byref(n)))
+        return n.value
+
     def gather(self, graph: Graph, layer: int, sequence: int, begin: int, count: int):
-        """Position-major token rows [count][kv_heads][head_dim] in the cache dtypes."""
+        """Position-major token rows [count][kv_heads][head_dim] in the cache
+        dtypes; tiered values come back as float32."""
         kvh, d = self.info.kv_heads, self.info.head_dim
         dev = f"cuda:{self.ctx.device}"
         k = torch.empty((count, kvh, d), dtype=torch_dtype(self.key_dtype), device=dev)
-        v = torch.empty((count, kvh, d), dtype=torch_dtype(self.value_dtype), device=dev)
+        vdt = F32 if self.value_dtype == abi.I8_TIERED else self.value_dtype
+        v = torch.empty((count, kvh, d), dtype=torch_dtype(vdt), device=dev)
         check(lib().qxh_encode_kv_gather_token_rows(graph.handle, self._h, layer, sequence, begin, count,
                                                     _ptr(k), _ptr(v)))
         return k, v

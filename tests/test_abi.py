@@ -36,7 +36,7 @@ def test_bindings_cover_every_declared_symbol():
 
 def test_abi_version_and_shapes():
     lib = abi.lib()
-    assert lib.qxh_abi_version() == 1
+    assert lib.qxh_abi_version() == 2
     info = abi.ShapeInfo()
     assert lib.qxh_shape_query(abi.SHAPE_GRANITE, ctypes.byref(info)) == 0
     assert (info.q_heads, info.kv_heads, info.head_dim, info.hidden) == (16, 8, 64, 1024)
@@ -70,6 +70,44 @@ def test_kv_arena_bytes_qwen_and_batched():
     desc = abi.KvDesc(abi.SHAPE_GRANITE, abi.F16, abi.F16, 24, 256, 4096)
     assert abi.lib().qxh_kv_cache_bytes(ctypes.byref(desc), ctypes.byref(n)) == 0
     assert n.value == 24 * 256 * 4096 * 8 * 64 * 2 * 2  # 2.147 GB per layer-step x 24
+
+
+def test_tiered_value_arena_bytes():
+    # Granite at ctx 4096 with fp32 K (docs/qx-structural-memory-2026-08-25.md:69-74:
+    # "moving old V from FP16 to INT8 can save roughly another 48 MiB before
+    # scale metadata"): INT8 codes are 48 MiB below the f16 values, then come
+    # one f16 scale per 32 elements and the f16 window
+    n = ctypes.c_uint64()
+    f16v = abi.KvDesc(abi.SHAPE_GRANITE, abi.F32, abi.F16, 24, 1, 4096)
+    assert abi.lib().qxh_kv_cache_bytes(ctypes.byref(f16v), ctypes.byref(n)) == 0
+    base = n.value
+    tiered = abi.KvDesc(abi.SHAPE_GRANITE, abi.F32, abi.I8_TIERED, 24, 1, 4096, 256)
+    assert abi.lib().qxh_kv_cache_bytes(ctypes.byref(tiered), ctypes.byref(n)) == 0
+    elems = 24 * 8 * 4096 * 64
+    assert base - elems * 4 == 2 * elems and 2 * elems - elems == 48 << 20
+    assert n.value == elems * 4 + elems + elems // 32 * 2 + 24 * 8 * 256 * 64 * 2
+    assert base - n.value == (48 << 20) - (3 << 20) - (6 << 20)
+
+
+@pytest.mark.parametrize("shape,kd,window,code", [
+    (abi.SHAPE_GRANITE, abi.F32, 48, abi.QXH_ERR_INVALID_ARGUMENT),   # not a power of two
+    (abi.SHAPE_GRANITE, abi.F32, 16, abi.QXH_ERR_INVALID_ARGUMENT),   # below 32
+    (abi.SHAPE_GRANITE, abi.F32, 0, abi.QXH_ERR_INVALID_ARGUMENT),
+    (abi.SHAPE_QWEN3, abi.F16, 256, abi.QXH_ERR_UNSUPPORTED),
+    (abi.SHAPE_GRANITE, abi.BF16, 256, abi.QXH_ERR_UNSUPPORTED),
+])
+def test_tiered_descriptors_are_validated(shape, kd, window, code):
+    n = ctypes.c_uint64()
+    desc = abi.KvDesc(shape, kd, abi.I8_TIERED, 1, 1, 512, window)
+    assert abi.lib().qxh_kv_cache_bytes(ctypes.byref(desc), ctypes.byref(n)) == code
+    assert "tiered" in abi.last_error()
+
+
+def test_value_window_needs_tiered_values():
+    n = ctypes.c_uint64()
+    desc = abi.KvDesc(abi.SHAPE_GRANITE, abi.F32, abi.F16, 1, 1, 512, 64)
+    assert abi.lib().qxh_kv_cache_bytes(ctypes.byref(desc), ctypes.byref(n)) == abi.QXH_ERR_INVALID_ARGUMENT
+    assert "value_window" in abi.last_error()
 
 
 def test_invalid_descriptors_are_rejected():

@@ -1,0 +1,188 @@
+"""GPU parity for the tiered value cache (QXH_I8_TIERED): recent values in
+f16, older values as INT8 blocks of 32 with f16 scales.  The reference only
+proposes the format (docs/qx-structural-memory-2026-08-25.md:69-74), so the
+check is against the oracle's restatement of this build's definition
+(oracle.TieredValueCache, pinned in tests/test_oracle_tiered_v.py):
+
+- cache contents bit for bit: the synthetic fill against its CPU
+  restatement (oracle.tiered_fill_values); appends (RoPE append and store-only, every input dtype, appends
+  longer than the window) and rollbacks against the tier model;
+- attention (decode, batched decode and causal verifier rows) at the fp32 bar
+  against the oracle fed the values the cache holds, which are exact in f32;
+- the entries that do not serve tiered values refuse them.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from qx_amd import abi
+from qx_amd import runtime as rt
+from tests.helpers import TOL_F32, log, rel_err
+from tests.test_gpu_mixed_kv import attend64, check_fp32_bar
+
+pytestmark = pytest.mark.gpu
+
+KVH, D = 8, 64
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    return rt.Context(0)
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def values(arena, layer, seq, length):
+    with rt.Graph(arena.ctx) as g:
+        kk, vv = arena.gather(g, layer, seq, 0, length)
+    return kk, vv.cpu().numpy()
+
+
+@pytest.mark.parametrize("length", [40, 300])
+def test_tiered_fill_matches_its_restatement(ctx, length):
+    """The synthetic fill: keys as for any cache, values from the integer
+    generator oracle.tiered_fill_values, quantised below length - window."""
+    log("tiered fill", length)
+    W, S, cap = 64, 2, 512
+    plain = rt.KvArena(ctx, abi.SHAPE_GRANITE, 2, S, cap, abi.F32, abi.F16)
+    tiered = rt.KvArena(ctx, abi.SHAPE_GRANITE, 2, S, cap, abi.F32, abi.I8_TIERED, value_window=W)
+    with rt.Graph(ctx) as g:
+        plain.fill_normal(g, seed=11, length=length)
+        tiered.fill_normal(g, seed=11, length=length)
+    for layer in range(2):
+        for seq in range(S):
+            assert tiered.value_tier(layer, seq) == max(0, length - W)
+            k16, _ = values(plain, layer, seq, length)
+            kt, vt = values(tiered, layer, seq, length)
+            assert torch.equal(k16, kt)
+            src = np.stack([O.tiered_fill_values(11, (layer * S + seq) * KVH + h, cap, length)
+                            for h in range(KVH)], axis=1)
+            model = O.TieredValueCache(W)
+            model.append(src.astype(np.float32))
+            assert np.array_equal(vt.view(np.uint32), model.rows().view(np.uint32)), (layer, seq)
+
+
+def test_tiered_appends_and_rollbacks_match_the_model(ctx):
+    W, cap = 32, 600
+    rng = np.random.default_rng(17)
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 2, cap, abi.F32, abi.I8_TIERED, value_window=W)
+    models = [O.TieredValueCache(W), O.TieredValueCache(W)]
+    dtypes = [torch.float32, torch.float16, torch.bfloat16]
+    step = 0
+    for op in range(40):
+        length = arena.len(0, 0)
+        both = arena.len(0, 1) == length and arena.value_tier(0, 0) == arena.value_tier(0, 1)
+        if length and rng.random() < 0.3:
+            seq = int(rng.integers(0, 2))
+            keep = int(rng.integers(0, arena.len(0, seq) + 1))
+            arena.rollback(seq, keep)
+            models[seq].rollback(keep)
+            log(f"op {op}: rollback seq {seq} to {keep}")
+        else:
+            seqs = [0, 1] if both else [int(np.argmin([arena.len(0, 0), arena.len(0, 1)]))]
+            start = arena.len(0, seqs[0])
+            t = int(rng.choice([1, 1, 3, 31, 33, 70]))
+            if start + t > cap:
+                continue
+            dt = dtypes[op % 3]
+            k = torch.randn((len(seqs), t, KVH, D), device="cuda:0").to(dt)
+            v = (torch.randn((len(seqs), t, KVH, D), device="cuda:0") * (0.5 + op)).to(dt)
+            with rt.Graph(ctx) as g:
+                if op % 2:
+                    rt.store_kv(g, arena, 0, start, k, v, first_sequence=seqs[0])
+                else:
+                    rt.rope_kv_batch(g, arena, 0, start, None, k, v, first_sequence=seqs[0])
+            for i, s in enumerate(seqs):
+                models[s].append(v[i].float().cpu().numpy())
+            log(f"op {op}: append {t} at {start} to {seqs} ({dt})")
+        for s in range(2):
+            m = models[s]
+            assert arena.len(0, s) == m.length and arena.value_tier(0, s) == m.boundary, (op, s)
+            if m.length:
+                _, vt = values(arena, 0, s, m.length)
+                assert np.array_equal(vt.view(np.uint32), m.rows().view(np.uint32)), (op, s)
+        step += 1
+    assert step > 20
+
+
+@pytest.mark.parametrize("kdt", [abi.F32, abi.F16])
+@pytest.mark.parametrize("length", [1, 300, 4096])
+def test_tiered_decode_matches_oracle(ctx, kdt, length):
+    log("tiered decode", kdt, length)
+    rng = np.random.default_rng(length + kdt)
+    S, W = 2, 256
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, S, 4096, kdt, abi.I8_TIERED, value_window=W)
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=length + 5, length=length)
+    q = dev(rng.standard_normal((S, 16, 64), dtype=np.float32))
+    with rt.Graph(ctx) as g:
+        out = rt.attention(g, arena, 0, q, length)
+    for s in range(S):
+        kk, vf = values(arena, 0, s, length)
+        kf = kk.float().cpu().numpy()
+        ref_cache = O.KvCache(4096)
+        ref_cache.extend(kf, vf)
+        qs = q[s].cpu().numpy()
+        ref = O.granite_attend(qs.ravel(), ref_cache, length)
+        e = check_fp32_bar(out[s].cpu().numpy().ravel(), ref, attend64(qs, kf, vf, 0.015625).ravel())
+        log(f"  seq {s}: {e:.2e}")
+
+
+@pytest.mark.parametrize("start,tokens", [(0, 4), (500, 4), (1000, 40)])
+def test_tiered_causal_rows_match_oracle(ctx, start, tokens):
+    """Verifier rows over a tiered cache whose last rows were appended by the
+    RoPE append (and, for 40 rows past a window of 32, partly quantised on
+    the way in)."""
+    log("tiered causal rows", start, tokens)
+    rng = np.random.default_rng(start + tokens)
+    W = 32
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, 1200, abi.F32, abi.I8_TIERED, value_window=W)
+    if start:
+        with rt.Graph(ctx) as g:
+            arena.fill_normal(g, seed=13, length=start)
+    k = dev(rng.standard_normal((1, tokens, KVH, D), dtype=np.float32))
+    v = dev(rng.standard_normal((1, tokens, KVH, D), dtype=np.float32))
+    with rt.Graph(ctx) as g:
+        rt.rope_kv_batch(g, arena, 0, start, None, k, v)
+    assert arena.value_tier() == max(0, start + tokens - W)
+    kk, vf = values(arena, 0, 0, start + tokens)
+    ref = O.KvCache(1200)
+    ref.extend(kk.cpu().numpy(), vf)
+    q = rng.standard_normal((tokens, 16, 64), dtype=np.float32)
+    with rt.Graph(ctx) as g:
+        out = rt.prefill_attention(g, arena, 0, start, dev(q))
+    r = O.granite_prefill_rows(q.reshape(tokens, -1), ref, start, np.arange(tokens))
+    e = rel_err(out.cpu().numpy().reshape(tokens, -1), r)
+    log(f"  causal rows max-abs/rms {e:.2e}")
+    assert e <= TOL_F32
+
+
+def test_tiered_values_are_refused_where_unsupported(ctx):
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 2, 256, abi.F32, abi.I8_TIERED, value_window=32)
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=3, length=100)
+    q = torch.zeros((16, 64), device="cuda:0")
+    kv = torch.zeros((8, 64), device="cuda:0")
+    with rt.Graph(ctx) as g:
+        with pytest.raises(abi.QxhError, match="tiered"):
+            rt.decode_step(g, arena, 0, 100, q, kv, kv)
+        with pytest.raises(abi.QxhError, match="tiered"):
+            arena.leaf_hashes(g, 0, 0, 4)
+    # sequences whose boundaries differ cannot share a launch: sequence 0
+    # rolled back to 50 and refilled to 60 keeps boundary 50, sequence 1
+    # rolled back from 100 to 60 has boundary min(68, 60)
+    arena.rollback(0, 50)
+    with rt.Graph(ctx) as g:
+        k = torch.zeros((1, 10, KVH, D), device="cuda:0")
+        rt.store_kv(g, arena, 0, 50, k, k)
+    arena.rollback(1, 60)
+    assert arena.len(0, 0) == arena.len(0, 1) == 60
+    assert arena.value_tier(0, 0) == 50 and arena.value_tier(0, 1) == 60
+    with rt.Graph(ctx) as g:
+        with pytest.raises(abi.QxhError, match="boundaries differ"):
+            rt.attention(g, arena, 0, torch.zeros((2, 16, 64), device="cuda:0"), 60)
+        out = rt.attention(g, arena, 0, torch.zeros((1, 16, 64), device="cuda:0"), 60, first_sequence=1)
+    assert torch.isfinite(out).all()
