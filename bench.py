@@ -65,10 +65,10 @@ def roofline_hbm(bytes_per_launch, ms_per_launch, traffic=None):
 
 
 # ---------------------------------------------------------------------------
-# Achievable HBM on this box: a plain streaming read (a torch reduction over
-# 2 GiB, far beyond the 256 MB MALL) and a 1 GiB copy, timed like the rest,
-# so the decode rooflines can be read against the measured ceiling as well as
-# the 8 TB/s specification.
+# Achievable HBM on this box: a plain streaming read of 2 GiB (far beyond the
+# 256 MB MALL) by the library's probe kernel, timed like the rest, so the
+# decode rooflines can be read against the measured ceiling as well as the
+# 8 TB/s specification.
 # ---------------------------------------------------------------------------
 def bench_hbm_probe(ctx, steps, warmup):
     import torch
@@ -137,6 +137,51 @@ def bench_cfg4(ctx, steps, warmup):
     }
     del arena
     torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------------------
+# Tiered values: Granite batched decode at ctx 4096 on the reference's
+# canonical KV plan (fp32 K, f16 V) and on fp32 K with tiered values (f16
+# window of 256, INT8 blocks before it), same shape, same kernel family.
+# ---------------------------------------------------------------------------
+def bench_tiered_v(ctx, steps, warmup):
+    import torch
+    from qx_amd import abi
+    from qx_amd import runtime as rt
+
+    S, L, LAYERS, W = 64, 4096, 8, 256
+    stream = torch.cuda.current_stream()
+    q = torch.empty((LAYERS, S, 16, 64), device="cuda:0")
+    out = torch.empty_like(q)
+    with rt.Graph(ctx, stream) as g:
+        rt.fill_normal(g, q, seed=45)
+    res = {"shape": f"{S} sequences x ctx {L}, Granite, {LAYERS} layers", "window": W}
+    k_bytes = S * 8 * L * 64 * 4
+    io_bytes = 2 * S * 16 * 64 * 4
+    plans = (("fp32k_f16v", abi.F16, 0, S * 8 * L * 64 * 2),
+             ("fp32k_tiered", abi.I8_TIERED, W, S * 8 * ((L - W) * (64 + 4) + W * 64 * 2)))
+    for name, vdt, window, v_bytes in plans:
+        arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, LAYERS, S, L, abi.F32, vdt, value_window=window)
+        with rt.Graph(ctx, stream) as g:
+            arena.fill_normal(g, seed=4, length=L)
+        ws = torch.empty(max(rt.attention_workspace_bytes(arena, S, L), 1), dtype=torch.uint8, device="cuda:0")
+        g = rt.Graph(ctx, stream)
+
+        def step():
+            for layer in range(LAYERS):
+                rt.attention(g, arena, layer, q[layer], L, out=out[layer], workspace=ws)
+
+        ms = timed(step, steps, warmup, stream)
+        g.finish()
+        per_launch_ms = ms / LAYERS
+        nbytes = k_bytes + v_bytes + io_bytes
+        res[name] = {"us_per_layer_step": round(per_launch_ms * 1000.0, 2), "bytes_per_launch": nbytes,
+                     "arena_bytes": arena.arena.numel() - 256,
+                     "roofline": roofline_hbm(nbytes, per_launch_ms)}
+        del arena, ws
+        torch.cuda.empty_cache()
+    res["speedup"] = round(res["fp32k_f16v"]["us_per_layer_step"] / res["fp32k_tiered"]["us_per_layer_step"], 3)
     return res
 
 
@@ -519,7 +564,7 @@ def run(ctx, args):
                          ("cfg2q4", lambda c, k, w: bench_cfg2(c, k, w, q4=True)),
                          ("cfg3", lambda c, k, w: bench_prefill(c, k, w, "cfg3")),
                          ("cfg5a", bench_cfg5a), ("qwenblock", bench_qwen_block), ("cfg5b", lambda c, k, w: bench_prefill(c, k, w, "cfg5b")),
-                         ("kvhash", bench_kv_hash)):
+                         ("kvhash", bench_kv_hash), ("tieredv", bench_tiered_v)):
             if only and name not in only:
                 continue
             try:

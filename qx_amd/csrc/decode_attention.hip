@@ -193,59 +193,77 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
         for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
     }
 
-    for (uint32_t base = w0; base < w1; base += STEP) {
-        RowSlice<KDT, EPL> kr[UNROLL];
-        typename std::conditional<VDT == I8T, TieredSlice<EPL>, RowSlice<VDT, EPL>>::type vr[UNROLL];
+    // One online-softmax pass over rows [begin, end).  TIER selects where the
+    // value rows come from: 0 the plain value dtype, 1 the INT8 tier, 2 the f16
+    // window of a tiered cache (the two tiered passes split the rows at the
+    // boundary, so no load carries a per-row tier test).
+    auto pass = [&](uint32_t begin, uint32_t end, auto tier_tag) {
+        constexpr int TIER = decltype(tier_tag)::value;
+        using VSlice = typename std::conditional<
+            TIER == 1, TieredCodes<EPL>,
+            typename std::conditional<TIER == 2, RowSlice<F16, EPL>, RowSlice<VDT, EPL>>::type>::type;
+        for (uint32_t base = begin; base < end; base += STEP) {
+            RowSlice<KDT, EPL> kr[UNROLL];
+            VSlice vr[UNROLL];
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            const uint32_t row = base + u * RPW + lrow;
-            const uint32_t rc = row < w1 ? row : w1 - 1;
-            kr[u].template load<NT>(kb + ((size_t)rc * D + lcol) * EB);
-            if constexpr (VDT == I8T)
-                vr[u].template load<NT>(reinterpret_cast<const int8_t*>(vb), vsc, vring, rc, a.tier, a.window_mask, D,
-                                        lcol);
-            else
-                vr[u].template load<NT>(vb + ((size_t)rc * D + lcol) * VEB);
-        }
-        float s[UNROLL][G];
+            for (int u = 0; u < UNROLL; ++u) {
+                const uint32_t row = base + u * RPW + lrow;
+                const uint32_t rc = row < end ? row : end - 1;
+                kr[u].template load<NT>(kb + ((size_t)rc * D + lcol) * EB);
+                if constexpr (TIER == 1)
+                    vr[u].template load<NT>(reinterpret_cast<const int8_t*>(vb), vsc, rc, D, lcol);
+                else if constexpr (TIER == 2)
+                    vr[u].template load<NT>(reinterpret_cast<const char*>(vring + (size_t)(rc & a.window_mask) * D + lcol));
+                else
+                    vr[u].template load<NT>(vb + ((size_t)rc * D + lcol) * VEB);
+            }
+            float s[UNROLL][G];
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            float kf[EPL];
-            kr[u].unpack(kf);
-            const bool valid = base + u * RPW + lrow < w1;
+            for (int u = 0; u < UNROLL; ++u) {
+                float kf[EPL];
+                kr[u].unpack(kf);
+                const bool valid = base + u * RPW + lrow < end;
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    float d = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) d = __builtin_fmaf(q[g][e], kf[e], d);
+                    d = group_sum<LPR>(d);
+                    s[u][g] = valid ? d : -INFINITY;
+                }
+            }
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                float d = 0.0f;
+                float mb = s[0][g];
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) d = __builtin_fmaf(q[g][e], kf[e], d);
-                d = group_sum<LPR>(d);
-                s[u][g] = valid ? d : -INFINITY;
+                for (int u = 1; u < UNROLL; ++u) mb = fmaxf(mb, s[u][g]);
+                const float mn = fmaxf(m[g], mb);
+                const float alpha = fast_exp2(m[g] - mn);
+                m[g] = mn;
+                l[g] *= alpha;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
+            }
+#pragma unroll
+            for (int u = 0; u < UNROLL; ++u) {
+                float vf[EPL];
+                vr[u].unpack(vf);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float p = fast_exp2(s[u][g] - m[g]);
+                    l[g] += p;
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) acc[g][e] = __builtin_fmaf(p, vf[e], acc[g][e]);
+                }
             }
         }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float mb = s[0][g];
-#pragma unroll
-            for (int u = 1; u < UNROLL; ++u) mb = fmaxf(mb, s[u][g]);
-            const float mn = fmaxf(m[g], mb);
-            const float alpha = fast_exp2(m[g] - mn);
-            m[g] = mn;
-            l[g] *= alpha;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
-        }
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            float vf[EPL];
-            vr[u].unpack(vf);
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float p = fast_exp2(s[u][g] - m[g]);
-                l[g] += p;
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) acc[g][e] = __builtin_fmaf(p, vf[e], acc[g][e]);
-            }
-        }
+    };
+    if constexpr (VDT == I8T) {
+        const uint32_t cut = min(max(a.tier, w0), w1);
+        pass(w0, cut, std::integral_constant<int, 1>{});
+        pass(cut, w1, std::integral_constant<int, 2>{});
+    } else {
+        pass(w0, w1, std::integral_constant<int, 0>{});
     }
 
     // merge the RPW row groups of the wave (lanes sharing lcol)

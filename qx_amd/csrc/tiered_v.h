@@ -46,61 +46,35 @@ __device__ __forceinline__ void tiered_quantize_row(const float (&v)[D / 64], in
 
 typedef uint32_t tv_u32x2 __attribute__((ext_vector_type(2)));
 
-// N consecutive value elements of one row, read from whichever tier holds the
-// row: N INT8 codes plus the block's scale, or N f16 values of the window.
-// The lane layout is the key's (N = 16 bytes of K), as for RowSlice.
-template <int N> struct TieredSlice {
+// N consecutive INT8-tier elements of one row (N codes and the scale of their
+// block), in the key's lane layout (N = 16 bytes of K).  Rows of the f16
+// window are read as plain f16 slices.
+template <int N> struct TieredCodes {
     static_assert(N == 4 || N == 8, "4 or 8 elements per lane");
-    uint32_t w[N / 2];
-    float scale;  // >= 0: w holds INT8 codes; -1: w holds f16 values
+    uint32_t w[N / 4];
+    float scale;
     template <bool NT>
-    __device__ __forceinline__ void load(const int8_t* codes, const uint16_t* scales, const uint16_t* ring,
-                                         uint32_t row, uint32_t tier, uint32_t window_mask, int d, int lcol) {
-        if (row < tier) {
-            const size_t e = (size_t)row * d + lcol;
-            if constexpr (N == 4) {
-                const uint32_t* p = reinterpret_cast<const uint32_t*>(codes + e);
-                if constexpr (NT) w[0] = __builtin_nontemporal_load(p);
-                else w[0] = *p;
-            } else {
-                const tv_u32x2* p = reinterpret_cast<const tv_u32x2*>(codes + e);
-                tv_u32x2 v;
-                if constexpr (NT) v = __builtin_nontemporal_load(p);
-                else v = *p;
-                w[0] = v[0];
-                w[1] = v[1];
-            }
-            scale = half_bits_to_f32(scales[e / kTierBlock]);
+    __device__ __forceinline__ void load(const int8_t* codes, const uint16_t* scales, uint32_t row, int d, int lcol) {
+        const size_t e = (size_t)row * d + lcol;
+        if constexpr (N == 4) {
+            const uint32_t* p = reinterpret_cast<const uint32_t*>(codes + e);
+            if constexpr (NT) w[0] = __builtin_nontemporal_load(p);
+            else w[0] = *p;
         } else {
-            const uint16_t* p = ring + (size_t)(row & window_mask) * d + lcol;
-            if constexpr (N == 4) {
-                const tv_u32x2* q = reinterpret_cast<const tv_u32x2*>(p);
-                tv_u32x2 v;
-                if constexpr (NT) v = __builtin_nontemporal_load(q);
-                else v = *q;
-                w[0] = v[0];
-                w[1] = v[1];
-            } else {
-                const u32x4 v = load16<NT>(p);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) w[j] = v[j];
-            }
-            scale = -1.0f;
+            const tv_u32x2* p = reinterpret_cast<const tv_u32x2*>(codes + e);
+            tv_u32x2 v;
+            if constexpr (NT) v = __builtin_nontemporal_load(p);
+            else v = *p;
+            w[0] = v[0];
+            w[1] = v[1];
         }
+        scale = half_bits_to_f32(scales[e / kTierBlock]);
     }
     __device__ __forceinline__ void unpack(float (&out)[N]) const {
-        if (scale >= 0.0f) {
 #pragma unroll
-            for (int i = 0; i < N; ++i) {
-                const int32_t c = (int32_t)(w[i >> 2] << (24 - 8 * (i & 3))) >> 24;
-                out[i] = (float)c * scale;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < N / 2; ++i) {
-                out[2 * i] = half_bits_to_f32((uint16_t)(w[i] & 0xffffu));
-                out[2 * i + 1] = half_bits_to_f32((uint16_t)(w[i] >> 16));
-            }
+        for (int i = 0; i < N; ++i) {
+            const int32_t c = (int32_t)(w[i >> 2] << (24 - 8 * (i & 3))) >> 24;
+            out[i] = (float)c * scale;
         }
     }
 };
