@@ -33,6 +33,7 @@ struct KvLayer {
     // slot p & (window - 1).  Positions below `tier` are INT8.
     void* value_scales;
     void* value_ring;
+    uint32_t* value_tags;           // position each window slot holds, [sequence][kv head][window]
     uint64_t ring_head_stride;      // elements (window * head_dim)
     uint64_t ring_sequence_stride;  // elements
     uint32_t window;                // power of two

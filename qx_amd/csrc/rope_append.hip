@@ -241,6 +241,7 @@ __global__ __launch_bounds__(256) void tiered_fill_kernel(KvLayer kv, uint64_t r
                          (size_t)(row & (kv.window - 1)) * D;
 #pragma unroll
         for (int e = 0; e < E; ++e) ring[lane * E + e] = f32_to_half_bits(v[e]);
+        if (lane == 0) kv.value_tags[hb * kv.window + (row & (kv.window - 1))] = row;
     }
 }
 

@@ -81,7 +81,7 @@ struct qxh_kv_cache {
     uint64_t key_region_bytes;
     // tiered values: byte offsets of the scale and window regions from the
     // arena base, and the INT8 / f16 boundary of every (layer, sequence)
-    uint64_t scales_offset, ring_offset;
+    uint64_t scales_offset, ring_offset, tags_offset;
     std::vector<uint32_t> cursor;  // [layer][sequence]
     std::vector<uint32_t> tier;    // [layer][sequence]
     uint32_t& at(uint32_t layer, uint32_t seq) { return cursor[(size_t)layer * desc.sequences + seq]; }
@@ -340,7 +340,8 @@ static int32_t check_desc(const qxh_kv_desc* d, ShapeDims* dims) {
 }
 
 // Tiered values: INT8 codes (one byte per element), f16 scales (one per 32
-// elements), then the f16 windows [layer][sequence][kv head][window][d].
+// elements), the f16 windows [layer][sequence][kv head][window][d], then one
+// u32 tag per window slot (the position the slot holds).
 static void region_bytes(const qxh_kv_desc* d, const ShapeDims& s, uint64_t* kbytes, uint64_t* vbytes,
                          uint64_t* scale_bytes = nullptr) {
     const uint64_t elems = (uint64_t)d->layers * d->sequences * s.kv_heads * d->capacity * s.head_dim;
@@ -349,9 +350,10 @@ static void region_bytes(const qxh_kv_desc* d, const ShapeDims& s, uint64_t* kby
     if (scale_bytes) *scale_bytes = 0;
     if (d->value_dtype == QXH_I8_TIERED) {
         const uint64_t sb = align256(elems / 32 * 2);
-        const uint64_t ring = align256((uint64_t)d->layers * d->sequences * s.kv_heads * d->value_window * s.head_dim * 2);
+        const uint64_t slots = (uint64_t)d->layers * d->sequences * s.kv_heads * d->value_window;
+        const uint64_t ring = align256(slots * s.head_dim * 2);
         if (scale_bytes) *scale_bytes = sb;
-        *vbytes += sb + ring;
+        *vbytes += sb + ring + align256(slots * 4);
     }
 }
 
@@ -402,6 +404,10 @@ extern "C" int32_t qxh_kv_cache_create(qxh_context* ctx, const qxh_kv_desc* desc
     const uint64_t codes_bytes = align256((uint64_t)c->layer_stride * desc->layers);
     c->scales_offset = c->tiered() ? kb + codes_bytes : 0;
     c->ring_offset = c->tiered() ? kb + codes_bytes + sb : 0;
+    c->tags_offset = c->tiered() ? c->ring_offset +
+                                       align256((uint64_t)desc->layers * desc->sequences * s.kv_heads *
+                                                desc->value_window * s.head_dim * 2)
+                                 : 0;
     c->cursor.assign((size_t)desc->layers * desc->sequences, 0u);
     c->tier.assign((size_t)desc->layers * desc->sequences, 0u);
     *out = c;
@@ -512,6 +518,8 @@ static KvLayer kv_layer(const qxh_kv_cache* c, uint32_t layer, uint32_t first_se
         const uint64_t ring_seq = (uint64_t)c->dims.kv_heads * c->desc.value_window * c->dims.head_dim;
         k.value_scales = c->arena + c->scales_offset + off / 32 * 2;
         k.value_ring = c->arena + c->ring_offset + ((uint64_t)layer * c->desc.sequences + first_seq) * ring_seq * 2;
+        k.value_tags = reinterpret_cast<uint32_t*>(c->arena + c->tags_offset) +
+                       ((uint64_t)layer * c->desc.sequences + first_seq) * c->dims.kv_heads * c->desc.value_window;
         k.ring_head_stride = (uint64_t)c->desc.value_window * c->dims.head_dim;
         k.ring_sequence_stride = ring_seq;
         k.window = c->desc.value_window;

@@ -10,8 +10,12 @@
 // A slot can be read (a row leaving) and written (a new row) by the same
 // append, so one wave owns each slot that the append touches and handles its
 // rows in ascending position order: the read of the leaving row is consumed
-// before the new row's store is issued.  Every row passes through f16 before
-// quantisation, so a row's codes do not depend on when it leaves the window.
+// before the new row's store is issued.  Each slot carries a tag, the position
+// it holds, and a row leaves only if its slot still holds it: a captured
+// append replayed after a rollback to its start finds its leaving row's slot
+// taken by the rolled-back row and keeps the codes the first run wrote.
+// Every row passes through f16 before quantisation, so a row's codes do not
+// depend on when it leaves the window.
 // The work is a few rows per (sequence, kv head), latency-bound.
 #include "common.h"
 #include "internal.h"
@@ -25,6 +29,7 @@ struct TieredAppendArgs {
     int8_t* codes;            // layer base of the first sequence
     uint16_t* scales;         // element offset / 32
     uint16_t* ring;
+    uint32_t* tags;           // [sequence][kv_heads][window]
     const void* value;        // [sequence][tokens][kv_heads][d]
     uint64_t head_stride;     // elements
     uint64_t seq_stride;
@@ -62,9 +67,11 @@ __global__ __launch_bounds__(256) void tiered_value_append_kernel(TieredAppendAr
     int8_t* codes = a.codes + base;
     uint16_t* scales = a.scales + base / kTierBlock;
     uint16_t* ring = a.ring + (size_t)s * a.ring_seq_stride + (size_t)h * a.ring_head_stride + (size_t)slot * D;
+    uint32_t* tag = a.tags + ((size_t)s * kv_heads + h) * a.window + slot;
     // rows leaving the window (at most one per slot)
     const uint32_t leave_end = a.tier + a.leaving;
     for (uint32_t p = a.tier + ((slot - a.tier) & mask); p < leave_end; p += a.window) {
+        if (__hip_atomic_load(tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != p) continue;  // left already
         float v[E];
 #pragma unroll
         for (int e = 0; e < E; ++e) v[e] = half_bits_to_f32(ring[lane * E + e]);
@@ -83,6 +90,7 @@ __global__ __launch_bounds__(256) void tiered_value_append_kernel(TieredAppendAr
         } else {
 #pragma unroll
             for (int e = 0; e < E; ++e) ring[lane * E + e] = f32_to_half_bits(v[e]);
+            if (lane == 0) *tag = p;
         }
     }
 }
@@ -119,6 +127,7 @@ hipError_t launch_tiered_value_append(const ShapeDims& s, const KvLayer& kv, uin
     a.codes = reinterpret_cast<int8_t*>(kv.values);
     a.scales = reinterpret_cast<uint16_t*>(kv.value_scales);
     a.ring = reinterpret_cast<uint16_t*>(kv.value_ring);
+    a.tags = kv.value_tags;
     a.value = value;
     a.head_stride = kv.head_stride;
     a.seq_stride = kv.sequence_stride;

@@ -85,8 +85,9 @@ def test_tiered_value_arena_bytes():
     assert abi.lib().qxh_kv_cache_bytes(ctypes.byref(tiered), ctypes.byref(n)) == 0
     elems = 24 * 8 * 4096 * 64
     assert base - elems * 4 == 2 * elems and 2 * elems - elems == 48 << 20
-    assert n.value == elems * 4 + elems + elems // 32 * 2 + 24 * 8 * 256 * 64 * 2
-    assert base - n.value == (48 << 20) - (3 << 20) - (6 << 20)
+    slots = 24 * 8 * 256  # window rows, each with a 4-byte position tag
+    assert n.value == elems * 4 + elems + elems // 32 * 2 + slots * 64 * 2 + slots * 4
+    assert base - n.value == (48 << 20) - (3 << 20) - (6 << 20) - slots * 4
 
 
 @pytest.mark.parametrize("shape,kd,window,code", [

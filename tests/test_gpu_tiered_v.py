@@ -160,6 +160,53 @@ def test_tiered_causal_rows_match_oracle(ctx, start, tokens):
     assert e <= TOL_F32
 
 
+def test_tiered_graph_replay_after_rollback(ctx):
+    """A captured append + decode replayed after rolling back to its start:
+    the row that left the window in the first replay has its slot taken by
+    the appended row, so later replays must keep its codes (the slot tags)."""
+    W, L = 32, 100
+    rng = np.random.default_rng(23)
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, 256, abi.F32, abi.I8_TIERED, value_window=W)
+    side = torch.cuda.Stream()
+    k = dev(rng.standard_normal((1, 1, KVH, D), dtype=np.float32))
+    v = dev(rng.standard_normal((1, 1, KVH, D), dtype=np.float32))
+    q = dev(rng.standard_normal((1, 16, 64), dtype=np.float32))
+    out = torch.empty_like(q)
+    ws = torch.empty(max(rt.attention_workspace_bytes(arena, 1, L + 1), 1), dtype=torch.uint8, device="cuda:0")
+    model = O.TieredValueCache(W)
+    model.append(np.stack([O.tiered_fill_values(3, h, 256, L) for h in range(KVH)], axis=1).astype(np.float32))
+    model.append(v[0].cpu().numpy())
+    with torch.cuda.stream(side):
+        with rt.Graph(ctx, side) as g:
+            arena.fill_normal(g, seed=3, length=L)
+        side.synchronize()
+        g = rt.Graph(ctx, side)
+        g.capture_begin()
+        rt.rope_kv_batch(g, arena, 0, L, None, k, v)
+        rt.attention(g, arena, 0, q, L + 1, out=out, workspace=ws)
+        replay = g.capture_end()
+        g.discard()
+        first = None
+        for i in range(3):
+            out.zero_()
+            side.synchronize()
+            replay.launch(side)
+            side.synchronize()
+            if first is None:
+                first = out.clone()
+            assert torch.equal(out, first), i
+            _, vt = values(arena, 0, 0, L + 1)
+            assert arena.value_tier() == model.boundary == L + 1 - W
+            assert np.array_equal(vt.view(np.uint32), model.rows().view(np.uint32)), i
+            arena.rollback(0, L)
+            arena.set_len(L + 1)  # the replay wrote row L again; the boundary settles at L + 1 - W
+        del replay
+    kk, vf = values(arena, 0, 0, L + 1)
+    ref = O.KvCache(256)
+    ref.extend(kk.cpu().numpy(), vf)
+    assert rel_err(first.cpu().numpy().ravel(), O.granite_attend(q.cpu().numpy().ravel(), ref, L + 1)) <= TOL_F32
+
+
 def test_tiered_values_are_refused_where_unsupported(ctx):
     arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 2, 256, abi.F32, abi.I8_TIERED, value_window=32)
     with rt.Graph(ctx) as g:
