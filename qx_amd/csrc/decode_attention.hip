@@ -707,32 +707,43 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
 }
 
 // Reduce the per-split partials: out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
-// grid (q_heads x D/32, sequences), block 1024: one workgroup per 32 dims of
-// a head.  The reduction is latency-bound (a
-// few hundred KB per launch), so every partial a thread needs is requested in
-// one round: thread (sub, d4) loads (m, l) and the float4 column d4 of acc for
-// splits sub, sub + NSUB, ... (up to kBatch at a time), folds them into a
-// running (m, l, acc) of its own, and the NSUB running states of a column are
-// then merged through LDS with the same rule.
+// grid (q_heads x D/32, sequences), block 256: one workgroup per 32 dims of a
+// head.  The reduction is latency-bound (a few hundred KB to a few MB per
+// launch), so every partial a thread needs is requested in one round: thread
+// (sub, c4) of the 32 subs x 8 float4 columns folds splits sub, sub + 32, ...
+// (up to kBatch at a time) into a running (m, l, acc); the 8 subs of a wave
+// then merge by xor shuffles over the lane bits that number them, and the 4
+// waves through LDS, with one barrier.
 constexpr int kMaxSplits = 1024;
-constexpr int kCombineThreads = 1024;
+constexpr int kCombineThreads = 256;
 
 constexpr int kCombineDims = 32;  // dims of one head per combine workgroup
 
+__device__ __forceinline__ void merge_partial(float& M, float& L, f32x4& A, float Mo, float Lo, f32x4 Ao) {
+    const float mn = fmaxf(M, Mo);
+    const float f0 = fast_exp2(M - mn), f1 = fast_exp2(Mo - mn);
+    L = __builtin_fmaf(L, f0, Lo * f1);
+    A = A * f0 + Ao * f1;
+    M = mn;
+}
+
 template <int D, int G>
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeArgs a) {
-    constexpr int D4 = kCombineDims / 4;
-    constexpr int NSUB = kCombineThreads / D4;
+    constexpr int D4 = kCombineDims / 4;          // float4 columns per workgroup
+    constexpr int WAVES = kCombineThreads / 64;
+    constexpr int NSUB = kCombineThreads / D4;    // 32
     constexpr int kBatch = 4;
     constexpr int DSPLIT = D / kCombineDims;
-    __shared__ float sm_m[NSUB], sm_l[NSUB];
-    __shared__ f32x4 sm_acc[NSUB][D4];
+    __shared__ float sm_m[WAVES][D4], sm_l[WAVES][D4];
+    __shared__ f32x4 sm_acc[WAVES][D4];
     const uint32_t hq = blockIdx.x / DSPLIT, dpart = blockIdx.x % DSPLIT, seq = blockIdx.y;
     const uint32_t q_heads = gridDim.x / DSPLIT;
     const uint32_t hkv = q_heads / G;
     const uint32_t kvh = hq / G, g = hq % G;
-    const int t = threadIdx.x;
-    const int d4 = (int)dpart * D4 + t % D4, sub = t / D4;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int c4 = lane % D4;
+    const int sub = wave * (64 / D4) + lane / D4;
+    const int d4 = (int)dpart * D4 + c4;
     const uint32_t S = a.splits;
     const size_t p0 = ((size_t)seq * hkv + kvh) * S * G + g;
 
@@ -768,38 +779,23 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeA
         }
         M = mb;
     }
-    // tree merge of the NSUB states of each column: log2(NSUB) steps
-    const int c4 = t % D4;  // column slot in LDS
-    sm_m[sub] = M;  // every column of a sub holds the same (M, L)
-    sm_l[sub] = L;
-    sm_acc[sub][c4] = A;
-    __syncthreads();
+    // the 8 subs of this wave: lane bits 3..5
 #pragma unroll
-    for (int half = NSUB / 2; half >= 1; half >>= 1) {
-        float Mo = 0.f, Lo = 0.f;
-        f32x4 Ao = f32x4{0.f, 0.f, 0.f, 0.f};
-        const bool act = sub < half;
-        if (act) {
-            Mo = sm_m[sub + half];
-            Lo = sm_l[sub + half];
-            Ao = sm_acc[sub + half][c4];
-        }
-        __syncthreads();
-        if (act) {
-            const float mn = fmaxf(M, Mo);
-            const float f0 = fast_exp2(M - mn), f1 = fast_exp2(Mo - mn);
-            L = __builtin_fmaf(L, f0, Lo * f1);
-            A = A * f0 + Ao * f1;
-            M = mn;
-            sm_acc[sub][c4] = A;
-            if (c4 == 0) {
-                sm_m[sub] = M;
-                sm_l[sub] = L;
-            }
-        }
-        __syncthreads();
+    for (int mask = D4; mask < 64; mask <<= 1) {
+        f32x4 Ao;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Ao[j] = __shfl_xor(A[j], mask);
+        merge_partial(M, L, A, __shfl_xor(M, mask), __shfl_xor(L, mask), Ao);
     }
-    if (sub == 0) {
+    if (lane < D4) {
+        sm_m[wave][c4] = M;
+        sm_l[wave][c4] = L;
+        sm_acc[wave][c4] = A;
+    }
+    __syncthreads();
+    if (t < D4) {
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) merge_partial(M, L, A, sm_m[w][t], sm_l[w][t], sm_acc[w][t]);
         const float inv = 1.0f / L;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
