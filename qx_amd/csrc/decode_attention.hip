@@ -820,8 +820,8 @@ static int rows_per_wave_load(int head_dim, int key_dtype) {
 static bool valu_path(int key_dtype, int value_dtype) { return key_dtype == F32 || key_dtype != value_dtype; }
 
 bool decode_dtypes_supported(const ShapeDims& s, int key_dtype, int value_dtype) {
-    // tiered values: Granite with fp32 (the reference's proposal keeps K in fp32) or f16 keys
-    if (value_dtype == I8T) return s.head_dim == 64 && s.group == 2 && (key_dtype == F32 || key_dtype == F16);
+    // tiered values: any key dtype (the reference's proposal keeps K in fp32), both shapes
+    if (value_dtype == I8T) return key_dtype == F32 || key_dtype == F16 || key_dtype == BF16;
     if (key_dtype == value_dtype) return true;
     // mixed pairs are the Granite KV plans Fp32KFp16V / Fp16KFp32V (and their bf16 twins)
     return s.head_dim == 64 && s.group == 2 && (key_dtype == F32 || value_dtype == F32);
@@ -922,11 +922,16 @@ static hipError_t launch_decode_impl(const ShapeDims& s, const KvLayer& kv, cons
         else if (kd == F16 && vd == F32) launch_valu<64, 2, F16, F32>(a, grid, st);
         else if (kd == F32 && vd == I8T) launch_valu<64, 2, F32, I8T>(a, grid, st);
         else if (kd == F16 && vd == I8T) launch_valu<64, 2, F16, I8T>(a, grid, st);
+        else if (kd == BF16 && vd == I8T) launch_valu<64, 2, BF16, I8T>(a, grid, st);
         else launch_valu<64, 2, BF16, F32>(a, grid, st);
         if (p.splits > 1)
             hipLaunchKernelGGL((decode_combine_kernel<64, 2>), dim3(s.q_heads * (64 / kCombineDims), units_z), dim3(kCombineThreads), 0, st, a);
     } else if (s.head_dim == 128 && s.group == 8) {
-        if (kd == F32) launch_valu<128, 8, F32, F32>(a, grid, st);
+        if (vd == I8T) {
+            if (kd == F32) launch_valu<128, 8, F32, I8T>(a, grid, st);
+            else if (kd == F16) launch_valu<128, 8, F16, I8T>(a, grid, st);
+            else launch_valu<128, 8, BF16, I8T>(a, grid, st);
+        } else if (kd == F32) launch_valu<128, 8, F32, F32>(a, grid, st);
         else if (kd == F16) hipLaunchKernelGGL((decode_mfma_kernel<128, 8, F16, kWaves>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((decode_mfma_kernel<128, 8, BF16, kWaves>), grid, block, 0, st, a);
         if (p.splits > 1)

@@ -73,6 +73,7 @@ __global__ __launch_bounds__(256) void qwen_norm_rope_append_kernel(KvLayer kv, 
     const uint32_t pos = a.start_position + t;
     const size_t tok = (size_t)s * a.tokens + t;
     const bool is_q = head < q_heads;
+    if (is_q && !a.query_out) return;  // no rotated query wanted (the query may be null)
     const int h = is_q ? head : head - q_heads;
     const void* src = is_q ? a.query : a.key;
     const size_t base = is_q ? (tok * q_heads + h) * D : (tok * kv_heads + h) * D;

@@ -330,8 +330,6 @@ static int32_t check_desc(const qxh_kv_desc* d, ShapeDims* dims) {
         const uint32_t w = d->value_window;
         QXH_REQUIRE(w >= 32 && w <= 65536 && (w & (w - 1)) == 0, QXH_ERR_INVALID_ARGUMENT,
                     "tiered value window %u is not a power of two in [32, 65536]", w);
-        QXH_REQUIRE(d->shape == QXH_SHAPE_GRANITE && (d->key_dtype == QXH_F32 || d->key_dtype == QXH_F16),
-                    QXH_ERR_UNSUPPORTED, "tiered values are built for the Granite shape with fp32 or f16 keys");
     } else {
         QXH_REQUIRE(d->value_window == 0, QXH_ERR_INVALID_ARGUMENT,
                     "value_window %u is only meaningful for tiered values", d->value_window);

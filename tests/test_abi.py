@@ -90,18 +90,22 @@ def test_tiered_value_arena_bytes():
     assert base - n.value == (48 << 20) - (3 << 20) - (6 << 20) - slots * 4
 
 
-@pytest.mark.parametrize("shape,kd,window,code", [
-    (abi.SHAPE_GRANITE, abi.F32, 48, abi.QXH_ERR_INVALID_ARGUMENT),   # not a power of two
-    (abi.SHAPE_GRANITE, abi.F32, 16, abi.QXH_ERR_INVALID_ARGUMENT),   # below 32
-    (abi.SHAPE_GRANITE, abi.F32, 0, abi.QXH_ERR_INVALID_ARGUMENT),
-    (abi.SHAPE_QWEN3, abi.F16, 256, abi.QXH_ERR_UNSUPPORTED),
-    (abi.SHAPE_GRANITE, abi.BF16, 256, abi.QXH_ERR_UNSUPPORTED),
-])
-def test_tiered_descriptors_are_validated(shape, kd, window, code):
+@pytest.mark.parametrize("window", [48, 16, 0, 1 << 17])  # not a power of two, below 32, none, above 65536
+def test_tiered_descriptors_are_validated(window):
     n = ctypes.c_uint64()
-    desc = abi.KvDesc(shape, kd, abi.I8_TIERED, 1, 1, 512, window)
-    assert abi.lib().qxh_kv_cache_bytes(ctypes.byref(desc), ctypes.byref(n)) == code
+    desc = abi.KvDesc(abi.SHAPE_GRANITE, abi.F32, abi.I8_TIERED, 1, 1, 512, window)
+    assert abi.lib().qxh_kv_cache_bytes(ctypes.byref(desc), ctypes.byref(n)) == abi.QXH_ERR_INVALID_ARGUMENT
     assert "tiered" in abi.last_error()
+
+
+def test_tiered_qwen_arena_bytes():
+    # Qwen at ctx 32768 with bf16 K: 4 kv heads x 128 dims per position
+    n = ctypes.c_uint64()
+    desc = abi.KvDesc(abi.SHAPE_QWEN3, abi.BF16, abi.I8_TIERED, 48, 1, 32768, 1024)
+    assert abi.lib().qxh_kv_cache_bytes(ctypes.byref(desc), ctypes.byref(n)) == 0
+    elems = 48 * 4 * 32768 * 128
+    slots = 48 * 4 * 1024
+    assert n.value == 2 * elems + elems + elems // 16 + slots * 128 * 2 + slots * 4
 
 
 def test_value_window_needs_tiered_values():

@@ -249,3 +249,21 @@ def test_qwen_in_place_qk_norm_rope(ctx):
     rq, rk = O.qwen_qk_norm_rope(qb, kb, ones, ones, 37, O.F16)
     assert np.max(np.abs(gq.astype(np.int32) - rq.astype(np.int32))) <= 1
     assert np.max(np.abs(gk.astype(np.int32) - rk.astype(np.int32))) <= 1
+
+
+def test_qwen_append_without_query_stores_the_same_rows():
+    """A Qwen RoPE append with no query (only the cache rows wanted) stores
+    the K/V rows bit for bit as the append with a query does; the query
+    heads do nothing when there is no rotated query to write."""
+    ctx = rt.Context(0)
+    rng = np.random.default_rng(31)
+    k = torch.from_numpy(rng.standard_normal((1, 3, 4, 128), dtype=np.float32)).cuda().half()
+    v = torch.from_numpy(rng.standard_normal((1, 3, 4, 128), dtype=np.float32)).cuda().half()
+    q = torch.from_numpy(rng.standard_normal((1, 3, 32, 128), dtype=np.float32)).cuda().half()
+    rows = []
+    for query, qout in ((q, torch.empty_like(q)), (None, None)):
+        arena = rt.KvArena(ctx, abi.SHAPE_QWEN3, 1, 1, 64, abi.F16)
+        with rt.Graph(ctx) as g:
+            rt.rope_kv_batch(g, arena, 0, 0, query, k, v, query_out=qout)
+            rows.append(arena.gather(g, 0, 0, 0, 3))
+    assert torch.equal(rows[0][0], rows[1][0]) and torch.equal(rows[0][1], rows[1][1])

@@ -207,6 +207,52 @@ def test_tiered_graph_replay_after_rollback(ctx):
     assert rel_err(first.cpu().numpy().ravel(), O.granite_attend(q.cpu().numpy().ravel(), ref, L + 1)) <= TOL_F32
 
 
+@pytest.mark.parametrize("kdt", [abi.BF16, abi.F32])
+def test_tiered_qwen_shape(ctx, kdt):
+    """Qwen (4 kv heads x 128 dims, G = 8): fill, a RoPE append longer than
+    the window, batched decode and causal rows, against the tier model bit
+    for bit and float64 attention at the fp32 bar."""
+    log("tiered qwen", kdt)
+    W, S, cap, L, T = 64, 2, 1024, 700, 100
+    rng = np.random.default_rng(29 + kdt)
+    arena = rt.KvArena(ctx, abi.SHAPE_QWEN3, 1, S, cap, kdt, abi.I8_TIERED, value_window=W)
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=7, length=L)
+    models = []
+    for seq in range(S):
+        m = O.TieredValueCache(W, 4, 128)
+        m.append(np.stack([O.tiered_fill_values(7, seq * 4 + h, cap, L, 128) for h in range(4)], axis=1)
+                 .astype(np.float32))
+        models.append(m)
+    k = dev(rng.standard_normal((S, T, 4, 128), dtype=np.float32)).to(rt.torch_dtype(kdt))
+    v = dev(rng.standard_normal((S, T, 4, 128), dtype=np.float32)).to(rt.torch_dtype(kdt))
+    with rt.Graph(ctx) as g:
+        rt.rope_kv_batch(g, arena, 0, L, None, k, v)
+    n = L + T
+    kf, vf = [], []
+    for seq in range(S):
+        models[seq].append(v[seq].float().cpu().numpy())
+        kk, vt = values(arena, 0, seq, n)
+        assert arena.value_tier(0, seq) == models[seq].boundary == n - W
+        assert np.array_equal(vt.view(np.uint32), models[seq].rows().view(np.uint32)), seq
+        kf.append(kk.float().cpu().numpy())
+        vf.append(vt)
+    q = rng.standard_normal((S, 32, 128), dtype=np.float32)
+    with rt.Graph(ctx) as g:
+        out = rt.attention(g, arena, 0, dev(q), n).cpu().numpy()
+    for seq in range(S):
+        e = rel_err(out[seq], attend64(q[seq], kf[seq], vf[seq], 1 / np.sqrt(128)))
+        log(f"  decode seq {seq}: {e:.2e}")
+        assert e <= TOL_F32
+    rows = 6
+    qr = rng.standard_normal((rows, 32, 128), dtype=np.float32)
+    with rt.Graph(ctx) as g:
+        pr = rt.prefill_attention(g, arena, 0, n - rows, dev(qr)).cpu().numpy()
+    for t in range(rows):
+        p = n - rows + t + 1
+        assert rel_err(pr[t], attend64(qr[t], kf[0][:p], vf[0][:p], 1 / np.sqrt(128))) <= TOL_F32, t
+
+
 def test_tiered_values_are_refused_where_unsupported(ctx):
     arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 2, 256, abi.F32, abi.I8_TIERED, value_window=32)
     with rt.Graph(ctx) as g:
