@@ -182,6 +182,29 @@ def bench_tiered_v(ctx, steps, warmup):
         del arena, ws
         torch.cuda.empty_cache()
     res["speedup"] = round(res["fp32k_f16v"]["us_per_layer_step"] / res["fp32k_tiered"]["us_per_layer_step"], 3)
+    # Qwen at cfg 5a's shape (batch 1, ctx 32768, bf16 K, 48 layers replayed)
+    # with a window of 1024: the VALU tiered kernel against cfg 5a's MFMA path
+    QL, QN, QW = 48, 32768, 1024
+    arena = rt.KvArena(ctx, abi.SHAPE_QWEN3, QL, 1, QN, abi.BF16, abi.I8_TIERED, value_window=QW)
+    qq = torch.empty((QL, 1, 32, 128), dtype=torch.bfloat16, device="cuda:0")
+    qo = torch.empty_like(qq)
+    with rt.Graph(ctx, stream) as g:
+        arena.fill_normal(g, seed=5, length=QN)
+        rt.fill_normal(g, qq, seed=55)
+    ws = torch.empty(max(rt.attention_workspace_bytes(arena, 1, QN), 1), dtype=torch.uint8, device="cuda:0")
+    g = rt.Graph(ctx, stream)
+    g.capture_begin()
+    for layer in range(QL):
+        rt.attention(g, arena, layer, qq[layer], QN, out=qo[layer], workspace=ws)
+    replay = g.capture_end()
+    g.discard()
+    ms = timed(lambda: replay.launch(stream), steps, warmup, stream)
+    per_layer = ms / QL
+    nbytes = 4 * (QN * 128 * 2 + (QN - QW) * (128 + 8) + QW * 128 * 2)
+    res["qwen_bf16k_tiered_ctx32768"] = {"us_per_layer": round(per_layer * 1000.0, 2), "bytes_per_layer": nbytes,
+                                         "roofline": roofline_hbm(nbytes, per_layer)}
+    del replay, arena, ws
+    torch.cuda.empty_cache()
     return res
 
 
