@@ -539,10 +539,17 @@ __global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs 
 // bandwidth-bound kernel.  Lane (g, i) keeps the softmax state of head i, so
 // rescaling the O^T accumulators is lane-local.
 // ---------------------------------------------------------------------------
-template <int D, int G, int KDT, int WAVES>
+//
+// Tiered values (TV): the V tile is built from INT8 rows (codes x scale,
+// rounded to f16) below the boundary and from the f16 window above it, each
+// wave's rows cut at the boundary into two passes; P.V then runs in f16
+// whatever the key dtype, since the tile holds f16 values.
+template <int D, int G, int KDT, int WAVES, bool TV = false>
 __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
     using M = MfmaT<KDT>;
     using vec = typename M::vec;
+    using MV = MfmaT<TV ? F16 : KDT>;  // P.V operands
+    using vvec = typename MV::vec;
     constexpr int KSTEPS = D / 32;
     constexpr int DTILES = D / 16;
     constexpr int VROWB = D * 2 + 32;            // padded V row for conflict-light transposed reads
@@ -568,7 +575,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
 
     const size_t head_off = (size_t)seq * a.seq_stride + (size_t)kvh * a.head_stride;
     const char* kb = reinterpret_cast<const char*>(a.keys) + head_off * 2;
-    const char* vb = reinterpret_cast<const char*>(a.values) + head_off * 2;
+    const char* vb = reinterpret_cast<const char*>(a.values) + head_off * (TV ? 1 : 2);
+    const uint16_t* vsc = reinterpret_cast<const uint16_t*>(a.value_scales) + head_off / 32;
+    const char* vring = reinterpret_cast<const char*>(a.value_ring) +
+                        ((size_t)seq * a.ring_seq_stride + (size_t)kvh * a.ring_head_stride) * 2;
     char* vl = vtile[wave];
 
     // Q^T operand: lane (g, i) supplies head i (zero for i >= G), dims 32ks + 8g..
@@ -598,10 +608,14 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
     // One K load covers 64 of each row's 2D bytes, so the rest of the line is read by the next
     // instruction: K uses ordinary (temporal) loads so the line survives in L2 until then
     // (nontemporal K loads measured 8% extra HBM fetch); V loads read whole rows.
-    auto load_tile = [&](uint32_t base, u32x4 (&kr)[2][KSTEPS], u32x4 (&vr)[VCH]) {
+    // MODE 0: V rows of the cache dtype; 1: INT8 tier (codes in vr[.][0..1],
+    // the block scale in vs); 2: f16 window.
+    auto load_tile = [&](uint32_t base, uint32_t end, auto mode, u32x4 (&kr)[2][KSTEPS], u32x4 (&vr)[VCH],
+                         float (&vs)[VCH]) {
+        constexpr int MODE = decltype(mode)::value;
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-            const uint32_t row = min(base + 16 * mt + li, w1 - 1);
+            const uint32_t row = min(base + 16 * mt + li, end - 1);
 #pragma unroll
             for (int ks = 0; ks < KSTEPS; ++ks)
                 kr[mt][ks] = load16<false>(kb + ((size_t)row * D + 32 * ks + 8 * lg) * 2);
@@ -610,25 +624,48 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
         for (int cc = 0; cc < VCH; ++cc) {
             const int chunk = lane + 64 * cc;
             const int row = chunk / (D / 8), col = chunk % (D / 8);
-            const uint32_t pos = min(base + row, w1 - 1);
-            vr[cc] = load16<true>(vb + ((size_t)pos * D + col * 8) * 2);
+            const uint32_t pos = min(base + row, end - 1);
+            if constexpr (MODE == 1) {
+                const size_t e = (size_t)pos * D + col * 8;
+                const u32x2 c = load8<true>(vb + e);
+                vr[cc] = u32x4{c[0], c[1], 0u, 0u};
+                vs[cc] = half_bits_to_f32(vsc[e / kTierBlock]);
+            } else if constexpr (MODE == 2) {
+                vr[cc] = load16<true>(vring + ((size_t)(pos & a.window_mask) * D + col * 8) * 2);
+            } else {
+                vr[cc] = load16<true>(vb + ((size_t)pos * D + col * 8) * 2);
+            }
         }
     };
-    for (uint32_t base = w0; base < w1; base += 32) {
+    // One pass over positions [begin, end) of this wave.
+    auto pass = [&](uint32_t begin, uint32_t end, auto mode) {
+        constexpr int MODE = decltype(mode)::value;
+    for (uint32_t base = begin; base < end; base += 32) {
         u32x4 kr[2][KSTEPS], vr[VCH];
-        load_tile(base, kr, vr);
+        float vs[VCH];
+        load_tile(base, end, mode, kr, vr, vs);
         // S^T = K . Q^T
         f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks)
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) sacc[mt] = M::mma(__builtin_bit_cast(vec, kr[mt][ks]), qop[ks], sacc[mt]);
-        // V tile into this wave's LDS slot
+        // V tile into this wave's LDS slot (INT8 rows dequantised to f16 here)
 #pragma unroll
         for (int cc = 0; cc < VCH; ++cc) {
             const int chunk = lane + 64 * cc;
             const int row = chunk / (D / 8), col = chunk % (D / 8);
-            *reinterpret_cast<u32x4*>(vl + row * VROWB + col * 16) = vr[cc];
+            u32x4 w = vr[cc];
+            if constexpr (MODE == 1) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t cw = vr[cc][j >> 1] >> (16 * (j & 1));
+                    const float lo = (float)(int32_t)(int8_t)(cw & 0xffu) * vs[cc];
+                    const float hi = (float)(int32_t)(int8_t)((cw >> 8) & 0xffu) * vs[cc];
+                    w[j] = (uint32_t)f32_to_half_bits(lo) | ((uint32_t)f32_to_half_bits(hi) << 16);
+                }
+            }
+            *reinterpret_cast<u32x4*>(vl + row * VROWB + col * 16) = w;
         }
         // online softmax of head `li` over this tile's 32 positions
         float sv[8];
@@ -638,7 +675,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t pos = base + 16 * mt + 4 * lg + j;
-                const float v = pos < w1 ? sacc[mt][j] * c : -INFINITY;
+                const float v = pos < end ? sacc[mt][j] * c : -INFINITY;
                 sv[mt * 4 + j] = v;
                 tmax = fmaxf(tmax, v);
             }
@@ -646,15 +683,15 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
         const float mnew = fmaxf(mrun, tmax);
         const float alpha = fast_exp2(mrun - mnew);
         mrun = mnew;
-        vec phi, plo;
+        vvec phi, plo;
         float psum = 0.f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const float p = fast_exp2(sv[k] - mnew);
             psum += p;
-            const auto h = M::cvt(p);
+            const auto h = MV::cvt(p);
             phi[k] = h;
-            if constexpr (KDT == BF16) plo[k] = M::cvt(p - (float)h);
+            if constexpr (!TV && KDT == BF16) plo[k] = MV::cvt(p - (float)h);
         }
         lrun = __builtin_fmaf(lrun, alpha, psum);
 #pragma unroll
@@ -662,10 +699,18 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
         // O^T += V^T . P^T
 #pragma unroll
         for (int dt = 0; dt < DTILES; ++dt) {
-            const vec vop = __builtin_bit_cast(vec, vt_operand_rows32<VROWB>(vl, 0, 16 * dt, lg, li));
-            oacc[dt] = M::mma(vop, phi, oacc[dt]);
-            if constexpr (KDT == BF16) oacc[dt] = M::mma(vop, plo, oacc[dt]);
+            const vvec vop = __builtin_bit_cast(vvec, vt_operand_rows32<VROWB>(vl, 0, 16 * dt, lg, li));
+            oacc[dt] = MV::mma(vop, phi, oacc[dt]);
+            if constexpr (!TV && KDT == BF16) oacc[dt] = MV::mma(vop, plo, oacc[dt]);
         }
+    }
+    };
+    if constexpr (TV) {
+        const uint32_t cut = min(max(a.tier, w0), w1);
+        pass(w0, cut, std::integral_constant<int, 1>{});
+        pass(cut, w1, std::integral_constant<int, 2>{});
+    } else {
+        pass(w0, w1, std::integral_constant<int, 0>{});
     }
 
     // the four 16-lane groups hold disjoint positions of head li: total l
@@ -819,6 +864,13 @@ static int rows_per_wave_load(int head_dim, int key_dtype) {
 // dtypes take the MFMA kernel.
 static bool valu_path(int key_dtype, int value_dtype) { return key_dtype == F32 || key_dtype != value_dtype; }
 
+// Tiered values with 16-bit keys on the Qwen shape (G = 8) decode on the MFMA
+// kernel, where the VALU kernel's eight per-row dot reductions make it
+// compute-bound; causal rows and fp32 keys stay on the VALU kernel.
+static bool tiered_on_mfma(const ShapeDims& s, int key_dtype, int value_dtype) {
+    return value_dtype == I8T && key_dtype != F32 && s.group >= 8;
+}
+
 bool decode_dtypes_supported(const ShapeDims& s, int key_dtype, int value_dtype) {
     // tiered values: any key dtype (the reference's proposal keeps K in fp32), both shapes
     if (value_dtype == I8T) return key_dtype == F32 || key_dtype == F16 || key_dtype == BF16;
@@ -830,7 +882,7 @@ bool decode_dtypes_supported(const ShapeDims& s, int key_dtype, int value_dtype)
 DecodePlan plan_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t sequences, uint32_t length) {
     DecodePlan p{};
     p.waves = kWaves;
-    const bool valu = valu_path(key_dtype, value_dtype);
+    const bool valu = valu_path(key_dtype, value_dtype) && !tiered_on_mfma(s, key_dtype, value_dtype);
     const uint32_t rpw = (uint32_t)rows_per_wave_load(s.head_dim, key_dtype);
     const uint32_t step = rpw * kUnroll;
     const uint32_t units = sequences * (uint32_t)s.kv_heads;
@@ -929,8 +981,10 @@ static hipError_t launch_decode_impl(const ShapeDims& s, const KvLayer& kv, cons
     } else if (s.head_dim == 128 && s.group == 8) {
         if (vd == I8T) {
             if (kd == F32) launch_valu<128, 8, F32, I8T>(a, grid, st);
-            else if (kd == F16) launch_valu<128, 8, F16, I8T>(a, grid, st);
-            else launch_valu<128, 8, BF16, I8T>(a, grid, st);
+            else if (a.causal && kd == F16) launch_valu<128, 8, F16, I8T>(a, grid, st);
+            else if (a.causal) launch_valu<128, 8, BF16, I8T>(a, grid, st);
+            else if (kd == F16) hipLaunchKernelGGL((decode_mfma_kernel<128, 8, F16, kWaves, true>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((decode_mfma_kernel<128, 8, BF16, kWaves, true>), grid, block, 0, st, a);
         } else if (kd == F32) launch_valu<128, 8, F32, F32>(a, grid, st);
         else if (kd == F16) hipLaunchKernelGGL((decode_mfma_kernel<128, 8, F16, kWaves>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((decode_mfma_kernel<128, 8, BF16, kWaves>), grid, block, 0, st, a);

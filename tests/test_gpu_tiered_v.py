@@ -18,7 +18,7 @@ import torch
 from oracle import oracle as O
 from qx_amd import abi
 from qx_amd import runtime as rt
-from tests.helpers import TOL_F32, log, rel_err
+from tests.helpers import TOL_16, TOL_F32, log, rel_err
 from tests.test_gpu_mixed_kv import attend64, check_fp32_bar
 
 pytestmark = pytest.mark.gpu
@@ -207,11 +207,14 @@ def test_tiered_graph_replay_after_rollback(ctx):
     assert rel_err(first.cpu().numpy().ravel(), O.granite_attend(q.cpu().numpy().ravel(), ref, L + 1)) <= TOL_F32
 
 
-@pytest.mark.parametrize("kdt", [abi.BF16, abi.F32])
+@pytest.mark.parametrize("kdt", [abi.BF16, abi.F16, abi.F32])
 def test_tiered_qwen_shape(ctx, kdt):
     """Qwen (4 kv heads x 128 dims, G = 8): fill, a RoPE append longer than
     the window, batched decode and causal rows, against the tier model bit
-    for bit and float64 attention at the fp32 bar."""
+    for bit and float64 attention.  Decode with 16-bit keys runs on the MFMA
+    kernel, whose V tile holds the values rounded once to f16: the 16-bit
+    bar; fp32 keys and the causal rows (VALU kernel, exact values): the fp32
+    bar."""
     log("tiered qwen", kdt)
     W, S, cap, L, T = 64, 2, 1024, 700, 100
     rng = np.random.default_rng(29 + kdt)
@@ -237,13 +240,16 @@ def test_tiered_qwen_shape(ctx, kdt):
         assert np.array_equal(vt.view(np.uint32), models[seq].rows().view(np.uint32)), seq
         kf.append(kk.float().cpu().numpy())
         vf.append(vt)
-    q = rng.standard_normal((S, 32, 128), dtype=np.float32)
+    # queries in the key dtype (as the 16-bit decode tests pass them), so both
+    # sides see the same q and only the value path differs
+    q = torch.from_numpy(rng.standard_normal((S, 32, 128), dtype=np.float32)).to(rt.torch_dtype(kdt)).float().numpy()
     with rt.Graph(ctx) as g:
         out = rt.attention(g, arena, 0, dev(q), n).cpu().numpy()
+    tol = TOL_F32 if kdt == abi.F32 else TOL_16
     for seq in range(S):
         e = rel_err(out[seq], attend64(q[seq], kf[seq], vf[seq], 1 / np.sqrt(128)))
         log(f"  decode seq {seq}: {e:.2e}")
-        assert e <= TOL_F32
+        assert e <= tol
     rows = 6
     qr = rng.standard_normal((rows, 32, 128), dtype=np.float32)
     with rt.Graph(ctx) as g:
