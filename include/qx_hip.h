@@ -210,8 +210,8 @@ QXH_API int32_t qxh_kv_cache_desc(const qxh_kv_cache* cache, qxh_kv_desc* out);
  * rest of the committed positions binary16 (no counterpart in the reference,
  * which only proposes the format).  An append of `tokens` at cursor s moves
  * the boundary to max(boundary, s + tokens - value_window); a rollback to L
- * lowers it to min(boundary, L); reset clears it; set_len puts it at
- * max(0, length - value_window).  Launches over several sequences of a tiered
+ * lowers it to min(boundary, L), and so does set_len; a fill of `length`
+ * rows puts it at max(0, length - value_window); reset clears it.  Launches over several sequences of a tiered
  * cache need equal boundaries (QXH_ERR_UNSUPPORTED otherwise).  Returns 0 for
  * other value dtypes. */
 QXH_API int32_t qxh_kv_cache_value_tier(const qxh_kv_cache* cache, uint32_t layer, uint32_t sequence,

@@ -638,9 +638,10 @@ class TieredValueCache:
         self.length = length
         self.boundary = min(self.boundary, length)
 
-    def set_len(self, length: int):
-        self.length = length
-        self.boundary = max(0, length - self.window)
+    def fill(self, rows):
+        """A bulk fill of rows [0, n): the boundary settles at max(0, n - window)."""
+        self.length, self.boundary = 0, 0
+        self.append(rows)
 
     def rows(self):
         out = self.half[: self.length].astype(np.float32)

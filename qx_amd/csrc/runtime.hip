@@ -438,7 +438,7 @@ extern "C" int32_t qxh_kv_cache_reset(qxh_kv_cache* c) {
     return QXH_OK;
 }
 
-// Boundary after a bulk write of `length` rows (fill, set_len).
+// Boundary after a fill of `length` rows.
 static uint32_t settled_tier(const qxh_kv_cache* c, uint32_t length) {
     return c->tiered() && length > c->desc.value_window ? length - c->desc.value_window : 0u;
 }
@@ -468,7 +468,9 @@ extern "C" int32_t qxh_kv_cache_set_len(qxh_kv_cache* c, uint32_t seq, uint32_t 
         for (uint32_t s = 0; s < c->desc.sequences; ++s)
             if (seq == UINT32_MAX || s == seq) {
                 c->at(l, s) = length;
-                c->tier_at(l, s) = settled_tier(c, length);
+                // the fill and the appends set the boundary as they write;
+                // a cursor move never claims rows as quantised
+                c->tier_at(l, s) = std::min(c->tier_at(l, s), length);
             }
     return QXH_OK;
 }

@@ -106,6 +106,10 @@ def test_tiered_appends_and_rollbacks_match_the_model(ctx):
                 assert np.array_equal(vt.view(np.uint32), m.rows().view(np.uint32)), (op, s)
         step += 1
     assert step > 20
+    # set_len moves the cursor and never raises the boundary
+    before = [arena.value_tier(0, s) for s in range(2)]
+    arena.set_len(3)
+    assert [arena.value_tier(0, s) for s in range(2)] == [min(b, 3) for b in before]
 
 
 @pytest.mark.parametrize("kdt", [abi.F32, abi.F16])
@@ -199,7 +203,7 @@ def test_tiered_graph_replay_after_rollback(ctx):
             assert arena.value_tier() == model.boundary == L + 1 - W
             assert np.array_equal(vt.view(np.uint32), model.rows().view(np.uint32)), i
             arena.rollback(0, L)
-            arena.set_len(L + 1)  # the replay wrote row L again; the boundary settles at L + 1 - W
+            arena.set_len(L + 1)  # the replay wrote row L again; the boundary stays at L + 1 - W
         del replay
     kk, vf = values(arena, 0, 0, L + 1)
     ref = O.KvCache(256)
