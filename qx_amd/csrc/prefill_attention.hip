@@ -419,8 +419,16 @@ __global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a
 // bytes for long prefills); equal 16-bit dtypes take the MFMA prefill.
 static bool prefill_on_decode(const KvLayer& kv) { return kv.key_dtype == F32 || kv.key_dtype != kv.value_dtype; }
 
+// Tiered values with 16-bit keys take the pipelined MFMA prefill (T >= 64),
+// its V^T pre-pass reading the tiers; the shorter verifier rows stay on the
+// decode kernels.
+static bool tiered_on_pipe(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t tokens) {
+    return value_dtype == I8T && key_dtype != F32 && prefill_pipe_supported(s, tokens);
+}
+
 uint64_t prefill_workspace_bytes(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t capacity,
                                  uint32_t tokens) {
+    if (tiered_on_pipe(s, key_dtype, value_dtype, tokens)) return prefill_pipe_workspace_bytes(s, capacity, tokens);
     if (key_dtype == F32 || key_dtype != value_dtype)
         return decode_causal_workspace_bound(s, key_dtype, value_dtype, capacity, tokens);
     const int kv_dtype = key_dtype;
@@ -434,6 +442,11 @@ hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint3
                                     const void* query, int query_dtype, void* out, int out_dtype, void* workspace,
                                     hipStream_t st, int* dispatches) {
     *dispatches = 0;
+    if (tiered_on_pipe(s, kv.key_dtype, kv.value_dtype, tokens)) {
+        if (kv.key_dtype != query_dtype) return hipErrorNotSupported;
+        return launch_prefill_pipe(s, kv, start_position, tokens, query, query_dtype, out, out_dtype, workspace, st,
+                                   dispatches);
+    }
     if (prefill_on_decode(kv)) {
         const DecodePlan p = plan_decode_causal(s, kv.key_dtype, kv.value_dtype, start_position, tokens);
         return launch_decode_causal_rows(s, kv, p, start_position, tokens, query, query_dtype, out, out_dtype, workspace,

@@ -32,6 +32,7 @@
 
 #include "common.h"
 #include "internal.h"
+#include "tiered_v.h"
 #include "mfma.h"
 
 namespace qxh {
@@ -119,6 +120,70 @@ __global__ __launch_bounds__(D) void prefill_vt_kernel(VtArgs a) {
     }
     ovf = __syncthreads_or(ovf);
     if (tid == 0) a.flags[(size_t)h * a.vt_tiles + t] = ovf ? 1u : 0u;
+    uint16_t* dst = a.vt + ((size_t)h * a.vt_tiles + t) * D * kTile + 32 * half + 8 * g;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int w = k >> 1;
+        u32x4 o;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t x = row[2 * q][w], y = row[2 * q + 1][w];
+            o[q] = (k & 1) ? (x >> 16) | (y & 0xffff0000u) : (x & 0xffffu) | (y << 16);
+        }
+        *reinterpret_cast<u32x4*>(dst + (size_t)(dg * 8 + k) * kTile) = o;
+    }
+}
+
+// The same V^T tiles from a tiered value cache: rows below the boundary are
+// INT8 codes times their block scale, rounded to f16 (clamped to the f16
+// range, which code x scale can pass by less than one f16 step), rows at or
+// above it the f16 window.  Every value is then a finite f16, so no tile is
+// flagged for the exact pass.
+struct TieredVtArgs {
+    const int8_t* codes;       // [Hkv][cap][D]
+    const uint16_t* scales;    // one per 32 elements
+    const uint16_t* ring;      // [Hkv][window][D] f16
+    uint16_t* vt;
+    uint64_t head_stride;      // elements between kv heads
+    uint64_t ring_head_stride;
+    uint32_t window_mask;
+    uint32_t tier;
+    uint32_t vt_tiles;
+    uint32_t kv_len;
+};
+
+template <int D>
+__global__ __launch_bounds__(D) void prefill_vt_tiered_kernel(TieredVtArgs a) {
+    constexpr int DG = D / 8;
+    const uint32_t t = blockIdx.x, h = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int dg = tid % DG, g = (tid / DG) % 4, half = tid / (DG * 4);
+    const int8_t* codes = a.codes + (size_t)h * a.head_stride;
+    const uint16_t* scales = a.scales + (size_t)h * a.head_stride / kTierBlock;
+    const uint16_t* ring = a.ring + (size_t)h * a.ring_head_stride;
+    u32x4 row[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t pos = t * kTile + 32 * half + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
+        const uint32_t src = min(pos, a.kv_len - 1);
+        if (src < a.tier) {
+            const size_t e = (size_t)src * D + dg * 8;
+            const uint32_t* cw = reinterpret_cast<const uint32_t*>(codes + e);
+            const uint32_t c0 = cw[0], c1 = cw[1];
+            const float sc = half_bits_to_f32(scales[e / kTierBlock]);
+            u32x4 v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t w = (i < 2 ? c0 : c1) >> (16 * (i & 1));
+                const float lo = fminf(fmaxf((float)(int8_t)(w & 0xffu) * sc, -65504.0f), 65504.0f);
+                const float hi = fminf(fmaxf((float)(int8_t)((w >> 8) & 0xffu) * sc, -65504.0f), 65504.0f);
+                v[i] = (uint32_t)f32_to_half_bits(lo) | ((uint32_t)f32_to_half_bits(hi) << 16);
+            }
+            row[j] = v;
+        } else {
+            row[j] = *reinterpret_cast<const u32x4*>(ring + (size_t)(src & a.window_mask) * D + dg * 8);
+        }
+    }
     uint16_t* dst = a.vt + ((size_t)h * a.vt_tiles + t) * D * kTile + 32 * half + 8 * g;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -675,13 +740,21 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
     uint16_t* vt = reinterpret_cast<uint16_t*>(ws + flag_bytes);
     char* parts = ws + flag_bytes + (uint64_t)s.kv_heads * vt_tiles * s.head_dim * kTile * 2;
 
-    VtArgs va{kv.values, vt, flags, kv.head_stride, vt_tiles, kv_len};
     dim3 vgrid(tiles, s.kv_heads);
     const bool bf = dtype == BF16;
-    if (s.head_dim == 128) {
+    const bool tiered = kv.value_dtype == I8T;
+    if (tiered) {
+        TieredVtArgs ta{reinterpret_cast<const int8_t*>(kv.values), reinterpret_cast<const uint16_t*>(kv.value_scales),
+                        reinterpret_cast<const uint16_t*>(kv.value_ring), vt, kv.head_stride, kv.ring_head_stride,
+                        kv.window - 1, kv.tier, vt_tiles, kv_len};
+        if (s.head_dim == 128) hipLaunchKernelGGL((prefill_vt_tiered_kernel<128>), vgrid, dim3(128), 0, st, ta);
+        else hipLaunchKernelGGL((prefill_vt_tiered_kernel<64>), vgrid, dim3(64), 0, st, ta);
+    } else if (s.head_dim == 128) {
+        VtArgs va{kv.values, vt, flags, kv.head_stride, vt_tiles, kv_len};
         if (bf) hipLaunchKernelGGL((prefill_vt_kernel<128, BF16>), vgrid, dim3(128), 0, st, va);
         else hipLaunchKernelGGL((prefill_vt_kernel<128, F16>), vgrid, dim3(128), 0, st, va);
     } else {
+        VtArgs va{kv.values, vt, flags, kv.head_stride, vt_tiles, kv_len};
         if (bf) hipLaunchKernelGGL((prefill_vt_kernel<64, BF16>), vgrid, dim3(64), 0, st, va);
         else hipLaunchKernelGGL((prefill_vt_kernel<64, F16>), vgrid, dim3(64), 0, st, va);
     }
@@ -690,7 +763,7 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
     a.query = query;
     a.keys = kv.keys;
     a.vt = vt;
-    a.flags = bf ? flags : nullptr;
+    a.flags = bf && !tiered ? flags : nullptr;
     a.out = out;
     a.head_stride = kv.head_stride;
     a.vt_tiles = vt_tiles;

@@ -263,6 +263,41 @@ def test_tiered_qwen_shape(ctx, kdt):
         assert rel_err(pr[t], attend64(qr[t], kf[0][:p], vf[0][:p], 1 / np.sqrt(128))) <= TOL_F32, t
 
 
+@pytest.mark.parametrize("shape,kdt", [(abi.SHAPE_QWEN3, abi.BF16), (abi.SHAPE_QWEN3, abi.F16),
+                                       (abi.SHAPE_GRANITE, abi.F16)])
+def test_tiered_prefill_on_the_pipelined_kernel(ctx, shape, kdt):
+    """128 prompt rows (T >= 64) over a tiered cache with 16-bit keys take
+    the pipelined MFMA prefill, its V^T pre-pass building f16 tiles from
+    both tiers; the 16-bit bar against float64 attention over the cached
+    values."""
+    log("tiered prefill", shape, kdt)
+    hq, hkv, d = (32, 4, 128) if shape == abi.SHAPE_QWEN3 else (16, 8, 64)
+    scale = 1 / np.sqrt(128) if shape == abi.SHAPE_QWEN3 else 0.015625
+    W, cap, start, T = 256, 2048, 1000, 128
+    rng = np.random.default_rng(41 + shape + kdt)
+    dt = rt.torch_dtype(kdt)
+    arena = rt.KvArena(ctx, shape, 1, 1, cap, kdt, abi.I8_TIERED, value_window=W)
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=9, length=start)
+    k = dev(rng.standard_normal((1, T, hkv, d), dtype=np.float32)).to(dt)
+    v = dev(rng.standard_normal((1, T, hkv, d), dtype=np.float32)).to(dt)
+    with rt.Graph(ctx) as g:
+        rt.store_kv(g, arena, 0, start, k, v)
+    assert arena.value_tier() == start + T - W
+    q = dev(rng.standard_normal((T, hq, d), dtype=np.float32)).to(dt)
+    with rt.Graph(ctx) as g:
+        # fp32 output: a 16-bit output alone is ~1e-2 (bf16) of RMS off float64
+        out = rt.prefill_attention(g, arena, 0, start, q, out_dtype=torch.float32).cpu().numpy()
+    kk, vf = values(arena, 0, 0, start + T)
+    kf, qf = kk.float().cpu().numpy(), q.float().cpu().numpy()
+    worst = 0.0
+    for t in (0, 1, 63, 64, 100, 127):
+        n = start + t + 1
+        worst = max(worst, rel_err(out[t], attend64(qf[t], kf[:n], vf[:n], scale)))
+    log(f"  worst row max-abs/rms {worst:.2e}")
+    assert worst <= TOL_16
+
+
 def test_tiered_values_are_refused_where_unsupported(ctx):
     arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 2, 256, abi.F32, abi.I8_TIERED, value_window=32)
     with rt.Graph(ctx) as g:
