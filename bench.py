@@ -205,6 +205,30 @@ def bench_tiered_v(ctx, steps, warmup):
                                          "roofline": roofline_hbm(nbytes, per_layer)}
     del replay, arena, ws
     torch.cuda.empty_cache()
+    # cfg 5b's prompt (Qwen, 8192 tokens, bf16 K) over tiered values: the
+    # pipelined prefill with the tiered V^T pre-pass, timed like cfg 5b
+    T = 8192
+    arena = rt.KvArena(ctx, abi.SHAPE_QWEN3, 1, 1, T, abi.BF16, abi.I8_TIERED, value_window=QW)
+    kv = torch.empty((1, T, 4, 128), dtype=torch.bfloat16, device="cuda:0")
+    qp = torch.empty((T, 32, 128), dtype=torch.bfloat16, device="cuda:0")
+    with rt.Graph(ctx, stream) as g:
+        rt.fill_normal(g, kv, seed=61)
+        rt.fill_normal(g, qp, seed=62)
+        rt.store_kv(g, arena, 0, 0, kv, kv)
+    ws = torch.empty(max(rt.prefill_workspace_bytes(arena, T), 1), dtype=torch.uint8, device="cuda:0")
+    po = torch.empty_like(qp)
+
+    g = rt.Graph(ctx, stream)
+    ms = timed(lambda: rt.prefill_attention(g, arena, 0, 0, qp, out=po, workspace=ws), steps, warmup, stream)
+    g.finish()
+    tflops = 4.0 * 128 * 32 * T * (T + 1) / 2 / (ms * 1e-3) / 1e12
+    peak = MFMA_PEAK_TFLOPS["bf16"]
+    res["qwen_bf16k_tiered_prefill_8192"] = {
+        "us_per_prefill": round(ms * 1000.0, 1),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(tflops / peak, 4), "traffic": None}}
+    del arena, ws
+    torch.cuda.empty_cache()
     return res
 
 

@@ -660,8 +660,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const uint32_t cw = vr[cc][j >> 1] >> (16 * (j & 1));
-                    const float lo = (float)(int32_t)(int8_t)(cw & 0xffu) * vs[cc];
-                    const float hi = (float)(int32_t)(int8_t)((cw >> 8) & 0xffu) * vs[cc];
+                    // code x scale can pass the f16 range by less than one step: clamp
+                    const float lo = fminf(fmaxf((float)(int32_t)(int8_t)(cw & 0xffu) * vs[cc], -65504.0f), 65504.0f);
+                    const float hi =
+                        fminf(fmaxf((float)(int32_t)(int8_t)((cw >> 8) & 0xffu) * vs[cc], -65504.0f), 65504.0f);
                     w[j] = (uint32_t)f32_to_half_bits(lo) | ((uint32_t)f32_to_half_bits(hi) << 16);
                 }
             }
