@@ -180,7 +180,10 @@ typedef struct {
     /* QXH_I8_TIERED only (NULL / 0 otherwise): one binary16 scale per 32
      * elements at element offset / 32, and the binary16 window, where position
      * p of a (sequence, kv head) sits in slot p % value_window of a
-     * value_window x head_dim block; blocks ordered [layer][sequence][kv head]. */
+     * value_window x head_dim block; blocks ordered [layer][sequence][kv head].
+     * Read-only for callers: each window slot also carries a position tag
+     * (internal to the arena) that the library's appends keep, and rows
+     * written into the tiers by other means would not be tracked. */
     void* value_scales;
     void* value_ring;
     uint32_t value_window;
