@@ -22,7 +22,8 @@
  *      batch query/output    [sequences][tokens][q_heads][head_dim]
  *      key/value inputs      [sequences][tokens][kv_heads][head_dim]
  *      KV arena (head-major) K: [layer][sequence][kv_head][capacity][head_dim]
- *                            V: same, after the whole K region
+ *                            V: same, after the whole K region (tiered values:
+ *                            INT8 codes, f16 block scales, f16 windows)
  *    The reference's KV rows are position-major [position][kv_head][head_dim]
  *    (crates/qx-runtime/src/lib.rs:400-415); qxh_encode_kv_gather_token_rows
  *    converts for consumers that read token rows.
@@ -308,8 +309,9 @@ QXH_API int32_t qxh_encode_prefill_attention(qxh_graph* graph, qxh_kv_cache* cac
                                      int32_t query_dtype, void* output, int32_t output_dtype, void* workspace,
                                      uint64_t workspace_bytes);
 
-/* Position-major token rows [count][kv_heads][head_dim] (cache dtypes) out of
- * the head-major arena, for consumers that read KV by token
+/* Position-major token rows [count][kv_heads][head_dim] (cache dtypes; tiered
+ * values as fp32, code x scale or the window's f16 widened) out of the
+ * head-major arena, for consumers that read KV by token
  * (crates/qx-runtime/src/lib.rs:418-430 KvCache::token;
  * crates/qx-runtime-v2/src/lib.rs:2194-2213; tools/qx-bench/src/main.rs:10994-11025). */
 QXH_API int32_t qxh_encode_kv_gather_token_rows(qxh_graph* graph, const qxh_kv_cache* cache, uint32_t layer,
