@@ -1079,6 +1079,9 @@ hipError_t launch_block_decode_attention(const ShapeDims& s, const KvLayer& kv, 
     else if (kd == F32 && vd == BF16) launch_block_valu<F32, BF16>(a, grid, st);
     else if (kd == F16 && vd == F32) launch_block_valu<F16, F32>(a, grid, st);
     else if (kd == BF16 && vd == F32) launch_block_valu<BF16, F32>(a, grid, st);
+    else if (kd == F32 && vd == I8T) launch_block_valu<F32, I8T>(a, grid, st);
+    else if (kd == F16 && vd == I8T) launch_block_valu<F16, I8T>(a, grid, st);
+    else if (kd == BF16 && vd == I8T) launch_block_valu<BF16, I8T>(a, grid, st);
     else return hipErrorNotSupported;
     return hipGetLastError();
 }

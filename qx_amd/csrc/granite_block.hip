@@ -93,8 +93,13 @@ __global__ __launch_bounds__(256) void granite_qkv_rope_kernel(KvLayer kv, Grani
     if (lane != 0) return;
     const size_t slot = (size_t)head * kv.head_stride + (size_t)a.position * 64;
     if (hb >= 24) {
-        store_any(kv.values, slot + p, x, kv.value_dtype);
-        store_any(kv.values, slot + 32 + p, y, kv.value_dtype);
+        if (kv.values) {
+            store_any(kv.values, slot + p, x, kv.value_dtype);
+            store_any(kv.values, slot + 32 + p, y, kv.value_dtype);
+        } else {  // a tiered value cache: the row goes through tiered_v.hip's append
+            a.value_row[head * 64 + p] = x;
+            a.value_row[head * 64 + 32 + p] = y;
+        }
         return;
     }
     float sn, cs;

@@ -153,6 +153,7 @@ struct GraniteBlockArgs {
     float* hidden_out;
     float* query_rot;   // workspace [1024]
     float* attention;   // workspace [1024]
+    float* value_row;   // workspace [512]: the new V row, for tiered caches
     uint32_t position;
     BlockPartials parts;
 };
@@ -181,6 +182,7 @@ struct GraniteQ4Args {
     float* hidden_out;
     float* query_rot;         // workspace [1024]
     float* attention;         // workspace [1024]
+    float* value_row;         // workspace [512]: the new V row, for tiered caches
     uint32_t position;
     BlockPartials parts;
 };

@@ -148,8 +148,13 @@ __global__ __launch_bounds__(256) void granite_q4_qkv_rope_kernel(KvLayer kv, Gr
     if (lane != 0) return;
     const size_t slot = (size_t)head * kv.head_stride + (size_t)a.position * 64;
     if (hb >= 24) {
-        store_any(kv.values, slot + p, xr, kv.value_dtype);
-        store_any(kv.values, slot + 32 + p, yr, kv.value_dtype);
+        if (kv.values) {
+            store_any(kv.values, slot + p, xr, kv.value_dtype);
+            store_any(kv.values, slot + 32 + p, yr, kv.value_dtype);
+        } else {  // a tiered value cache: the row goes through tiered_v.hip's append
+            a.value_row[head * 64 + p] = xr;
+            a.value_row[head * 64 + 32 + p] = yr;
+        }
         return;
     }
     float sn, cs;

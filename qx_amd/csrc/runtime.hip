@@ -933,8 +933,30 @@ static BlockAttention block_attention_plan(const qxh_kv_cache* c, uint32_t lengt
     return b;
 }
 
+// Block workspace: rotated query [1024], attention [1024], the new V row
+// [512] (tiered caches), then the attention's split partials.
+constexpr uint64_t kBlockScratchBytes = (2 * 1024 + 512) * sizeof(float);
+
 static uint64_t block_workspace_bytes(const BlockAttention& b) {
-    return 2 * 1024 * sizeof(float) + align256(b.plan.workspace_bytes);
+    return kBlockScratchBytes + align256(b.plan.workspace_bytes);
+}
+
+// The K/V append half of a Granite block: the QKV kernel (`launch_qkv`) with
+// V redirected to the workspace row for a tiered cache, then the tiered value
+// append.  Returns the layer view the attention must read (the boundary moves).
+template <typename Launch>
+static hipError_t block_append(qxh_kv_cache* c, uint32_t layer, uint32_t position, float* value_row, Launch launch_qkv,
+                               hipStream_t st, int* dispatches, KvLayer* after) {
+    KvLayer kv = kv_layer(c, layer, 0);
+    if (c->tiered()) kv.values = nullptr;
+    hipError_t e = launch_qkv(kv);
+    *dispatches = 1;
+    if (e == hipSuccess && c->tiered()) {
+        e = append_tiered_values(c, layer, 0, 1, position, 1, value_row, QXH_F32, st);
+        *dispatches = 2;
+    }
+    *after = kv_layer(c, layer, 0);
+    return e;
 }
 
 // Launches the attention of a block; `parts` tells the o kernel where the
@@ -967,7 +989,6 @@ extern "C" int32_t qxh_encode_granite_attention_block(qxh_graph* g, qxh_kv_cache
                                                       float* hidden_out, void* workspace, uint64_t workspace_bytes) {
     int32_t r = check_graph(g);
     if (r) return r;
-    if ((r = reject_tiered(c, "the Granite attention block"))) return r;
     if ((r = check_range(c, layer, 0, 1))) return r;
     QXH_REQUIRE(c->desc.shape == QXH_SHAPE_GRANITE, QXH_ERR_INVALID_ARGUMENT, "Granite block needs a Granite cache");
     QXH_REQUIRE(w && w->input_norm && w->q_proj && w->k_proj && w->v_proj && w->o_proj, QXH_ERR_INVALID_ARGUMENT,
@@ -995,17 +1016,21 @@ extern "C" int32_t qxh_encode_granite_attention_block(qxh_graph* g, qxh_kv_cache
     a.hidden_out = hidden_out;
     a.query_rot = reinterpret_cast<float*>(workspace);
     a.attention = a.query_rot + 1024;
+    a.value_row = a.query_rot + 2048;
     a.position = position;
-    void* attn_ws = reinterpret_cast<char*>(workspace) + 2 * 1024 * sizeof(float);
-    const KvLayer kv = kv_layer(c, layer, 0);
-    hipError_t e = launch_granite_qkv_rope(c->dims, kv, a, g->stream);
+    void* attn_ws = reinterpret_cast<char*>(workspace) + kBlockScratchBytes;
+    KvLayer kv;
+    int appends = 0;
+    hipError_t e = block_append(c, layer, position, a.value_row,
+                                [&](const KvLayer& k) { return launch_granite_qkv_rope(c->dims, k, a, g->stream); },
+                                g->stream, &appends, &kv);
     if (e != hipSuccess) return hip_fail(e, "granite qkv launch");
     int dispatches = 0;
     e = launch_block_attention(c, kv, b, length, a.query_rot, a.attention, attn_ws, g->stream, &dispatches, &a.parts);
     if (e != hipSuccess) return hip_fail(e, "granite attention launch");
     e = b.fused ? launch_granite_out_merge_residual(a, g->stream) : launch_granite_out_residual(a, g->stream);
     if (e != hipSuccess) return hip_fail(e, "granite output launch");
-    g->dispatches += 2 + dispatches;
+    g->dispatches += appends + 1 + dispatches;
     advance(c, layer, 0, 1, 1);
     return QXH_OK;
 }
@@ -1063,7 +1088,6 @@ extern "C" int32_t qxh_encode_granite_attention_block_q4(qxh_graph* g, qxh_kv_ca
                                                          uint64_t workspace_bytes) {
     int32_t r = check_graph(g);
     if (r) return r;
-    if ((r = reject_tiered(c, "the Granite Q4 attention block"))) return r;
     if ((r = check_range(c, layer, 0, 1))) return r;
     QXH_REQUIRE(c->desc.shape == QXH_SHAPE_GRANITE, QXH_ERR_INVALID_ARGUMENT, "Granite block needs a Granite cache");
     QXH_REQUIRE(w && w->input_norm, QXH_ERR_INVALID_ARGUMENT, "granite q4 block: null weights or input norm");
@@ -1096,17 +1120,21 @@ extern "C" int32_t qxh_encode_granite_attention_block_q4(qxh_graph* g, qxh_kv_ca
     a.hidden_out = hidden_out;
     a.query_rot = reinterpret_cast<float*>(workspace);
     a.attention = a.query_rot + 1024;
+    a.value_row = a.query_rot + 2048;
     a.position = position;
-    void* attn_ws = reinterpret_cast<char*>(workspace) + 2 * 1024 * sizeof(float);
-    const KvLayer kv = kv_layer(c, layer, 0);
-    hipError_t e = launch_granite_q4_qkv_rope(kv, a, g->stream);
+    void* attn_ws = reinterpret_cast<char*>(workspace) + kBlockScratchBytes;
+    KvLayer kv;
+    int appends = 0;
+    hipError_t e = block_append(c, layer, position, a.value_row,
+                                [&](const KvLayer& k) { return launch_granite_q4_qkv_rope(k, a, g->stream); },
+                                g->stream, &appends, &kv);
     if (e != hipSuccess) return hip_fail(e, "granite q4 qkv launch");
     int dispatches = 0;
     e = launch_block_attention(c, kv, b, length, a.query_rot, a.attention, attn_ws, g->stream, &dispatches, &a.parts);
     if (e != hipSuccess) return hip_fail(e, "granite q4 attention launch");
     e = b.fused ? launch_granite_q4_out_merge_residual(a, g->stream) : launch_granite_q4_out_residual(a, g->stream);
     if (e != hipSuccess) return hip_fail(e, "granite q4 output launch");
-    g->dispatches += 2 + dispatches;
+    g->dispatches += appends + 1 + dispatches;
     if (inverse_rms) {
         e = launch_rms_inverse(hidden_out, inverse_rms, g->stream);
         if (e != hipSuccess) return hip_fail(e, "granite q4 residual rms launch");

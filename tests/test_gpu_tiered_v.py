@@ -298,6 +298,88 @@ def test_tiered_prefill_on_the_pipelined_kernel(ctx, shape, kdt):
     assert worst <= TOL_16
 
 
+def test_tiered_granite_q4_block(ctx):
+    """The Granite attention half with Q4 weights on a tiered cache: the QKV
+    kernel leaves the new V row to the tiered append, which demotes the row
+    leaving the window.  The cache against the tier model bit for bit (the new
+    row bit-equal to the same block's row on an Fp32KFp16V cache), the
+    attention at the fp32 bar against the oracle over the cached rows, and
+    the o projection + residual of the GPU's attention bit for bit."""
+    from tests.test_gpu_q4 import HID, assert_bits, device_layer, q4_weights, workspace_query_and_attention
+    rng = np.random.default_rng(47)
+    nw, mats = q4_weights(rng)
+    layer = device_layer(nw, mats)
+    W, cap, p = 64, 512, 300
+    tiered = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, cap, abi.F32, abi.I8_TIERED, value_window=W)
+    plain = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, cap, abi.F32, abi.F16)
+    with rt.Graph(ctx) as g:
+        tiered.fill_normal(g, seed=5, length=p)
+        plain.fill_normal(g, seed=5, length=p)
+    h = dev(rng.standard_normal(HID, dtype=np.float32))
+    outs, wsps = [], []
+    for arena in (tiered, plain):
+        out = torch.empty(HID, device="cuda:0")
+        wsp = torch.zeros(rt.granite_block_workspace_bytes(arena, p + 1), dtype=torch.uint8, device="cuda:0")
+        with rt.Graph(ctx) as g:
+            rt.granite_attention_block_q4(g, arena, 0, p, layer, h, out, wsp)
+        outs.append(out.cpu().numpy())
+        wsps.append(wsp)
+    assert tiered.len() == p + 1 and tiered.value_tier() == p + 1 - W
+    kk, vt = values(tiered, 0, 0, p + 1)
+    _, v16 = values(plain, 0, 0, p + 1)
+    assert np.array_equal(vt[p].view(np.uint32), v16[p].astype(np.float32).view(np.uint32))
+    model = O.TieredValueCache(W)
+    model.append(np.stack([O.tiered_fill_values(5, hh, cap, p) for hh in range(KVH)], axis=1).astype(np.float32))
+    model.append(vt[p][None])
+    assert np.array_equal(vt.view(np.uint32), model.rows().view(np.uint32))
+    q_gpu, att_gpu = workspace_query_and_attention(wsps[0])
+    ref = O.KvCache(cap)
+    ref.extend(kk.cpu().numpy(), vt)
+    att_ref = O.granite_attend(q_gpu, ref, p + 1)
+    e = rel_err(att_gpu, att_ref)
+    log(f"tiered q4 block attention max-abs/rms {e:.2e}")
+    assert e <= TOL_F32
+    assert_bits(outs[0], O.granite_residual(h.cpu().numpy(), O.q4_mat_vec_simd32(mats[3], att_gpu)),
+                "o projection + residual")
+
+
+def test_tiered_granite_fp32_block(ctx):
+    """The fp32-weight Granite attention half on a tiered cache: the new V
+    row bit-equal to the same block's row on an Fp32KFp16V cache, the cache
+    against the tier model, the attention at the fp32 bar against the oracle
+    over the cached rows."""
+    from tests.test_gpu_mixed_kv import granite_weights
+    rng = np.random.default_rng(53)
+    nw, ws = granite_weights(rng)
+    layer = rt.GraniteLayer(dev(nw), *[dev(w) for w in ws])
+    W, cap, p = 32, 256, 100
+    tiered = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, cap, abi.F32, abi.I8_TIERED, value_window=W)
+    plain = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, cap, abi.F32, abi.F16)
+    with rt.Graph(ctx) as g:
+        tiered.fill_normal(g, seed=6, length=p)
+        plain.fill_normal(g, seed=6, length=p)
+    h = dev(rng.standard_normal(1024, dtype=np.float32))
+    wsps = []
+    for arena in (tiered, plain):
+        out = torch.empty(1024, device="cuda:0")
+        wsp = torch.zeros(rt.granite_block_workspace_bytes(arena, p + 1), dtype=torch.uint8, device="cuda:0")
+        with rt.Graph(ctx) as g:
+            rt.granite_attention_block(g, arena, 0, p, layer, h, out, wsp)
+        wsps.append(wsp)
+    assert tiered.value_tier() == p + 1 - W
+    kk, vt = values(tiered, 0, 0, p + 1)
+    _, v16 = values(plain, 0, 0, p + 1)
+    assert np.array_equal(vt[p].view(np.uint32), v16[p].astype(np.float32).view(np.uint32))
+    model = O.TieredValueCache(W)
+    model.append(np.stack([O.tiered_fill_values(6, hh, cap, p) for hh in range(KVH)], axis=1).astype(np.float32))
+    model.append(vt[p][None])
+    assert np.array_equal(vt.view(np.uint32), model.rows().view(np.uint32))
+    w = wsps[0][:2 * 1024 * 4].view(torch.float32).cpu().numpy()
+    ref = O.KvCache(cap)
+    ref.extend(kk.cpu().numpy(), vt)
+    assert rel_err(w[1024:], O.granite_attend(w[:1024], ref, p + 1)) <= TOL_F32
+
+
 def test_tiered_values_are_refused_where_unsupported(ctx):
     arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 2, 256, abi.F32, abi.I8_TIERED, value_window=32)
     with rt.Graph(ctx) as g:
