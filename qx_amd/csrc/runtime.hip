@@ -1163,7 +1163,6 @@ extern "C" int32_t qxh_encode_qwen_attention_block(qxh_graph* g, qxh_kv_cache* c
                                                    uint64_t workspace_bytes) {
     int32_t r = check_graph(g);
     if (r) return r;
-    if ((r = reject_tiered(c, "the Qwen attention block"))) return r;
     if ((r = check_range(c, layer, 0, 1))) return r;
     QXH_REQUIRE(c->desc.shape == QXH_SHAPE_QWEN3, QXH_ERR_INVALID_ARGUMENT, "Qwen block needs a Qwen cache");
     QXH_REQUIRE(w && w->input_norm && w->query_norm && w->key_norm && w->post_attention_norm,
@@ -1206,7 +1205,8 @@ extern "C" int32_t qxh_encode_qwen_attention_block(qxh_graph* g, qxh_kv_cache* c
     a.hidden_after = hidden_after;
     a.moe_input = moe_input;
     void* attn_ws = reinterpret_cast<char*>(workspace) + align256(kQwenBlockScratch);
-    const KvLayer kv = kv_layer(c, layer, 0);
+    KvLayer kv = kv_layer(c, layer, 0);
+    if (c->tiered()) kv.values = nullptr;  // the value row goes through the tiered append below
     hipError_t e = launch_qwen_norm_qkv(a, g->stream);
     if (e != hipSuccess) return hip_fail(e, "qwen norm + qkv launch");
     RopeAppendArgs ra{};
@@ -1224,6 +1224,12 @@ extern "C" int32_t qxh_encode_qwen_attention_block(qxh_graph* g, qxh_kv_cache* c
     ra.mode = 1;
     qwen_inverse_frequencies(ra.qwen_inv_freq);
     e = launch_rope_append(c->dims, kv, ra, g->stream);
+    int appends = 0;
+    if (e == hipSuccess && c->tiered()) {
+        e = append_tiered_values(c, layer, 0, 1, position, 1, a.value, QXH_F16, g->stream);
+        appends = 1;
+    }
+    kv = kv_layer(c, layer, 0);  // the boundary the attention reads
     if (e != hipSuccess) return hip_fail(e, "qwen rope + append launch");
     int dispatches = 0;
     e = launch_decode_attention(c->dims, kv, p, 1, length, query_rot, QXH_F16, attention, QXH_F16, attn_ws, g->stream,
@@ -1233,7 +1239,7 @@ extern "C" int32_t qxh_encode_qwen_attention_block(qxh_graph* g, qxh_kv_cache* c
     if (e != hipSuccess) return hip_fail(e, "qwen o projection launch");
     e = launch_qwen_residual_norm(a, g->stream);
     if (e != hipSuccess) return hip_fail(e, "qwen residual norm launch");
-    g->dispatches += 4 + dispatches;
+    g->dispatches += 4 + appends + dispatches;
     advance(c, layer, 0, 1, 1);
     return QXH_OK;
 }

@@ -380,6 +380,44 @@ def test_tiered_granite_fp32_block(ctx):
     assert rel_err(w[1024:], O.granite_attend(w[:1024], ref, p + 1)) <= TOL_F32
 
 
+def test_tiered_qwen_block(ctx):
+    """The Qwen attention half (Q4 projections) on a tiered cache with f16
+    keys: the value row reaches the cache through the tiered append (the
+    window row it leaves quantised), attention on the MFMA tiered decode.
+    The cache against the tier model with the new row equal to the block's
+    own V stage bit for bit; attention against float64 over the cached rows
+    and the o projection of the GPU's attention against the oracle, at the
+    16-bit bar."""
+    from tests.test_gpu_qwen_block import err16, f16, weights, workspace_stages
+    rng = np.random.default_rng(59)
+    mats, _, layer = weights(rng)
+    W, cap, pos = 64, 512, 300
+    arena = rt.KvArena(ctx, abi.SHAPE_QWEN3, 1, 1, cap, abi.F16, abi.I8_TIERED, value_window=W)
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=4, length=pos)
+    h = rng.standard_normal(2048).astype(np.float16)
+    after = torch.empty(2048, dtype=torch.int16, device="cuda:0")
+    moe = torch.empty_like(after)
+    wsp = torch.zeros(rt.qwen_block_workspace_bytes(arena, pos + 1), dtype=torch.uint8, device="cuda:0")
+    with rt.Graph(ctx) as g:
+        rt.qwen_attention_block(g, arena, 0, pos, layer, dev(h.view(np.int16)), after, moe, wsp)
+    assert arena.len() == pos + 1 and arena.value_tier() == pos + 1 - W
+    _, _, v, qrot, att, proj = workspace_stages(wsp)
+    kk, vt = values(arena, 0, 0, pos + 1)
+    assert np.array_equal(vt[pos].ravel().view(np.uint32), f16(v).view(np.uint32))
+    model = O.TieredValueCache(W, 4, 128)
+    model.append(np.stack([O.tiered_fill_values(4, hh, cap, pos, 128) for hh in range(4)], axis=1).astype(np.float32))
+    model.append(vt[pos][None])
+    assert np.array_equal(vt.view(np.uint32), model.rows().view(np.uint32))
+    kf = kk.float().cpu().numpy()
+    ref_att = attend64(f16(qrot).reshape(32, 128), kf, vt, 1 / np.sqrt(128)).ravel()
+    e_att = err16(f16(att), ref_att)
+    log(f"tiered qwen block attention err16 {e_att:.2e}")
+    assert e_att <= TOL_16
+    ref_proj = O.q4_mat_vec(mats[3], f16(att)).astype(np.float16).astype(np.float32)
+    assert err16(f16(proj), ref_proj) <= TOL_16
+
+
 def test_tiered_values_are_refused_where_unsupported(ctx):
     arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 2, 256, abi.F32, abi.I8_TIERED, value_window=32)
     with rt.Graph(ctx) as g:
