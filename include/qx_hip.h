@@ -255,8 +255,8 @@ QXH_API int32_t qxh_encode_rope_kv_for_layer(qxh_graph* graph, qxh_kv_cache* cac
  * sequence 0, the pair GpuRuntimeBuffers::encode_attention_layer_with_plan
  * issues (crates/qx-runtime-v2/src/lib.rs:6942-6982).  Up to 1024 positions it
  * is one dispatch (one workgroup per kv head streams the whole context; the
- * appended row is used from registers); longer contexts take the two-call
- * path, which needs query_output and a workspace of
+ * appended row is used from registers); longer contexts and tiered value
+ * caches take the two-call path, which needs query_output and a workspace of
  * qxh_attention_workspace_bytes(cache, 1, position + 1) bytes.  query_output
  * (rotated q, fp32) may be null on the one-dispatch path and may equal query.
  * The appended K/V bits equal those of qxh_encode_rope_kv_for_layer. */

@@ -664,7 +664,6 @@ extern "C" int32_t qxh_encode_decode_step_for_layer(qxh_graph* g, qxh_kv_cache* 
                                                     int32_t output_dtype, void* workspace, uint64_t workspace_bytes) {
     int32_t r = check_graph(g);
     if (r) return r;
-    if ((r = reject_tiered(c, "the one-dispatch decode step"))) return r;
     if ((r = check_range(c, layer, 0, 1))) return r;
     QXH_REQUIRE(c->desc.shape == QXH_SHAPE_GRANITE, QXH_ERR_INVALID_ARGUMENT,
                 "decode_step is the Granite single-token entry point");
@@ -676,10 +675,12 @@ extern "C" int32_t qxh_encode_decode_step_for_layer(qxh_graph* g, qxh_kv_cache* 
     QXH_REQUIRE(position <= 4096, QXH_ERR_INVALID_ARGUMENT, "unregistered Granite RoPE coordinate %u", position);
     if ((r = check_append(c, layer, 0, 1, position, 1))) return r;
     const uint32_t length = position + 1;
-    if (length > kDecodeStepMaxLength) {
-        // long context: the two-call path (append, then split-K attention)
+    if (length > kDecodeStepMaxLength || c->tiered()) {
+        // long context, or a tiered value cache (whose value row goes through
+        // the tiered append): the two-call path (append, then split-K attention)
         QXH_REQUIRE(query_output, QXH_ERR_INVALID_ARGUMENT,
-                    "decode_step beyond %u positions needs query_output for the rotated query", kDecodeStepMaxLength);
+                    "decode_step beyond %u positions or on a tiered value cache needs query_output for the rotated "
+                    "query", kDecodeStepMaxLength);
         const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, c->desc.value_dtype, 1, length);
         QXH_REQUIRE(workspace_bytes >= p.workspace_bytes && (p.workspace_bytes == 0 || workspace),
                     QXH_ERR_INVALID_ARGUMENT, "decode_step workspace holds %llu bytes, needs %llu",

@@ -306,7 +306,7 @@ def decode_step(graph: Graph, cache: KvArena, layer: int, position: int, query, 
         out = torch.empty((cache.info.q_heads, cache.info.head_dim), dtype=out_dtype or torch.float32,
                           device=query.device)
     ws_bytes = 0
-    if workspace is None and position + 1 > 1024:
+    if workspace is None and (position + 1 > 1024 or cache.value_dtype == abi.I8_TIERED):  # the two-call path
         need = attention_workspace_bytes(cache, 1, position + 1)
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=query.device) if need else None
     if workspace is not None:

@@ -418,6 +418,29 @@ def test_tiered_qwen_block(ctx):
     assert err16(f16(proj), ref_proj) <= TOL_16
 
 
+def test_tiered_decode_step_is_the_two_call_path(ctx):
+    """qxh_encode_decode_step_for_layer on a tiered cache: the same bits as
+    the RoPE append + attention calls on an identically filled cache."""
+    rng = np.random.default_rng(61)
+    q, k, v = (dev(rng.standard_normal(s, dtype=np.float32)) for s in ((16, 64), (8, 64), (8, 64)))
+    outs = []
+    for step in (True, False):
+        arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, 256, abi.F32, abi.I8_TIERED, value_window=32)
+        with rt.Graph(ctx) as g:
+            arena.fill_normal(g, seed=8, length=100)
+        qo = torch.empty_like(q)
+        ws = torch.empty(max(rt.attention_workspace_bytes(arena, 1, 101), 1), dtype=torch.uint8, device="cuda:0")
+        with rt.Graph(ctx) as g:
+            if step:
+                out = rt.decode_step(g, arena, 0, 100, q, k, v, query_out=qo, workspace=ws)
+            else:
+                rt.rope_kv_batch(g, arena, 0, 100, q[None, None], k[None, None], v[None, None], query_out=qo[None, None])
+                out = rt.attention(g, arena, 0, qo[None], 101, workspace=ws)[0]
+        assert arena.len() == 101 and arena.value_tier() == 101 - 32
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
+
+
 def test_tiered_values_are_refused_where_unsupported(ctx):
     arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 2, 256, abi.F32, abi.I8_TIERED, value_window=32)
     with rt.Graph(ctx) as g:
@@ -425,7 +448,9 @@ def test_tiered_values_are_refused_where_unsupported(ctx):
     q = torch.zeros((16, 64), device="cuda:0")
     kv = torch.zeros((8, 64), device="cuda:0")
     with rt.Graph(ctx) as g:
-        with pytest.raises(abi.QxhError, match="tiered"):
+        # the decode step takes the two-call path on a tiered cache, which
+        # needs the rotated query's buffer
+        with pytest.raises(abi.QxhError, match="tiered value cache needs query_output"):
             rt.decode_step(g, arena, 0, 100, q, kv, kv)
         with pytest.raises(abi.QxhError, match="tiered"):
             arena.leaf_hashes(g, 0, 0, 4)
