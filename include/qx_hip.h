@@ -206,7 +206,13 @@ QXH_API int32_t qxh_kv_cache_reset(qxh_kv_cache* cache);
 QXH_API int32_t qxh_kv_cache_rollback(qxh_kv_cache* cache, uint32_t sequence, uint32_t length);
 /* commit_kv (crates/qx-runtime-v2/src/lib.rs:3290-3310) counterpart used for
  * caches whose rows were written in bulk (fill / store): set every cursor of
- * `sequence` (UINT32_MAX: all sequences) to `length` <= capacity. */
+ * `sequence` (UINT32_MAX: all sequences) to `length` <= capacity.
+ * QXH_I8_TIERED: rows enter a tiered cache only through the library's
+ * appends, stores and fill (they keep the window's position tags and the tier
+ * boundary); rows written into the arena by other means are not tracked and
+ * read back unspecified.  A length above min(boundary, length) + value_window
+ * is rejected with QXH_ERR_KV_POSITION, since such rows cannot all sit in the
+ * window. */
 QXH_API int32_t qxh_kv_cache_set_len(qxh_kv_cache* cache, uint32_t sequence, uint32_t length);
 QXH_API int32_t qxh_kv_cache_layout(const qxh_kv_cache* cache, qxh_kv_layout* out);
 QXH_API int32_t qxh_kv_cache_desc(const qxh_kv_cache* cache, qxh_kv_desc* out);

@@ -464,6 +464,19 @@ extern "C" int32_t qxh_kv_cache_set_len(qxh_kv_cache* c, uint32_t seq, uint32_t 
                 seq);
     QXH_REQUIRE(length <= c->desc.capacity, QXH_ERR_KV_POSITION, "KV length %u exceeds context %u", length,
                 c->desc.capacity);
+    // Tiered values: the rows [boundary, length) must all sit in the window,
+    // or decode would read slots that hold other (or already quantised) rows
+    // and the next append would give two rows one slot.  A raise may only
+    // recommit rows that are still in the window.
+    if (c->tiered())
+        for (uint32_t l = 0; l < c->desc.layers; ++l)
+            for (uint32_t s = 0; s < c->desc.sequences; ++s)
+                if (seq == UINT32_MAX || s == seq)
+                    QXH_REQUIRE((uint64_t)length <= (uint64_t)std::min(c->tier_at(l, s), length) + c->desc.value_window,
+                                QXH_ERR_KV_POSITION,
+                                "KV length %u leaves more than the value window (%u) above the tier boundary %u "
+                                "(layer %u, sequence %u)",
+                                length, c->desc.value_window, c->tier_at(l, s), l, s);
     for (uint32_t l = 0; l < c->desc.layers; ++l)
         for (uint32_t s = 0; s < c->desc.sequences; ++s)
             if (seq == UINT32_MAX || s == seq) {
@@ -590,6 +603,13 @@ static int32_t check_append(qxh_kv_cache* c, uint32_t layer, uint32_t first, uin
     }
     QXH_REQUIRE((uint64_t)start + tokens <= c->desc.capacity, QXH_ERR_KV_POSITION, "KV position %llu exceeds context %u",
                 (unsigned long long)start + tokens - 1, c->desc.capacity);
+    // Tiered values: one wave owns each window slot of an append only while
+    // the rows leaving the window, [boundary, start), fit in one window.
+    if (c->tiered())
+        for (uint32_t s = first; s < first + count; ++s)
+            QXH_REQUIRE(start - std::min(c->tier_at(layer, s), start) <= c->desc.value_window, QXH_ERR_KV_POSITION,
+                        "tiered append at %u: %u rows above the tier boundary exceed the value window %u (sequence %u)",
+                        start, start - std::min(c->tier_at(layer, s), start), c->desc.value_window, s);
     return QXH_OK;
 }
 

@@ -112,6 +112,25 @@ def test_tiered_appends_and_rollbacks_match_the_model(ctx):
     assert [arena.value_tier(0, s) for s in range(2)] == [min(b, 3) for b in before]
 
 
+def test_tiered_set_len_cannot_raise_past_the_window(ctx):
+    """A cursor raise on a tiered cache may only recommit rows that are still
+    in the window: after a fill of 4096 rows (window 256) and set_len(100),
+    set_len(4096) would claim rows [100, 4096) whose slots hold other rows."""
+    W = 256
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, 4096, abi.F32, abi.I8_TIERED, value_window=W)
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=7, length=4096)
+    assert arena.value_tier() == 4096 - W
+    arena.set_len(100)
+    assert arena.value_tier() == 100 and arena.len() == 100
+    with pytest.raises(abi.QxhError, match="value window") as ei:
+        arena.set_len(4096)
+    assert ei.value.code == abi.QXH_ERR_KV_POSITION
+    assert arena.len() == 100 and arena.value_tier() == 100  # unchanged by the refused call
+    arena.set_len(100 + W)  # every row of [100, 356) is still in its slot
+    assert arena.len() == 100 + W and arena.value_tier() == 100
+
+
 @pytest.mark.parametrize("kdt", [abi.F32, abi.F16])
 @pytest.mark.parametrize("length", [1, 300, 4096])
 def test_tiered_decode_matches_oracle(ctx, kdt, length):
