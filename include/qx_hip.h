@@ -294,6 +294,20 @@ QXH_API int32_t qxh_encode_attention_for_layer(qxh_graph* graph, qxh_kv_cache* c
                                        uint32_t first_sequence, uint32_t sequences, uint32_t length,
                                        const void* query, int32_t query_dtype, void* output,
                                        int32_t output_dtype, void* workspace, uint64_t workspace_bytes);
+/* No counterpart in the reference.  For callers that cannot allocate (code
+ * under HIP-graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): qxh_encode_attention_for_layer without a workspace, its split
+ * partials kept in a per-GPU device scratch of 16 MiB that the library
+ * reserves at load and holds until the process ends.  It allocates nothing.
+ * Results equal those of qxh_encode_attention_for_layer bit for bit.  Calls
+ * needing more partial bytes than the scratch holds (qxh_attention_workspace_bytes
+ * > 16 MiB) return QXH_ERR_INVALID_ARGUMENT.  Every call on one GPU shares
+ * that GPU's scratch: calls that may overlap on one GPU (other streams, other
+ * threads) race and must be ordered by the caller. */
+QXH_API int32_t qxh_encode_attention_for_layer_no_alloc(qxh_graph* graph, qxh_kv_cache* cache, uint32_t layer,
+                                                        uint32_t first_sequence, uint32_t sequences, uint32_t length,
+                                                        const void* query, int32_t query_dtype, void* output,
+                                                        int32_t output_dtype);
 
 /* Causal prefill attention: query row t of `tokens` (positions
  * start_position + t) attends to cache positions [0, start_position + t].

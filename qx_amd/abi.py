@@ -115,6 +115,8 @@ SIGNATURES = {
     "qxh_attention_workspace_bytes": (c_int32, [c_void_p, c_uint32, c_uint32, P(c_uint64)]),
     "qxh_encode_attention_for_layer": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32,
                                                  c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_uint64]),
+    "qxh_encode_attention_for_layer_no_alloc": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32, c_uint32,
+                                                          c_uint32, c_void_p, c_int32, c_void_p, c_int32]),
     "qxh_prefill_workspace_bytes": (c_int32, [c_void_p, c_uint32, P(c_uint64)]),
     "qxh_encode_prefill_attention": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32,
                                                c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_uint64]),

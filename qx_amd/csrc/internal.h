@@ -93,6 +93,13 @@ hipError_t launch_kv_fill_normal(const ShapeDims& s, const KvLayer& kv_all_layer
 hipError_t launch_conformance(const float* in, const uint32_t* coords, uint32_t n, uint32_t* e, uint32_t* r, uint32_t* sn,
                               uint32_t* cs, hipStream_t st);
 
+// noalloc.hip: the per-GPU device scratch of the entry points that allocate
+// nothing.  noalloc_scratch_init resolves the calling device's copy (the
+// device must be current); noalloc_scratch returns it (null before init).
+constexpr uint64_t kNoAllocScratchBytes = 16ull << 20;
+hipError_t noalloc_scratch_init(int device);
+void* noalloc_scratch(int device);
+
 // Decode attention plan chosen on the host.
 struct DecodePlan {
     uint32_t splits;        // context splits per (sequence, kv_head)

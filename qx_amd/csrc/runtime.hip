@@ -154,6 +154,8 @@ extern "C" int32_t qxh_context_create(int32_t device, qxh_context** out) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(QXH_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
     if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+    // this device's copy of the no-alloc scratch, resolved once with the device current
+    if ((e = noalloc_scratch_init(device)) != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(no-alloc scratch)");
     qxh_context* c = new qxh_context();
     c->device = device;
     c->metrics = qxh_metrics{0, 0, 0.0};
@@ -774,10 +776,11 @@ extern "C" int32_t qxh_attention_workspace_bytes(const qxh_kv_cache* c, uint32_t
     return QXH_OK;
 }
 
-extern "C" int32_t qxh_encode_attention_for_layer(qxh_graph* g, qxh_kv_cache* c, uint32_t layer, uint32_t first,
-                                                  uint32_t count, uint32_t length, const void* query,
-                                                  int32_t query_dtype, void* output, int32_t output_dtype,
-                                                  void* workspace, uint64_t workspace_bytes) {
+// Validation, plan and launch of decode attention; `workspace` holds
+// `workspace_bytes` (the caller's, or the no-alloc scratch).
+static int32_t encode_attention(qxh_graph* g, qxh_kv_cache* c, uint32_t layer, uint32_t first, uint32_t count,
+                                uint32_t length, const void* query, int32_t query_dtype, void* output,
+                                int32_t output_dtype, void* workspace, uint64_t workspace_bytes, bool scratch) {
     int32_t r = check_graph(g);
     if (r) return r;
     if ((r = check_range(c, layer, first, count))) return r;
@@ -793,15 +796,43 @@ extern "C" int32_t qxh_encode_attention_for_layer(qxh_graph* g, qxh_kv_cache* c,
                 c->desc.value_dtype);
     if ((r = check_equal_tiers(c, layer, first, count))) return r;
     const DecodePlan p = plan_decode(c->dims, c->desc.key_dtype, c->desc.value_dtype, count, length);
-    QXH_REQUIRE(workspace_bytes >= p.workspace_bytes && (p.workspace_bytes == 0 || workspace),
-                QXH_ERR_INVALID_ARGUMENT, "attention workspace holds %llu bytes, needs %llu",
-                (unsigned long long)workspace_bytes, (unsigned long long)p.workspace_bytes);
+    if (scratch)
+        QXH_REQUIRE(p.workspace_bytes <= workspace_bytes, QXH_ERR_INVALID_ARGUMENT,
+                    "attention_no_alloc: %u sequences at length %u need %llu bytes of split partials, above the "
+                    "%llu-byte device scratch; use qxh_encode_attention_for_layer with a workspace",
+                    count, length, (unsigned long long)p.workspace_bytes, (unsigned long long)workspace_bytes);
+    else
+        QXH_REQUIRE(workspace_bytes >= p.workspace_bytes && (p.workspace_bytes == 0 || workspace),
+                    QXH_ERR_INVALID_ARGUMENT, "attention workspace holds %llu bytes, needs %llu",
+                    (unsigned long long)workspace_bytes, (unsigned long long)p.workspace_bytes);
     int dispatches = 0;
     hipError_t e = launch_decode_attention(c->dims, kv_layer(c, layer, first), p, count, length, query, query_dtype,
                                            output, output_dtype, workspace, g->stream, &dispatches);
     if (e != hipSuccess) return hip_fail(e, "attention launch");
     g->dispatches += dispatches;
     return QXH_OK;
+}
+
+extern "C" int32_t qxh_encode_attention_for_layer(qxh_graph* g, qxh_kv_cache* c, uint32_t layer, uint32_t first,
+                                                  uint32_t count, uint32_t length, const void* query,
+                                                  int32_t query_dtype, void* output, int32_t output_dtype,
+                                                  void* workspace, uint64_t workspace_bytes) {
+    return encode_attention(g, c, layer, first, count, length, query, query_dtype, output, output_dtype, workspace,
+                            workspace_bytes, false);
+}
+
+// The same attention with the split partials in the device's no-alloc
+// scratch (noalloc.hip): no allocation of any kind on this path.
+extern "C" int32_t qxh_encode_attention_for_layer_no_alloc(qxh_graph* g, qxh_kv_cache* c, uint32_t layer,
+                                                           uint32_t first, uint32_t count, uint32_t length,
+                                                           const void* query, int32_t query_dtype, void* output,
+                                                           int32_t output_dtype) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    void* ws = noalloc_scratch(g->ctx->device);
+    QXH_REQUIRE(ws, QXH_ERR_HIP, "attention_no_alloc: device %d has no resolved scratch", g->ctx->device);
+    return encode_attention(g, c, layer, first, count, length, query, query_dtype, output, output_dtype, ws,
+                            kNoAllocScratchBytes, true);
 }
 
 extern "C" int32_t qxh_prefill_workspace_bytes(const qxh_kv_cache* c, uint32_t tokens, uint64_t* bytes) {

@@ -337,6 +337,19 @@ def attention(graph: Graph, cache: KvArena, layer: int, query, length: int, out=
     return out
 
 
+def attention_no_alloc(graph: Graph, cache: KvArena, layer: int, query, length: int, out, first_sequence: int = 0):
+    """Decode attention through qxh_encode_attention_for_layer_no_alloc: the
+    split partials live in the library's per-GPU device scratch, so the call
+    allocates nothing (out must be given)."""
+    seqs = query.shape[0]
+    if query.shape[1:] != (cache.info.q_heads, cache.info.head_dim):
+        raise ValueError(f"query must be [S][{cache.info.q_heads}][{cache.info.head_dim}]")
+    check(lib().qxh_encode_attention_for_layer_no_alloc(graph.handle, cache.handle, layer, first_sequence, seqs,
+                                                        length, _ptr(query), qxh_dtype(query), _ptr(out),
+                                                        qxh_dtype(out)))
+    return out
+
+
 def prefill_workspace_bytes(cache: KvArena, tokens: int) -> int:
     n = ctypes.c_uint64()
     check(lib().qxh_prefill_workspace_bytes(cache.handle, tokens, ctypes.byref(n)))
