@@ -140,6 +140,35 @@ QXH_API int32_t qxh_graph_finish(qxh_graph* graph, qxh_graph_metrics* metrics);
 /* Release a graph without waiting (work already enqueued still runs). */
 QXH_API int32_t qxh_graph_discard(qxh_graph* graph);
 
+/* ---- runtime buffers -----------------------------------------------------------
+ * Replaces RuntimeBuffer and its MetalContext helpers
+ * (crates/qx-metal/src/lib.rs:1368-1396, allocate_runtime_buffer :9847-9860,
+ * write_runtime_buffer :9920-9936, read_runtime_{u32,f32,f16} :9938-9999):
+ * device memory allocated once at initialisation and bound to encoders through
+ * views.  A view is {allocation, byte offset, byte length} passed by value;
+ * views never own, the caller frees the allocation once, after the last graph
+ * that uses it has completed.  Reads and writes are synchronous copies
+ * (host <-> device) of at most the view's length, at its start. */
+typedef struct qxh_buffer qxh_buffer;
+typedef struct {
+    qxh_buffer* buffer;
+    uint64_t offset;
+    uint64_t length;
+} qxh_buffer_view;
+
+/* allocate_runtime_buffer: `bytes` > 0, 256-byte aligned device memory. */
+QXH_API int32_t qxh_buffer_alloc(qxh_context* ctx, uint64_t bytes, qxh_buffer_view* out);
+QXH_API int32_t qxh_buffer_free(qxh_buffer* buffer);
+/* RuntimeBuffer::subregion: offset + length must stay inside the parent view. */
+QXH_API int32_t qxh_buffer_subregion(qxh_buffer_view parent, uint64_t offset, uint64_t length, qxh_buffer_view* out);
+/* The device address of a view, for the encoders' pointer arguments. */
+QXH_API int32_t qxh_buffer_device_ptr(qxh_buffer_view view, void** ptr);
+/* write_runtime_buffer: copies `bytes` host bytes to the view's start;
+ * more than the view's length is an error. */
+QXH_API int32_t qxh_buffer_write(qxh_buffer_view view, const void* data, uint64_t bytes);
+/* read_runtime_*: copies `bytes` (at most the view's length) to the host. */
+QXH_API int32_t qxh_buffer_read(qxh_buffer_view view, void* data, uint64_t bytes);
+
 /* HIP-graph capture of everything encoded between capture_begin and
  * capture_end, for launch-bound loops (replaces one command buffer per token,
  * docs/qx-current-status.md:56-57).  Host-side KV cursors advance once, at
@@ -485,6 +514,27 @@ QXH_API int32_t qxh_encode_qwen_attention_block(qxh_graph* graph, qxh_kv_cache* 
                                                 uint32_t position, const qxh_qwen_q4_layer_weights* weights,
                                                 const uint16_t* hidden, uint16_t* hidden_after_attention,
                                                 uint16_t* moe_input, void* workspace, uint64_t workspace_bytes);
+
+/* ---- synchronous Qwen helpers --------------------------------------------------
+ * MetalContext::run_qwen_qk_norm_rope (crates/qx-metal/src/lib.rs:14373-14483):
+ * host arrays in and out, executed and waited for on the context's stream.
+ * query [32 x 128] and key [4 x 128] are 16-bit bit patterns of `dtype`
+ * (QXH_F16 as the reference, or QXH_BF16); query_norm and key_norm are 128
+ * floats.  The normalised, rotated rows are written to query_out and key_out
+ * (which may equal query and key).  Lengths are element counts, checked as the
+ * reference checks its slices ("invalid Qwen Q/K shapes"). */
+QXH_API int32_t qxh_run_qwen_qk_norm_rope(qxh_context* ctx, const uint16_t* query, size_t query_len,
+                                          const uint16_t* key, size_t key_len, const float* query_norm,
+                                          size_t query_norm_len, const float* key_norm, size_t key_norm_len,
+                                          int32_t dtype, uint32_t position, uint16_t* query_out, uint16_t* key_out);
+/* MetalContext::run_qwen_gqa_attention (crates/qx-metal/src/lib.rs:14488-14599):
+ * query [32 x 128] over position-major caches [context][4][128] (16-bit bit
+ * patterns of `dtype`); output [32 x 128] in the same dtype.  The context is
+ * key_len / 512 positions; key_len must equal value_len, be positive and a
+ * multiple of 512 ("invalid Qwen GQA shapes"). */
+QXH_API int32_t qxh_run_qwen_gqa_attention(qxh_context* ctx, const uint16_t* query, size_t query_len,
+                                           const uint16_t* key_cache, size_t key_len, const uint16_t* value_cache,
+                                           size_t value_len, int32_t dtype, uint16_t* output);
 
 /* ---- synthetic data (bench / tests) ------------------------------------------
  * Counter-based N(0, stddev^2) values (SplitMix64 -> Box-Muller), on device. */

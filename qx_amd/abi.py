@@ -44,6 +44,10 @@ class GraphMetrics(ctypes.Structure):
     _fields_ = [("dispatches", c_uint32), ("gpu_ms", c_float)]
 
 
+class BufferView(ctypes.Structure):
+    _fields_ = [("buffer", c_void_p), ("offset", c_uint64), ("length", c_uint64)]
+
+
 class KvDesc(ctypes.Structure):
     _fields_ = [("shape", c_int32), ("key_dtype", c_int32), ("value_dtype", c_int32), ("layers", c_uint32),
                 ("sequences", c_uint32), ("capacity", c_uint32), ("value_window", c_uint32)]
@@ -93,6 +97,12 @@ SIGNATURES = {
     "qxh_graph_capture_end": (c_int32, [c_void_p, P(c_void_p)]),
     "qxh_replay_launch": (c_int32, [c_void_p, c_void_p]),
     "qxh_replay_destroy": (c_int32, [c_void_p]),
+    "qxh_buffer_alloc": (c_int32, [c_void_p, c_uint64, P(BufferView)]),
+    "qxh_buffer_free": (c_int32, [c_void_p]),
+    "qxh_buffer_subregion": (c_int32, [BufferView, c_uint64, c_uint64, P(BufferView)]),
+    "qxh_buffer_device_ptr": (c_int32, [BufferView, P(c_void_p)]),
+    "qxh_buffer_write": (c_int32, [BufferView, c_void_p, c_uint64]),
+    "qxh_buffer_read": (c_int32, [BufferView, c_void_p, c_uint64]),
     "qxh_kv_cache_bytes": (c_int32, [P(KvDesc), P(c_uint64)]),
     "qxh_kv_cache_create": (c_int32, [c_void_p, P(KvDesc), c_void_p, c_uint64, P(c_void_p)]),
     "qxh_kv_cache_destroy": (c_int32, [c_void_p]),
@@ -140,6 +150,10 @@ SIGNATURES = {
     "qxh_qwen_block_workspace_bytes": (c_int32, [c_void_p, c_uint32, P(c_uint64)]),
     "qxh_encode_qwen_attention_block": (c_int32, [c_void_p, c_void_p, c_uint32, c_uint32, P(QwenQ4LayerWeights),
                                                   c_void_p, c_void_p, c_void_p, c_void_p, c_uint64]),
+    "qxh_run_qwen_qk_norm_rope": (c_int32, [c_void_p, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_size_t,
+                                            c_void_p, c_size_t, c_int32, c_uint32, c_void_p, c_void_p]),
+    "qxh_run_qwen_gqa_attention": (c_int32, [c_void_p, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_size_t,
+                                             c_int32, c_void_p]),
     "qxh_encode_fill_normal": (c_int32, [c_void_p, c_void_p, c_int32, c_uint64, c_uint64, c_float]),
     "qxh_encode_hbm_read_probe": (c_int32, [c_void_p, c_void_p, c_uint64, c_void_p, c_uint32]),
     "qxh_encode_kv_fill_normal": (c_int32, [c_void_p, c_void_p, c_uint64, c_uint32]),

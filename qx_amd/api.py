@@ -15,11 +15,13 @@ enqueued on the GPU through libqx_hip and waited on before returning.
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import torch
 
 from . import runtime as rt
-from .abi import BF16, F16, F32, SHAPE_GRANITE, SHAPE_QWEN3, QxhError
+from .abi import BF16, F16, F32, SHAPE_GRANITE, SHAPE_QWEN3, QxhError, check, lib
 
 _ctx = None
 
@@ -88,38 +90,34 @@ def granite_attention_decode(query, key, value, position: int, cache: KvCache):
     return out.reshape(-1).cpu().numpy()
 
 
-def _bits_tensor(bits, fmt):
-    arr = np.ascontiguousarray(bits, dtype=np.uint16)
-    t = torch.from_numpy(arr.view(np.int16).copy()).to("cuda:0")
-    return t.view(torch.float16 if fmt == F16 else torch.bfloat16)
+def _u16(a):
+    return np.ascontiguousarray(a, dtype=np.uint16)
 
 
-def _to_bits(t):
-    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+def _f32c(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _np_ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
 
 
 def run_qwen_qk_norm_rope(query_bits, key_bits, query_norm, key_norm, position: int, fmt: int = F16):
-    """MetalContext::run_qwen_qk_norm_rope (crates/qx-metal/src/lib.rs:14373-14483)."""
-    q = _bits_tensor(query_bits, fmt)
-    k = _bits_tensor(key_bits, fmt)
-    qn, kn = _dev(query_norm), _dev(key_norm)
-    with rt.Graph(context()) as g:
-        rt.qwen_qk_norm_rope(g, q, k, position, qn, kn)
-    return _to_bits(q), _to_bits(k)
+    """MetalContext::run_qwen_qk_norm_rope (crates/qx-metal/src/lib.rs:14373-14483),
+    through the C ABI's synchronous qxh_run_qwen_qk_norm_rope."""
+    q, k, qn, kn = _u16(query_bits), _u16(key_bits), _f32c(query_norm), _f32c(key_norm)
+    qo, ko = np.empty_like(q), np.empty_like(k)
+    check(lib().qxh_run_qwen_qk_norm_rope(context().handle, _np_ptr(q), q.size, _np_ptr(k), k.size, _np_ptr(qn),
+                                          qn.size, _np_ptr(kn), kn.size, fmt, position, _np_ptr(qo), _np_ptr(ko)))
+    return qo, ko
 
 
 def run_qwen_gqa_attention(query_bits, key_cache_bits, value_cache_bits, fmt: int = F16):
-    """MetalContext::run_qwen_gqa_attention (crates/qx-metal/src/lib.rs:14488-14599):
-    q [4096], position-major caches [ctx][4][128] (16-bit), output [4096]."""
-    kc = np.ascontiguousarray(key_cache_bits, dtype=np.uint16)
-    context_len = kc.size // 512
-    if context_len == 0:
-        raise QxhError(1, "Qwen GQA buffers are smaller than the requested context")
-    arena = rt.KvArena(context(), SHAPE_QWEN3, 1, 1, context_len, fmt)
-    k = _bits_tensor(kc, fmt).reshape(1, context_len, 4, 128)
-    v = _bits_tensor(value_cache_bits, fmt).reshape(1, context_len, 4, 128)
-    q = _bits_tensor(query_bits, fmt).reshape(1, 32, 128)
-    with rt.Graph(context()) as g:
-        rt.store_kv(g, arena, 0, 0, k, v)
-        out = rt.attention(g, arena, 0, q, context_len)
-    return _to_bits(out).reshape(-1)
+    """MetalContext::run_qwen_gqa_attention (crates/qx-metal/src/lib.rs:14488-14599),
+    through the C ABI's synchronous qxh_run_qwen_gqa_attention: q [4096],
+    position-major caches [ctx][4][128] (16-bit), output [4096]."""
+    q, kc, vc = _u16(query_bits), _u16(key_cache_bits), _u16(value_cache_bits)
+    out = np.empty(4096, np.uint16)
+    check(lib().qxh_run_qwen_gqa_attention(context().handle, _np_ptr(q), q.size, _np_ptr(kc), kc.size, _np_ptr(vc),
+                                           vc.size, fmt, _np_ptr(out)))
+    return out

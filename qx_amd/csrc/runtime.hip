@@ -319,6 +319,89 @@ extern "C" int32_t qxh_replay_destroy(qxh_replay* r) {
 }
 
 // ---------------------------------------------------------------------------
+// runtime buffers (RuntimeBuffer, crates/qx-metal/src/lib.rs:1368-1396)
+// ---------------------------------------------------------------------------
+struct qxh_buffer {
+    int device;
+    char* base;
+    uint64_t bytes;
+};
+
+static int32_t check_view(const qxh_buffer_view& v, const char* what) {
+    QXH_REQUIRE(v.buffer, QXH_ERR_INVALID_ARGUMENT, "%s: null buffer", what);
+    QXH_REQUIRE(v.offset <= v.buffer->bytes && v.length <= v.buffer->bytes - v.offset, QXH_ERR_INVALID_ARGUMENT,
+                "%s: view [%llu, +%llu) exceeds its %llu-byte allocation", what, (unsigned long long)v.offset,
+                (unsigned long long)v.length, (unsigned long long)v.buffer->bytes);
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_buffer_alloc(qxh_context* ctx, uint64_t bytes, qxh_buffer_view* out) {
+    QXH_REQUIRE(ctx && out, QXH_ERR_INVALID_ARGUMENT, "buffer_alloc: null argument");
+    QXH_REQUIRE(bytes > 0, QXH_ERR_INVALID_ARGUMENT, "runtime buffers cannot be empty");
+    *out = qxh_buffer_view{nullptr, 0, 0};
+    hipError_t e = hipSetDevice(ctx->device);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return hip_fail(e, "runtime buffer allocation");
+    *out = qxh_buffer_view{new qxh_buffer{ctx->device, (char*)p, bytes}, 0, bytes};
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_buffer_free(qxh_buffer* b) {
+    if (!b) return QXH_OK;
+    (void)hipSetDevice(b->device);
+    hipError_t e = hipFree(b->base);
+    delete b;
+    if (e != hipSuccess) return hip_fail(e, "runtime buffer free");
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_buffer_subregion(qxh_buffer_view parent, uint64_t offset, uint64_t length,
+                                        qxh_buffer_view* out) {
+    int32_t r = check_view(parent, "buffer_subregion");
+    if (r) return r;
+    QXH_REQUIRE(out, QXH_ERR_INVALID_ARGUMENT, "buffer_subregion: null output");
+    QXH_REQUIRE(offset <= UINT64_MAX - length, QXH_ERR_INVALID_ARGUMENT, "runtime buffer region overflows");
+    QXH_REQUIRE(offset + length <= parent.length, QXH_ERR_INVALID_ARGUMENT, "runtime buffer region exceeds its parent");
+    *out = qxh_buffer_view{parent.buffer, parent.offset + offset, length};
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_buffer_device_ptr(qxh_buffer_view v, void** ptr) {
+    int32_t r = check_view(v, "buffer_device_ptr");
+    if (r) return r;
+    QXH_REQUIRE(ptr, QXH_ERR_INVALID_ARGUMENT, "buffer_device_ptr: null output");
+    *ptr = v.buffer->base + v.offset;
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_buffer_write(qxh_buffer_view v, const void* data, uint64_t bytes) {
+    int32_t r = check_view(v, "buffer_write");
+    if (r) return r;
+    QXH_REQUIRE(data || bytes == 0, QXH_ERR_INVALID_ARGUMENT, "buffer_write: null data");
+    QXH_REQUIRE(bytes <= v.length, QXH_ERR_INVALID_ARGUMENT, "initialization data (%llu bytes) exceeds runtime buffer (%llu)",
+                (unsigned long long)bytes, (unsigned long long)v.length);
+    if (!bytes) return QXH_OK;
+    hipError_t e = hipSetDevice(v.buffer->device);
+    if (e == hipSuccess) e = hipMemcpy(v.buffer->base + v.offset, data, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(e, "runtime buffer write");
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_buffer_read(qxh_buffer_view v, void* data, uint64_t bytes) {
+    int32_t r = check_view(v, "buffer_read");
+    if (r) return r;
+    QXH_REQUIRE(data || bytes == 0, QXH_ERR_INVALID_ARGUMENT, "buffer_read: null data");
+    QXH_REQUIRE(bytes <= v.length, QXH_ERR_INVALID_ARGUMENT, "read of %llu bytes exceeds runtime buffer (%llu)",
+                (unsigned long long)bytes, (unsigned long long)v.length);
+    if (!bytes) return QXH_OK;
+    hipError_t e = hipSetDevice(v.buffer->device);
+    if (e == hipSuccess) e = hipMemcpy(data, v.buffer->base + v.offset, bytes, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "runtime buffer read");
+    return QXH_OK;
+}
+
+// ---------------------------------------------------------------------------
 // KV cache
 // ---------------------------------------------------------------------------
 static int32_t check_desc(const qxh_kv_desc* d, ShapeDims* dims) {
@@ -1293,6 +1376,119 @@ extern "C" int32_t qxh_encode_qwen_attention_block(qxh_graph* g, qxh_kv_cache* c
     if (e != hipSuccess) return hip_fail(e, "qwen residual norm launch");
     g->dispatches += 4 + appends + dispatches;
     advance(c, layer, 0, 1, 1);
+    return QXH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// synchronous Qwen helpers (host arrays in and out)
+// ---------------------------------------------------------------------------
+namespace {
+// Device memory of one synchronous call, released on every path.
+struct DeviceScratch {
+    void* p = nullptr;
+    ~DeviceScratch() {
+        if (p) (void)hipFree(p);
+    }
+};
+struct GraphGuard {
+    qxh_graph* g = nullptr;
+    ~GraphGuard() {
+        if (g) (void)qxh_graph_discard(g);
+    }
+};
+struct CacheGuard {
+    qxh_kv_cache* c = nullptr;
+    ~CacheGuard() {
+        if (c) (void)qxh_kv_cache_destroy(c);
+    }
+};
+}  // namespace
+
+extern "C" int32_t qxh_run_qwen_qk_norm_rope(qxh_context* ctx, const uint16_t* query, size_t query_len,
+                                             const uint16_t* key, size_t key_len, const float* query_norm,
+                                             size_t query_norm_len, const float* key_norm, size_t key_norm_len,
+                                             int32_t dtype, uint32_t position, uint16_t* query_out,
+                                             uint16_t* key_out) {
+    QXH_REQUIRE(ctx, QXH_ERR_INVALID_ARGUMENT, "run_qwen_qk_norm_rope: null context");
+    QXH_REQUIRE(query && key && query_norm && key_norm && query_out && key_out, QXH_ERR_INVALID_ARGUMENT,
+                "run_qwen_qk_norm_rope: null argument");
+    QXH_REQUIRE(query_len == 32 * 128 && key_len == 4 * 128 && query_norm_len == 128 && key_norm_len == 128,
+                QXH_ERR_INVALID_ARGUMENT, "invalid Qwen Q/K shapes: q=%zu, k=%zu, q_norm=%zu, k_norm=%zu", query_len,
+                key_len, query_norm_len, key_norm_len);
+    QXH_REQUIRE(dtype == QXH_F16 || dtype == QXH_BF16, QXH_ERR_INVALID_ARGUMENT,
+                "run_qwen_qk_norm_rope: dtype %d is not a 16-bit format", dtype);
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    const size_t qb = query_len * 2, kb = key_len * 2, nb = 128 * sizeof(float);
+    DeviceScratch d;
+    if ((e = hipMalloc(&d.p, qb + kb + 2 * nb)) != hipSuccess) return hip_fail(e, "Qwen Q/K buffer allocation");
+    char* dq = (char*)d.p;
+    char* dk = dq + qb;
+    float* dqn = (float*)(dk + kb);
+    float* dkn = dqn + 128;
+    hipStream_t st = ctx->stream;
+    if ((e = hipMemcpyAsync(dq, query, qb, hipMemcpyHostToDevice, st)) == hipSuccess &&
+        (e = hipMemcpyAsync(dk, key, kb, hipMemcpyHostToDevice, st)) == hipSuccess &&
+        (e = hipMemcpyAsync(dqn, query_norm, nb, hipMemcpyHostToDevice, st)) == hipSuccess &&
+        (e = hipMemcpyAsync(dkn, key_norm, nb, hipMemcpyHostToDevice, st)) == hipSuccess) {
+        float inv[64];
+        qwen_inverse_frequencies(inv);
+        e = launch_qwen_qk_norm_rope(dq, dk, dqn, dkn, dtype, position, inv, st);
+    }
+    if (e == hipSuccess && (e = hipMemcpyAsync(query_out, dq, qb, hipMemcpyDeviceToHost, st)) == hipSuccess &&
+        (e = hipMemcpyAsync(key_out, dk, kb, hipMemcpyDeviceToHost, st)) == hipSuccess)
+        e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hip_fail(e, "Qwen Q/K norm + RoPE execution");
+    return QXH_OK;
+}
+
+extern "C" int32_t qxh_run_qwen_gqa_attention(qxh_context* ctx, const uint16_t* query, size_t query_len,
+                                              const uint16_t* key_cache, size_t key_len, const uint16_t* value_cache,
+                                              size_t value_len, int32_t dtype, uint16_t* output) {
+    QXH_REQUIRE(ctx, QXH_ERR_INVALID_ARGUMENT, "run_qwen_gqa_attention: null context");
+    QXH_REQUIRE(query && key_cache && value_cache && output, QXH_ERR_INVALID_ARGUMENT,
+                "run_qwen_gqa_attention: null argument");
+    QXH_REQUIRE(query_len == 32 * 128 && key_len > 0 && key_len == value_len && key_len % 512 == 0,
+                QXH_ERR_INVALID_ARGUMENT, "invalid Qwen GQA shapes: q=%zu, k_cache=%zu, v_cache=%zu", query_len,
+                key_len, value_len);
+    QXH_REQUIRE(key_len / 512 <= UINT32_MAX, QXH_ERR_INVALID_ARGUMENT, "Qwen GQA context exceeds u32");
+    QXH_REQUIRE(dtype == QXH_F16 || dtype == QXH_BF16, QXH_ERR_INVALID_ARGUMENT,
+                "run_qwen_gqa_attention: dtype %d is not a 16-bit format", dtype);
+    const uint32_t context = (uint32_t)(key_len / 512);
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    CacheGuard cache;
+    const qxh_kv_desc desc{QXH_SHAPE_QWEN3, dtype, dtype, 1, 1, context, 0};
+    int32_t r = qxh_kv_cache_create(ctx, &desc, nullptr, 0, &cache.c);
+    if (r) return r;
+    uint64_t ws = 0;
+    if ((r = qxh_attention_workspace_bytes(cache.c, 1, context, &ws))) return r;
+    const size_t qb = query_len * 2, cb = key_len * 2;
+    DeviceScratch d;
+    if ((e = hipMalloc(&d.p, 2 * qb + 2 * cb + ws)) != hipSuccess) return hip_fail(e, "Qwen GQA buffer allocation");
+    char* dq = (char*)d.p;
+    char* dout = dq + qb;
+    char* dk = dout + qb;
+    char* dv = dk + cb;
+    char* dws = dv + cb;
+    hipStream_t st = ctx->stream;
+    if ((e = hipMemcpyAsync(dq, query, qb, hipMemcpyHostToDevice, st)) != hipSuccess ||
+        (e = hipMemcpyAsync(dk, key_cache, cb, hipMemcpyHostToDevice, st)) != hipSuccess ||
+        (e = hipMemcpyAsync(dv, value_cache, cb, hipMemcpyHostToDevice, st)) != hipSuccess)
+        return hip_fail(e, "Qwen GQA upload");
+    GraphGuard g;
+    if ((r = qxh_graph_begin(ctx, st, &g.g))) return r;
+    // the position-major rows go into the head-major arena, then decode attention
+    if ((r = qxh_encode_store_kv(g.g, cache.c, 0, 0, 1, 0, context, dk, dv, dtype))) return r;
+    if ((r = qxh_encode_attention_for_layer(g.g, cache.c, 0, 0, 1, context, dq, dtype, dout, dtype, ws ? dws : nullptr,
+                                            ws)))
+        return r;
+    qxh_graph* done = g.g;
+    g.g = nullptr;
+    if ((r = qxh_graph_finish(done, nullptr))) return r;
+    if ((e = hipMemcpyAsync(output, dout, qb, hipMemcpyDeviceToHost, st)) != hipSuccess ||
+        (e = hipStreamSynchronize(st)) != hipSuccess)
+        return hip_fail(e, "Qwen GQA readback");
     return QXH_OK;
 }
 

@@ -15,7 +15,7 @@ import torch
 from oracle import oracle as O
 from qx_amd import abi, api
 from qx_amd import runtime as rt
-from tests.helpers import TOL_16, TOL_F32, log, rel_err
+from tests.helpers import FP32_ORACLE_BAR_MAX_LENGTH, TOL_16, TOL_F32, attend64, check_fp32_bar, log, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -29,17 +29,6 @@ def ctx():
 
 def dev(a, dtype=torch.float32):
     return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0").to(dtype)
-
-
-def attend64(q, keys, values, scale):
-    """float64 GQA attention: q [Hq][D], keys/values [L][Hkv][D]."""
-    out = np.zeros(q.shape)
-    g = q.shape[0] // keys.shape[1]
-    for h in range(q.shape[0]):
-        sc = keys[:, h // g, :].astype(np.float64) @ q[h].astype(np.float64) * scale
-        w = np.exp(sc - sc.max())
-        out[h] = (w / w.sum()) @ values[:, h // g, :].astype(np.float64)
-    return out
 
 
 def test_grouped_query_attention_uses_matching_kv_head():
@@ -117,14 +106,63 @@ def test_granite_decode_lengths_and_dtypes(ctx, kdt, length):
         exact = attend64(qs, kf, vf, 0.015625).ravel()
         e_gpu, e_ora = rel_err(got, exact), rel_err(r, exact)
         log(f"seq {s}: gpu-oracle {e:.3e}  gpu-f64 {e_gpu:.3e}  oracle-f64 {e_ora:.3e}")
-        if kdt == abi.F32 and e_ora > 0.5 * tol:
-            # At long contexts the oracle's own sequential binary32 rounding
-            # (measured here against float64) is already ~1e-5 x RMS, so the
-            # oracle is the noise floor: require the GPU to be at least as close
-            # to the exact result as the oracle is, and within 1.5x the bar.
-            assert e_gpu <= e_ora and e <= 1.5 * tol, (s, e, e_gpu, e_ora)
+        if kdt == abi.F32:
+            check_fp32_bar(got, r, exact, length)
         else:
             assert e <= tol, (s, e)
+
+
+def fp32_cases(ctx, S, L, seed):
+    """GPU decode of S fp32 sequences at length L; per sequence (gpu, oracle, exact)."""
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, S, L, abi.F32)
+    q = torch.empty((S, 16, 64), device="cuda:0")
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=seed, length=L)
+        rt.fill_normal(g, q, seed=seed + 1)
+    with rt.Graph(ctx) as g:
+        out = rt.attention(g, arena, 0, q, L)
+    for s in range(S):
+        with rt.Graph(ctx) as g:
+            kk, vv = arena.gather(g, 0, s, 0, L)
+        kf, vf = kk.cpu().numpy(), vv.cpu().numpy()
+        ref_cache = O.KvCache(L)
+        ref_cache.extend(kf, vf)
+        qs = q[s].cpu().numpy()
+        yield (out[s].cpu().numpy().ravel(), O.granite_attend(qs.ravel(), ref_cache, L),
+               attend64(qs, kf, vf, 0.015625).ravel())
+
+
+@pytest.mark.parametrize("S,L", [(1, 1), (256, 1), (1, 1000), (256, 1000)])
+def test_fp32_decode_strict_bar_single_and_batched(ctx, S, L):
+    """The north-star fp32 bar, unconditionally: every sequence of a single
+    and a 256-sequence batch within 1e-5 x RMS of the oracle (split-K with a
+    combine for one sequence, one split per unit for the batch)."""
+    log("fp32 strict bar", S, L)
+    assert L <= FP32_ORACLE_BAR_MAX_LENGTH
+    worst = 0.0
+    for got, r, exact in fp32_cases(ctx, S, L, seed=17 * L + S):
+        e = rel_err(got, r)
+        worst = max(worst, e)
+        assert e <= TOL_F32, e
+        assert rel_err(got, exact) <= TOL_F32 / 2
+        if L == 1:
+            assert np.array_equal(got, r)  # one position: out = v exactly
+    log(f"  worst gpu-oracle {worst:.2e}")
+
+
+@pytest.mark.parametrize("S", [1, 256])
+def test_fp32_decode_at_4096_against_exact_attention(ctx, S):
+    """At 4096 positions the reference's own sequential binary32 sums are up
+    to 1.6e-5 x RMS from exact attention (pinned on the CPU by
+    tests/test_oracle_attention.py), so there the bar is applied to exact
+    (float64) attention at half its width, for every sequence; the distance
+    to the oracle is logged."""
+    log("fp32 at 4096", S)
+    eg, eo, ef = [], [], []
+    for got, r, exact in fp32_cases(ctx, S, 4096, seed=4096 + S):
+        e, e_gpu, e_ora = check_fp32_bar(got, r, exact, 4096)
+        eo.append(e), eg.append(e_gpu), ef.append(e_ora)
+    log(f"  gpu-f64 max {max(eg):.2e}; gpu-oracle max {max(eo):.2e}; oracle-f64 max {max(ef):.2e}")
 
 
 def test_cfg4_batched_fp16_decode_full_size(ctx):
