@@ -50,12 +50,35 @@ def timed(fn, steps, warmup, stream):
     return start.elapsed_time(end) / steps  # ms per step
 
 
+def source_digest(paths):
+    """sha256 over the named repository files (the sources a kernel is built from)."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in sorted(paths):
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(rel.encode() + b"\0" + f.read())
+    return h.hexdigest()
+
+
 def load_traffic(kernel_key):
+    """HBM bytes per launch of a kernel from profiles/traffic.json (rocprofv3
+    FETCH_SIZE + WRITE_SIZE, scaled by a copy of known size).  Reported only
+    when the sources the measurement was taken on are the sources of this
+    tree, so the figure is evidence for the kernel that ran; else None."""
     try:
         with open(TRAFFIC_FILE) as f:
-            return json.load(f).get(kernel_key)
+            entry = json.load(f).get(kernel_key)
     except (OSError, ValueError):
         return None
+    if not isinstance(entry, dict) or "sources" not in entry:
+        return None
+    try:
+        if source_digest(entry["sources"]) != entry["source_sha256"]:
+            log(f"traffic {kernel_key}: kernel sources changed since the measurement; not reported")
+            return None
+    except OSError:
+        return None
+    return entry["traffic_bytes"]
 
 
 def roofline_hbm(bytes_per_launch, ms_per_launch, traffic=None):
@@ -502,66 +525,261 @@ def bench_prefill(ctx, steps, warmup, shape_name):
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the oracle's single-threaded Granite attention on a sample
+# CPU baselines: the oracle (a contraction-free C restatement of the
+# reference's CPU path, built -O2) timed on this host's cores, for every
+# configuration.  The reference attention is single-threaded, so each config
+# gets a 1-thread figure; the all-core figure runs independent units (whole
+# sequences, layers or query rows, each thread with its own cache) on the
+# GPU box's CPU share.  Samples are bounded (a few seconds each) and scaled
+# to the config's unit as stated in each entry.
 # ---------------------------------------------------------------------------
-def cpu_baseline(seconds=10.0):
-    import concurrent.futures as cf
+def cpu_threads():
+    """Threads for the all-core figures: the CPU share of one GPU on the
+    box (16 threads, the OMP_NUM_THREADS the box sets), never more than the
+    cores this process may run on."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    share = int(os.environ.get("OMP_NUM_THREADS") or 16)
+    return max(1, min(affinity, share, 16)), affinity, os.cpu_count() or 1
 
-    import numpy as np
 
-    from oracle import oracle as O
+def _timed_loop(fn, seconds, min_iters=1):
+    n = 0
+    t0 = time.perf_counter()
+    while n < min_iters or time.perf_counter() - t0 < seconds:
+        fn()
+        n += 1
+    return (time.perf_counter() - t0) / n, n
 
+
+def _threaded(fns, reps):
+    """Run fns[i]() `reps` times on thread i, all started together (ctypes
+    releases the GIL inside the oracle); returns the wall time."""
+    import threading
+    gate = threading.Barrier(len(fns) + 1)
+
+    def work(fn):
+        gate.wait()
+        for _ in range(reps):
+            fn()
+
+    ts = [threading.Thread(target=work, args=(f,)) for f in fns]
+    for t in ts:
+        t.start()
+    gate.wait()
+    t0 = time.perf_counter()
+    for t in ts:
+        t.join()
+    return time.perf_counter() - t0
+
+
+def _entry(value, unit, sample, all_value, threads, all_sample, **extra):
+    e = {"value": round(value, 3), "unit": unit, "cores": 1, "kind": "port", "sample": sample,
+         "all_core": {"value": round(all_value, 3), "cores": threads, "sample": all_sample}}
+    e.update(extra)
+    return e
+
+
+def cpu_cfg1(O, np, threads, secs):
+    """Config 1: granite_attention_decode for positions 0..511 of one layer."""
+    P = 512
+    g = np.random.default_rng(1)
+    q = g.standard_normal((P, 1024), dtype=np.float32)
+    k = g.standard_normal((P, 512), dtype=np.float32)
+    v = g.standard_normal((P, 512), dtype=np.float32)
+
+    def seq(cache):
+        cache.reset()
+        for p in range(P):
+            O.granite_attention_decode(q[p], k[p], v[p], p, cache)
+
+    c0 = O.KvCache(P)
+    t1, n = _timed_loop(lambda: seq(c0), secs)
+    caches = [O.KvCache(P) for _ in range(threads)]
+    reps = max(1, n // 2)
+    wall = _threaded([lambda c=c: seq(c) for c in caches], reps)
+    return _entry(t1 * 1e6 / P, "us/token", f"{n} runs of the 512-step sequence (RoPE + append + attention per token)",
+                  wall * 1e6 / (P * reps * threads), threads,
+                  f"{threads} independent 512-step sequences x {reps} run(s) on {threads} threads; per-token time of "
+                  f"the aggregate")
+
+
+def cpu_cfg2(O, np, threads, secs):
+    """Config 2: the attention half of a Granite layer at position 4095 over a
+    4095-row fp32 cache; a token is 24 such layers."""
+    g = np.random.default_rng(2)
+    weights = []
+    for _ in range(2):
+        weights.append((np.ones(1024, np.float32),
+                        (g.standard_normal((1024, 1024), dtype=np.float32) * 0.02),
+                        (g.standard_normal((512, 1024), dtype=np.float32) * 0.02),
+                        (g.standard_normal((512, 1024), dtype=np.float32) * 0.02),
+                        (g.standard_normal((1024, 1024), dtype=np.float32) * 0.02)))
+    keys = g.standard_normal((4095, 8, 64), dtype=np.float32)
+    vals = g.standard_normal((4095, 8, 64), dtype=np.float32)
+    hidden = g.standard_normal(1024, dtype=np.float32)
+
+    def make_cache():
+        c = O.KvCache(4096)
+        c.extend(keys, vals)
+        return c
+
+    it = [0]
+
+    def layer(cache, w):
+        O.granite_attention_block(hidden, *w, 4095, cache)
+        cache.rollback(4095)
+
+    c0 = make_cache()
+
+    def step():
+        layer(c0, weights[it[0] & 1])
+        it[0] += 1
+
+    t1, n = _timed_loop(step, secs)
+    caches = [make_cache() for _ in range(threads)]
+    reps = max(1, n // 2)
+    wall = _threaded([lambda c=c, i=i: layer(c, weights[i & 1]) for i, c in enumerate(caches)], reps)
+    return _entry(t1 * 24 * 1e6, "us/token (24 layers)",
+                  f"{n} single-thread layers (norm + fp32 q/k/v + RoPE + append + attention over 4096 positions + "
+                  f"o + residual, two alternating weight sets), x24 layers",
+                  wall * 24 * 1e6 / (reps * threads), threads,
+                  f"{threads} threads x {reps} layers (own cache each), x24 layers")
+
+
+def _prefill_scale(rows, T):
+    """Work of all T causal rows over the work of the sampled rows (row t
+    attends t + 1 positions)."""
+    return (T * (T + 1) / 2) / float(sum(int(r) + 1 for r in rows))
+
+
+def cpu_cfg3(O, np, threads, secs):
+    """Config 3: causal prefill of 2048 Granite tokens over fp16-rounded K/V
+    (the reference runs a prompt as repeated decode)."""
+    T = 2048
+    g = np.random.default_rng(3)
+    keys = g.standard_normal((T, 8, 64), dtype=np.float32).astype(np.float16).astype(np.float32)
+    vals = g.standard_normal((T, 8, 64), dtype=np.float32).astype(np.float16).astype(np.float32)
+    q = g.standard_normal((T, 1024), dtype=np.float32).astype(np.float16).astype(np.float32)
+
+    def make_cache():
+        c = O.KvCache(T)
+        c.extend(keys, vals)
+        return c
+
+    rows1 = np.linspace(0, T - 1, 64).astype(np.uint32)
+    c0 = make_cache()
+    t1, n = _timed_loop(lambda: O.granite_prefill_rows(q, c0, 0, rows1), secs)
+    rows_all = np.linspace(0, T - 1, 32 * threads).astype(np.uint32)
+    caches = [make_cache() for _ in range(threads)]
+    wall = _threaded([lambda c=c, i=i: O.granite_prefill_rows(q, c, 0, rows_all[i::threads])
+                      for i, c in enumerate(caches)], 1)
+    return _entry(t1 * _prefill_scale(rows1, T) * 1e6, "us/prefill",
+                  f"64 evenly spaced query rows of 2048 ({n} runs), scaled by the causal work of all rows "
+                  f"(x{_prefill_scale(rows1, T):.1f})",
+                  wall * _prefill_scale(rows_all, T) * 1e6, threads,
+                  f"{rows_all.size} evenly spaced rows over {threads} threads (own cache each), scaled by the causal "
+                  f"work of all rows (x{_prefill_scale(rows_all, T):.2f})")
+
+
+def cpu_cfg4(O, np, threads, secs):
+    """Config 4: one sequence-layer of decode at ctx 4096 over fp16-rounded K/V;
+    the unit is a sequence-token over 24 layers."""
     L = 4096
-    rng = np.random.default_rng(0)
-    keys = rng.standard_normal((L, 8, 64), dtype=np.float32).astype(np.float16).astype(np.float32)
-    vals = rng.standard_normal((L, 8, 64), dtype=np.float32).astype(np.float16).astype(np.float32)
-    q = rng.standard_normal(1024, dtype=np.float32)
+    g = np.random.default_rng(0)
+    keys = g.standard_normal((L, 8, 64), dtype=np.float32).astype(np.float16).astype(np.float32)
+    vals = g.standard_normal((L, 8, 64), dtype=np.float32).astype(np.float16).astype(np.float32)
+    q = g.standard_normal(1024, dtype=np.float32)
 
     def make_cache():
         c = O.KvCache(L)
         c.extend(keys, vals)
         return c
 
-    cache = make_cache()
-    n = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds or n < 3:
-        O.granite_attend(q, cache, L)
-        n += 1
-    t1 = (time.perf_counter() - t0) / n
-    cores = os.cpu_count() or 1
-    cores = min(cores, 16)
-    caches = [make_cache() for _ in range(cores)]
-    per_thread = max(2, n // cores)
+    c0 = make_cache()
+    t1, n = _timed_loop(lambda: O.granite_attend(q, c0, L), secs)
+    caches = [make_cache() for _ in range(threads)]
+    reps = max(2, n // 2)
+    wall = _threaded([lambda c=c: O.granite_attend(q, c, L) for c in caches], reps)
+    return _entry(t1 * 24 * 1e6, "us/sequence-token (24 layers)",
+                  f"{n} single-thread attends of one Granite layer at ctx 4096 (fp16-rounded KV, fp32 math), x24 "
+                  f"layers; a cfg4 step is 256 sequence-tokens",
+                  wall * 24 * 1e6 / (reps * threads), threads,
+                  f"{reps * threads} attends over {threads} threads (independent sequences, own cache each), x24")
 
-    def work(c):
-        for _ in range(per_thread):
-            O.granite_attend(q, c, L)
 
-    t0 = time.perf_counter()
-    with cf.ThreadPoolExecutor(cores) as ex:
-        list(ex.map(work, caches))
-    tall = (time.perf_counter() - t0) / (per_thread * cores)
-    # KV commitment leaves of fp16 token rows (1024-byte K and V rows), one thread
-    krow = keys[:256].astype(np.float16).tobytes()
-    vrow = vals[:256].astype(np.float16).tobytes()
-    nh = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < 2.0 or nh < 100:
-        O.kv_leaf_hash_v1(0, nh, krow[(nh % 256) * 1024:(nh % 256 + 1) * 1024],
-                          vrow[(nh % 256) * 1024:(nh % 256 + 1) * 1024])
-        nh += 1
-    th = (time.perf_counter() - t0) / nh
-    return {
-        "value": round(t1 * 24 * 1e6, 1), "unit": "us/sequence-token (24 layers)", "cores": 1, "kind": "port",
-        "sample": f"{n} single-thread oracle attends of one Granite layer at ctx 4096 (fp16-rounded KV, "
-                  f"upcast fp32 math), x24 layers; cfg4 step = 256 sequences",
-        "all_core": {"value": round(tall * 24 * 1e6, 1), "cores": cores,
-                     "sample": f"{per_thread * cores} attends over {cores} threads (independent sequences)"},
-        "kv_hash": {"value": round(1.0 / th, 1), "unit": "leaves/s", "cores": 1, "kind": "port",
-                    "sample": f"{nh} oracle kv_leaf_hash_v1 calls on 1024-byte fp16 K and V rows "
-                              f"(includes the Python call overhead)"},
-    }
+def cpu_cfg5a(O, np, threads, secs):
+    """Config 5a: cpu_gqa_attention of one Qwen token at ctx 32768 (bf16)."""
+    N = 32768
+    g = np.random.default_rng(5)
+    kc = O.to_bits16(g.standard_normal(N * 512, dtype=np.float32), O.BF16)
+    vc = O.to_bits16(g.standard_normal(N * 512, dtype=np.float32), O.BF16)
+    q = O.to_bits16(g.standard_normal(4096, dtype=np.float32), O.BF16)
+    t1, n = _timed_loop(lambda: O.qwen_gqa_attention(q, kc, vc, O.BF16), secs)
+    reps = max(1, n // 2)
+    wall = _threaded([lambda: O.qwen_gqa_attention(q, kc, vc, O.BF16)] * threads, reps)
+    return _entry(t1 * 1e6, "us/layer", f"{n} single-thread Qwen attentions over 32768 bf16 positions",
+                  wall * 1e6 / (reps * threads), threads,
+                  f"{threads} threads x {reps} attentions (independent layers; the threads share one read-only cache)")
+
+
+def cpu_cfg5b(O, np, threads, secs):
+    """Config 5b: causal prefill of 8192 Qwen tokens (bf16), rows as repeated
+    cpu_gqa_attention."""
+    T = 8192
+    g = np.random.default_rng(6)
+    kc = O.to_bits16(g.standard_normal(T * 512, dtype=np.float32), O.BF16)
+    vc = O.to_bits16(g.standard_normal(T * 512, dtype=np.float32), O.BF16)
+    q = O.to_bits16(g.standard_normal(T * 4096, dtype=np.float32), O.BF16)
+    rows1 = np.linspace(0, T - 1, 16).astype(np.uint32)
+    t1, n = _timed_loop(lambda: O.qwen_prefill_rows(q, kc, vc, 0, rows1, O.BF16), secs)
+    rows_all = np.linspace(0, T - 1, 8 * threads).astype(np.uint32)
+    wall = _threaded([lambda i=i: O.qwen_prefill_rows(q, kc, vc, 0, rows_all[i::threads], O.BF16)
+                      for i in range(threads)], 1)
+    return _entry(t1 * _prefill_scale(rows1, T) * 1e6, "us/prefill",
+                  f"16 evenly spaced query rows of 8192 ({n} runs), scaled by the causal work of all rows "
+                  f"(x{_prefill_scale(rows1, T):.1f})",
+                  wall * _prefill_scale(rows_all, T) * 1e6, threads,
+                  f"{rows_all.size} evenly spaced rows over {threads} threads, scaled by the causal work of all rows "
+                  f"(x{_prefill_scale(rows_all, T):.2f})")
+
+
+def cpu_kv_hash(O, np, threads, secs):
+    """kv_leaf_hash_v1 of fp16 Granite token rows (1 KiB K + 1 KiB V), a C loop."""
+    R = 2048
+    g = np.random.default_rng(7)
+    keys = g.integers(0, 256, (R, 1024), dtype=np.uint8)
+    vals = g.integers(0, 256, (R, 1024), dtype=np.uint8)
+    t1, n = _timed_loop(lambda: O.kv_leaf_hashes(0, 0, keys, vals), secs)
+    reps = max(1, n // 2)
+    wall = _threaded([lambda: O.kv_leaf_hashes(0, 0, keys, vals)] * threads, reps)
+    return _entry(R / t1, "leaves/s", f"{n} C loops over {R} leaves (qxo_kv_leaf_hashes)",
+                  R * reps * threads / wall, threads, f"{threads} threads x {reps} loops of {R} leaves")
+
+
+def cpu_baselines(names=None, secs=2.0):
+    import numpy as np
+
+    from oracle import oracle as O
+
+    threads, affinity, nproc = cpu_threads()
+    fns = {"cfg1": cpu_cfg1, "cfg2": cpu_cfg2, "cfg3": cpu_cfg3, "cfg4": cpu_cfg4, "cfg5a": cpu_cfg5a,
+           "cfg5b": cpu_cfg5b, "kvhash": cpu_kv_hash}
+    out = {}
+    for name, fn in fns.items():
+        if names and name not in names:
+            continue
+        try:
+            t0 = time.perf_counter()
+            out[name] = fn(O, np, threads, secs)
+            out[name]["host"] = {"nproc": nproc, "affinity": affinity}
+            log(f"cpu {name}", json.dumps(out[name]), f"({time.perf_counter() - t0:.1f} s)")
+        except Exception as e:  # report, keep the rest
+            out[name] = {"error": str(e)}
+            log(f"cpu {name} error", e)
+    return out
 
 
 def main():
@@ -623,9 +841,17 @@ def run(ctx, args):
             torch.cuda.empty_cache()
     if head and isinstance(detail.get("hbm_probe"), dict) and "read_gb_per_s" in detail["hbm_probe"]:
         head["frac_of_hbm_probe"] = round(head["roofline"]["achieved"] / detail["hbm_probe"]["read_gb_per_s"], 4)
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu = {} if args.no_cpu else cpu_baselines(set(only) | {"cfg4"} if only else None)
+    for name, entry in cpu.items():
+        if name in detail and isinstance(detail[name], dict) and "error" not in detail[name]:
+            detail[name]["cpu_baseline"] = entry
+    headline_cpu = None
+    if "cfg4" in cpu:
+        headline_cpu = dict(cpu["cfg4"])
+        if "kvhash" in cpu:
+            headline_cpu["kv_hash"] = cpu["kvhash"]
     if head is None:
-        print(json.dumps({"detail": detail, "cpu_baseline": cpu}))
+        print(json.dumps({"detail": detail, "cpu_baseline": headline_cpu}))
         return
     line = {
         "metric": "decode attn µs/token & HBM GB/s (% peak); prefill attn TFLOP/s (% MFMA peak)",
@@ -644,7 +870,7 @@ def run(ctx, args):
                    "q_heads": 16, "kv_heads": 8, "head_dim": 64, "kv_dtype": "f16",
                    "step": "one query token per sequence through 24 layers of independent caches"},
         "roofline": head["roofline"],
-        "cpu_baseline": cpu,
+        "cpu_baseline": headline_cpu,
         "detail": {"cfg4": {k: v for k, v in head.items() if k != "roofline"}, **detail},
     }
     print(json.dumps(line))

@@ -66,6 +66,7 @@ def lib():
         L.qxo_kv_cache_len.restype = ctypes.c_uint32
         L.qxo_kv_cache_reset.argtypes = [ctypes.c_void_p]
         L.qxo_kv_cache_reset.restype = None
+        L.qxo_kv_cache_rollback.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
         L.qxo_kv_cache_keys.argtypes = [ctypes.c_void_p]
         L.qxo_kv_cache_keys.restype = _f32p
         L.qxo_kv_cache_values.argtypes = [ctypes.c_void_p]
@@ -223,6 +224,11 @@ class KvCache:
 
     def __len__(self):
         return lib().qxo_kv_cache_len(self._h)
+
+    def rollback(self, length: int):
+        """Cursor-only rewind (rollback_kv, crates/qx-runtime-v2/src/lib.rs:3271-3285)."""
+        if lib().qxo_kv_cache_rollback(self._h, length):
+            raise OracleError(f"rollback to {length} beyond length {len(self)}")
 
     def reset(self):
         lib().qxo_kv_cache_reset(self._h)
@@ -543,6 +549,19 @@ def kv_leaf_hash_v1(layer: int, token: int, key: bytes, value: bytes) -> bytes:
     """kv_leaf_hash_v1, crates/qx-commit/src/state.rs:334-348."""
     return _digest_call(lib().qxo_kv_leaf_hash_v1, ctypes.c_uint16(layer), ctypes.c_uint32(token), _bytes_arg(key),
                         ctypes.c_size_t(len(key)), _bytes_arg(value), ctypes.c_size_t(len(value)))
+
+
+def kv_leaf_hashes(layer: int, token_begin: int, keys, values):
+    """kv_leaf_hash_v1 of every row of position-major keys / values
+    ([rows][row bytes] uint8): a C loop, one leaf after another."""
+    k = np.ascontiguousarray(keys, dtype=np.uint8)
+    v = np.ascontiguousarray(values, dtype=np.uint8)
+    rows = k.shape[0]
+    out = np.zeros((rows, 32), np.uint8)
+    _check(lib().qxo_kv_leaf_hashes(ctypes.c_uint16(layer), ctypes.c_uint32(token_begin), ctypes.c_uint32(rows),
+                                    _p(k, _u8p), ctypes.c_size_t(k.shape[1]), _p(v, _u8p),
+                                    ctypes.c_size_t(v.shape[1]), _p(out, _u8p)))
+    return out
 
 
 def verification_hashes(residuals: bytes, residual_stride: int, key_rows, value_rows, token: int, layers: int,

@@ -313,6 +313,13 @@ QXO_EXPORT void qxo_kv_cache_free(qxo_kv_cache* c) {
 }
 QXO_EXPORT uint32_t qxo_kv_cache_len(const qxo_kv_cache* c) { return c->length; }
 QXO_EXPORT void qxo_kv_cache_reset(qxo_kv_cache* c) { c->length = 0; }
+/* Cursor-only rewind to `length` <= len, as rollback_kv moves the cursor
+ * (crates/qx-runtime-v2/src/lib.rs:3271-3285); rows stay until overwritten. */
+QXO_EXPORT int qxo_kv_cache_rollback(qxo_kv_cache* c, uint32_t length) {
+    if (length > c->length) return 1;
+    c->length = length;
+    return 0;
+}
 QXO_EXPORT float* qxo_kv_cache_keys(qxo_kv_cache* c) { return c->keys; }
 QXO_EXPORT float* qxo_kv_cache_values(qxo_kv_cache* c) { return c->values; }
 

@@ -152,7 +152,8 @@ QXO_EXPORT int qxo_chunk_tree_hash(const uint8_t* bytes, size_t len, size_t chun
     size_t cap = 1;
     while (cap < leaves) cap <<= 1;
     if (cap > QXO_MAX_TREE_LEAVES) return -1;
-    static uint8_t nodes[QXO_MAX_TREE_LEAVES][32];
+    /* per thread: the CPU baseline hashes rows on several threads */
+    static _Thread_local uint8_t nodes[QXO_MAX_TREE_LEAVES][32];
     for (size_t i = 0; i < leaves; ++i) {
         const uint32_t idx = (uint32_t)i;
         const uint8_t ib[4] = {(uint8_t)idx, (uint8_t)(idx >> 8), (uint8_t)(idx >> 16), (uint8_t)(idx >> 24)};
@@ -195,6 +196,19 @@ QXO_EXPORT int qxo_kv_leaf_hash_v1(uint16_t layer, uint32_t token, const uint8_t
     if (qxo_chunk_tree_hash(key, key_len, 256, "QX:KV:KEY:CHUNK:V1", "QX:KV:KEY:TREE:V1", kr)) return -1;
     if (qxo_chunk_tree_hash(value, value_len, 256, "QX:KV:VALUE:CHUNK:V1", "QX:KV:VALUE:TREE:V1", vr)) return -1;
     return qxo_kv_leaf_hash_from_roots_v1(layer, token, kr, vr, out);
+}
+
+/* The leaves of `count` consecutive token rows, position-major K and V rows
+ * of key_len / value_len bytes: out + 32 i = kv_leaf_hash_v1(layer,
+ * token_begin + i, row i).  A plain loop over the function above (the CPU
+ * committer hashes one leaf at a time, crates/qx-commit/src/execution.rs:466-470). */
+QXO_EXPORT int qxo_kv_leaf_hashes(uint16_t layer, uint32_t token_begin, uint32_t count, const uint8_t* keys,
+                                  size_t key_len, const uint8_t* values, size_t value_len, uint8_t* out) {
+    for (uint32_t i = 0; i < count; ++i)
+        if (qxo_kv_leaf_hash_v1(layer, token_begin + i, keys + (size_t)i * key_len, key_len,
+                                values + (size_t)i * value_len, value_len, out + (size_t)i * 32))
+            return -1;
+    return 0;
 }
 
 /* ------------------------------------------------------------------------ */

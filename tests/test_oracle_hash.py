@@ -96,3 +96,22 @@ def test_verification_digest_layout():
         ckpt = (layer + 1) % interval == 0 or layer + 1 == layers
         assert d[:32] == (O.state_hash_v1(res[p * stride:(p + 1) * stride]) if ckpt else bytes(32))
         assert d[32:] == O.kv_leaf_hash_v1(layer, 77, krows[layer], vrows[layer])
+
+
+def test_batched_leaves_equal_single_leaves_and_are_thread_safe():
+    """qxo_kv_leaf_hashes (the CPU baseline's loop) equals kv_leaf_hash_v1 row
+    by row, also when four threads hash at once (the chunk tree's node
+    scratch is per thread)."""
+    import concurrent.futures as cf
+
+    import numpy as np
+
+    g = np.random.default_rng(12)
+    keys = g.integers(0, 256, (24, 1024), dtype=np.uint8)
+    values = g.integers(0, 256, (24, 2048), dtype=np.uint8)
+    got = O.kv_leaf_hashes(3, 100, keys, values)
+    for i in range(24):
+        assert bytes(got[i]) == O.kv_leaf_hash_v1(3, 100 + i, keys[i].tobytes(), values[i].tobytes())
+    with cf.ThreadPoolExecutor(4) as ex:
+        outs = list(ex.map(lambda _: O.kv_leaf_hashes(3, 100, keys, values), range(16)))
+    assert all(np.array_equal(o, got) for o in outs)
