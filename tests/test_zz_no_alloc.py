@@ -37,7 +37,7 @@ def run_both(ctx, arena, q, length):
 
 
 def test_no_alloc_matches_workspace_entry_on_two_calls(ctx):
-    # call 1: Qwen bf16, one sequence at 32768 positions (128 splits x 4 kv heads)
+    # call 1: Qwen bf16, one sequence at 32768 positions (64 splits x 4 kv heads)
     log("no-alloc call 1: qwen bf16 1 x 32768")
     big = rt.KvArena(ctx, abi.SHAPE_QWEN3, 1, 1, 32768, abi.BF16)
     qb = torch.empty((1, 32, 128), dtype=torch.bfloat16, device="cuda:0")
@@ -64,16 +64,17 @@ def test_no_alloc_matches_workspace_entry_on_two_calls(ctx):
 
 
 def test_no_alloc_refuses_partials_beyond_the_scratch(ctx):
-    # 511 Qwen sequences at 512 positions: 2044 units x 2 splits x 8 heads x
-    # 130 floats = 17.0 MB of partials, above the 16 MiB scratch
+    # 511 Qwen sequences at 1024 positions: 2044 units x 2 splits (of 512
+    # positions) x 8 heads x 130 floats = 17.0 MB of partials, above the
+    # 16 MiB scratch
     log("no-alloc: oversize request")
-    arena = rt.KvArena(ctx, abi.SHAPE_QWEN3, 1, 511, 512, abi.BF16)
-    arena.set_len(512)
-    assert rt.attention_workspace_bytes(arena, 511, 512) > SCRATCH_BYTES
+    arena = rt.KvArena(ctx, abi.SHAPE_QWEN3, 1, 511, 1024, abi.BF16)
+    arena.set_len(1024)
+    assert rt.attention_workspace_bytes(arena, 511, 1024) > SCRATCH_BYTES
     q = torch.zeros((511, 32, 128), dtype=torch.bfloat16, device="cuda:0")
     out = torch.empty_like(q)
     g = rt.Graph(ctx)
     with pytest.raises(abi.QxhError, match="device scratch") as ei:
-        rt.attention_no_alloc(g, arena, 0, q, 512, out=out)
+        rt.attention_no_alloc(g, arena, 0, q, 1024, out=out)
     assert ei.value.code == abi.QXH_ERR_INVALID_ARGUMENT
     assert g.finish().dispatches == 0  # refused before anything was enqueued
