@@ -1,418 +1,36 @@
-// Causal prefill attention on gfx950 MFMA (v_mfma_f32_16x16x32_{f16,bf16},
-// fp32 accumulate), FlashAttention-2 style with the transposed formulation:
-//
-//   S^T[pos][q] = K[pos][:] . Q^T[:][q]      A = K tile (LDS), B = Q^T (registers)
-//   O^T[d][q]  += V^T[d][pos] . P^T[pos][q]   A = V^T via ds_read_b64_tr_b16, B = P^T
-//
-// With S^T, each lane owns one query column (lane % 16) of every 16x16 block,
-// so the online-softmax state (running max, rescale factor) of a query is
-// lane-local for the O^T accumulators, and the exponentiated scores are
-// already laid out as the B operand of the P.V product: the 16x16 output
-// block gives lane l positions 4*(l/16)+j of query l%16, and two position
-// blocks together fill the 8 k-slots of a 16x16x32 operand.  The k-slot to
-// position map is the same for both operands, so the contraction is exact
-// whatever the hardware's internal k order is.
-//
-// Work decomposition: a workgroup of 8 waves shares one K/V head.  Each wave
-// owns 32 queries (two 16-column blocks) of one query head; the workgroup
-// covers HW heads of the GQA group x QW query blocks (Qwen: the 8 heads of a
-// group; Granite: 2 heads x 4 query blocks).  K/V tiles of 64 positions are
-// staged through double-buffered, padded LDS by all 512 threads, with the
-// global loads of tile t+2 in flight while tile t is consumed.  Tiles above the causal diagonal are never
-// loaded; the diagonal tile is masked per element.  Query blocks are issued
-// last-first so the longest rows start first.
-//
-// Precision of P.V: rounding the probabilities to bf16 would cost ~7e-3 of
-// output RMS, so P.V always runs in f16 (P to f16 costs ~8e-4).  bf16 value
-// tiles are converted to f16 while they are staged into LDS (exact inside the
-// f16 range).  A tile holding any value outside that range is voted at the
-// staging barrier; such a workgroup records a flag and leaves its rows to a
-// second, exact kernel (EXACT = true) that keeps V in bf16 and splits P into
-// bf16 hi + lo parts.  The exact kernel's other workgroups exit at once.
-#include <type_traits>
-
-#include "common.h"
-#include "internal.h"
-#include "mfma.h"
+// Causal prefill attention on gfx950 MFMA: the kernels over prefill_rows
+// (prefill_rows.h) and the routing of every prefill call.
+#include "prefill_rows.h"
 
 namespace qxh {
 
-struct PrefillArgs {
-    const void* query;   // [T][Hq][D]
-    const void* keys;    // head-major cache of this layer and sequence: [Hkv][cap][D]
-    const void* values;
-    void* out;           // [T][Hq][D]
-    uint64_t head_stride;  // elements between kv heads
-    uint32_t start;        // position of query row 0
-    uint32_t tokens;       // T
-    int q_heads;
-    int group;
-    int out_dtype;
-    float scale_log2;      // softmax scale * log2(e)
-    uint32_t* flags;       // per-workgroup "V outside the f16 range" votes (bf16 caches)
-    uint32_t qblocks;      // query blocks per head
-    uint32_t kv_heads;
-    uint32_t xcd_map;      // 1: XCD-aware block -> (head, query block) mapping
-    // exact pass after the pipelined kernel: per-(kv head, 64-position tile)
-    // flags of the V^T pre-pass replace the per-workgroup votes
-    const uint32_t* tile_flags;
-    uint32_t tile_flag_stride;  // tiles per kv head
-};
-
-// Scheduling hint: interleave one MFMA with `valu` VALU instructions, n times.
-template <int N, int VALU>
-__device__ __forceinline__ void interleave_mfma_valu() {
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, VALU, 0);
-    }
-}
-
-// A running max may lag the true max by up to this many binary orders of
-// magnitude before the accumulators are rescaled; probabilities then stay
-// below 2^8, well inside the f16 range.
-constexpr float kLazyRescale = 8.0f;
-
-// Convert 8 packed bf16 to 8 packed f16 (RNE; exact for |v| in the f16 normal
-// range).  Sets `ovf` when a value is not representable as a finite f16.
-__device__ __forceinline__ u32x4 bf16x8_to_f16x8(const u32x4& v, bool& ovf) {
-    u32x4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float lo = __uint_as_float(v[i] << 16);
-        const float hi = __uint_as_float(v[i] & 0xffff0000u);
-        ovf |= !(__builtin_fabsf(lo) <= 65504.0f) || !(__builtin_fabsf(hi) <= 65504.0f);
-        const _Float16 a = (_Float16)lo, b = (_Float16)hi;
-        r[i] = (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-    }
-    return r;
-}
-
 template <int D, int DT, int HW, int QW, bool EXACT>
 __global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a) {
-    using M = MfmaT<DT>;             // Q.K operands (the cache dtype)
-    using MH = MfmaT<F16>;           // P.V operands: f16 probabilities and f16 values
-    using vec = typename M::vec;
-    using hvec = typename MH::vec;
-    // probability operand: f16 on the fast pass, the cache dtype on the exact pass
-    using pvec = typename std::conditional<EXACT, vec, hvec>::type;
-    constexpr int WAVES = 8;
-    constexpr int KSTEPS = D / 32;      // 32-dim k-steps of Q.K
-    constexpr int DTILES = D / 16;      // 16-dim output tiles
-    constexpr int BN = 64;              // positions per tile
-    constexpr int KROWB = D * 2 + 16;   // padded K row: 16 lanes reading 16 rows hit distinct banks
-    constexpr int VROWB = D * 2 + 32;   // padded V row: the 4 rows of a transposed read hit distinct banks
-    constexpr int KTILEB = BN * KROWB;
-    constexpr int VTILEB = BN * VROWB;
-    constexpr int CHUNKS = BN * D * 2 / 16;            // 16-byte chunks per K (or V) tile
-    constexpr int CPT = (2 * CHUNKS) / (64 * WAVES);   // chunks per thread (K and V)
-    static_assert(HW * QW == WAVES, "one wave per (head, 32-query block)");
-    static_assert(CPT >= 1 && CPT * 64 * WAVES == 2 * CHUNKS, "tile staging must divide evenly");
+    __shared__ __attribute__((aligned(16))) char lds[prefill_rows_lds_bytes<D>()];
+    prefill_rows<D, DT, HW, QW, EXACT>(a, lds, blockIdx.x, blockIdx.z, blockIdx.x + gridDim.x * blockIdx.z);
+}
 
-    __shared__ __attribute__((aligned(16))) char lds_k[2][KTILEB];
-    __shared__ __attribute__((aligned(16))) char lds_v[2][VTILEB];  // f16 (fast) or the cache dtype (exact)
-
-    const uint32_t wg_id = blockIdx.x + gridDim.x * blockIdx.z;
-    if constexpr (EXACT) {
-        // only workgroups whose fast pass met a V value outside the f16 range
-        if (!a.tile_flags && a.flags[wg_id] == 0) return;
-    }
-
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    const int lg = lane >> 4, li = lane & 15;
-    // XCD-aware block mapping: workgroups are dispatched round-robin over the
-    // 8 XCDs (each with its own L2), so block b runs on XCD b % 8.  Give each
-    // XCD the query blocks of one K/V head (or of a fixed share of heads) so
-    // that head's K/V stays resident in that XCD's L2.  Within an XCD, query
-    // blocks go longest-first.
-    const uint32_t nqb = a.qblocks;
-    uint32_t kvh_u, qidx;
-    {
-        const uint32_t lin = blockIdx.x;
-        if (a.xcd_map) {
-            const uint32_t xcd = lin & 7, slot = lin >> 3;
-            const uint32_t per = 8 / a.kv_heads;        // XCDs serving one head
-            kvh_u = xcd / per;
-            qidx = slot * per + (xcd % per);
-        } else {
-            kvh_u = lin / nqb;
-            qidx = lin % nqb;
-        }
-    }
-    const int kvh = (int)kvh_u;
-    const int head = kvh * a.group + blockIdx.z * HW + (wave % HW);
-    const int qsub = wave / HW;
-    const uint32_t qblock = nqb - 1 - qidx;  // longest rows first
-    const uint32_t T = a.tokens;
-    const uint32_t wg_q0 = qblock * (32 * QW);
-    const uint32_t wg_qlast = min(T, wg_q0 + 32 * QW) - 1;
-    const uint32_t kv_len = a.start + wg_qlast + 1;
-    const uint32_t ntiles = (kv_len + BN - 1) / BN;
-    const uint32_t q0 = wg_q0 + qsub * 32;               // first query row of this wave
-    const bool wave_live = q0 < T;
-    const uint32_t wave_kv = wave_live ? a.start + min(T - 1, q0 + 31) + 1 : 0;
-    const uint32_t wave_tiles = (wave_kv + BN - 1) / BN;
-    const float c = a.scale_log2;
-
-    if constexpr (EXACT) {
-        if (a.tile_flags) {
-            // rows of this workgroup reach tiles [0, ntiles); the pipelined
-            // kernel left them here iff one of those tiles is flagged
-            const uint32_t* f = a.tile_flags + (size_t)kvh * a.tile_flag_stride;
-            bool bad = false;
-            for (uint32_t i = lane; i < ntiles; i += 64) bad |= f[i] != 0;
-            if (!__syncthreads_or(bad)) return;
-        }
-    }
-
-    const char* kbase = reinterpret_cast<const char*>(a.keys) + (size_t)kvh * a.head_stride * 2;
-    const char* vbase = reinterpret_cast<const char*>(a.values) + (size_t)kvh * a.head_stride * 2;
-
-    // Q^T operands: lane supplies query (q0 + 16*nt + li), dims 32*ks + 8*lg .. +8
-    vec qop[2][KSTEPS];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        const uint32_t qr = min(q0 + 16 * nt + li, T - 1);
-        const char* qp = reinterpret_cast<const char*>(a.query) + (((size_t)qr * a.q_heads + head) * D) * 2;
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks)
-            qop[nt][ks] = __builtin_bit_cast(vec, *reinterpret_cast<const u32x4*>(qp + (32 * ks + 8 * lg) * 2));
-    }
-
-    f32x4 oacc[DTILES][2];
-#pragma unroll
-    for (int dt = 0; dt < DTILES; ++dt)
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float mrun[2] = {-1.0e30f, -1.0e30f};  // running max of raw q.k (unscaled)
-    float lrun[2] = {0.f, 0.f};
-
-    // staging: each thread moves CPT 16-byte chunks of the K and V tiles
-    auto load_tile = [&](uint32_t t, u32x4 (&st)[CPT]) {
-#pragma unroll
-        for (int cc = 0; cc < CPT; ++cc) {
-            const int idx = tid + cc * 64 * WAVES;    // [0, 2*CHUNKS)
-            const int which = idx / CHUNKS;           // 0 = K, 1 = V
-            const int rem = idx % CHUNKS;
-            const int row = rem / (D / 8), col = rem % (D / 8);
-            const uint32_t pos = t * BN + row;
-            if (pos < kv_len) {
-                const char* src = (which ? vbase : kbase) + ((size_t)pos * D + col * 8) * 2;
-                st[cc] = *reinterpret_cast<const u32x4*>(src);
-            } else {
-                st[cc] = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-    };
-    // returns true when some V value of this thread's chunks is not a finite f16
-    auto store_tile = [&](int buf, const u32x4 (&st)[CPT]) -> bool {
-        bool ovf = false;
-#pragma unroll
-        for (int cc = 0; cc < CPT; ++cc) {
-            const int idx = tid + cc * 64 * WAVES;
-            const int which = idx / CHUNKS;
-            const int rem = idx % CHUNKS;
-            const int row = rem / (D / 8), col = rem % (D / 8);
-            if (which == 0) {
-                *reinterpret_cast<u32x4*>(&lds_k[buf][row * KROWB + col * 16]) = st[cc];
-            } else {
-                u32x4 h = st[cc];
-                if constexpr (DT == BF16 && !EXACT) h = bf16x8_to_f16x8(st[cc], ovf);
-                *reinterpret_cast<u32x4*>(&lds_v[buf][row * VROWB + col * 16]) = h;
-            }
-        }
-        return ovf;
-    };
-
-    const uint32_t qpos_base = a.start + q0;  // position of this wave's first query row
-
-    // One 64-position tile = two 32-position sub-tiles.  Per sub-tile: S^T by
-    // 16 MFMAs, online softmax, P.V by 16 MFMAs.  Both sub-tiles' Q.K products
-    // are issued first, so the softmax of sub-tile 0 runs on the VALU while
-    // the MFMA pipe still works on sub-tile 1, and the softmax of sub-tile 1
-    // overlaps the P.V of sub-tile 0.
-    auto qk = [&](const char* kl, int sub, f32x4 (&S)[2][2]) {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) S[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) {
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-                const vec kop = __builtin_bit_cast(
-                    vec, *reinterpret_cast<const u32x4*>(kl + (sub * 32 + mt * 16 + li) * KROWB + (32 * ks + 8 * lg) * 2));
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) S[mt][nt] = M::mma(kop, qop[nt][ks], S[mt][nt]);
-            }
-        }
-    };
-    // Online softmax of one 32-position sub-tile.  The running max is lazy: it
-    // moves (and the accumulators are rescaled) only when some query's tile
-    // max exceeds it by more than 2^kLazyRescale.  Probabilities are produced
-    // packed for the P.V operand; their sum comes from v_dot2 on the packed
-    // values, so l and the P.V product see the same rounded probabilities.
-    auto softmax = [&](uint32_t spos, f32x4 (&S)[2][2], pvec (&P)[2], vec (&Plo)[2]) {
-        if (spos + 31 > qpos_base) {
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const uint32_t qpos = qpos_base + 16 * nt + li;
-#pragma unroll
-                for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        if (spos + mt * 16 + 4 * lg + j > qpos) S[mt][nt][j] = -INFINITY;
-            }
-        }
-        float tmax[2];
-        bool need = false;
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            float m = fmaxf(fmaxf(fmaxf(S[0][nt][0], S[0][nt][1]), fmaxf(S[0][nt][2], S[0][nt][3])),
-                            fmaxf(fmaxf(S[1][nt][0], S[1][nt][1]), fmaxf(S[1][nt][2], S[1][nt][3])));
-            m = max_xor16(m);
-            tmax[nt] = max_xor32(m);
-            need |= (tmax[nt] - mrun[nt]) * c > kLazyRescale;
-        }
-        if (__any(need)) {
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const float mnew = fmaxf(mrun[nt], tmax[nt]);
-                const float alpha = fast_exp2((mrun[nt] - mnew) * c);
-                mrun[nt] = mnew;
-                lrun[nt] *= alpha;
-#pragma unroll
-                for (int dt = 0; dt < DTILES; ++dt) oacc[dt][nt] *= alpha;
-            }
-        }
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            const float moff = -mrun[nt] * c;
-            float p[8];
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) p[mt * 4 + j] = fast_exp2(__builtin_fmaf(S[mt][nt][j], c, moff));
-            if constexpr (!EXACT) {
-                typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-                float l = lrun[nt];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const h2 pr = {(_Float16)p[2 * k], (_Float16)p[2 * k + 1]};
-                    P[nt][2 * k] = pr[0];
-                    P[nt][2 * k + 1] = pr[1];
-                    l = __builtin_amdgcn_fdot2(pr, h2{(_Float16)1.0f, (_Float16)1.0f}, l, false);
-                }
-                lrun[nt] = l;
-            } else {
-                // exact pass: cache-dtype hi + lo parts reproduce p to ~2^-16
-                float l = lrun[nt];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const auto h = M::cvt(p[k]);
-                    P[nt][k] = h;
-                    Plo[nt][k] = M::cvt(p[k] - (float)h);
-                    l += p[k];
-                }
-                lrun[nt] = l;
-            }
-        }
-    };
-    // lane (lg, li) addresses row base + li/4, dims 16*dt + 4*(li%4); after the
-    // transpose it holds V[base + j][16*dt + li] for j = 0..3
-    auto vt_operand = [&](const char* vl, int sub, int dt) {
-        const int coloff = (16 * dt + 4 * (li & 3)) * 2;
-        const int rbase = 32 * sub + 4 * lg + (li >> 2);
-        const lds_i16x4* p0 = (const lds_i16x4*)(vl + rbase * VROWB + coloff);
-        const lds_i16x4* p1 = (const lds_i16x4*)(vl + (rbase + 16) * VROWB + coloff);
-        const i16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p0));
-        const i16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p1));
-        return __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
-    };
-    auto pv = [&](const char* vl, int sub, const pvec (&P)[2], const vec (&Plo)[2]) {
-        if constexpr (!EXACT) {
-#pragma unroll
-            for (int dt = 0; dt < DTILES; ++dt) {
-                const hvec vop = __builtin_bit_cast(hvec, vt_operand(vl, sub, dt));
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = MH::mma(vop, P[nt], oacc[dt][nt]);
-            }
-        } else {
-#pragma unroll
-            for (int dt = 0; dt < DTILES; ++dt) {
-                const vec vop = __builtin_bit_cast(vec, vt_operand(vl, sub, dt));
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
-                    oacc[dt][nt] = M::mma(vop, P[nt], oacc[dt][nt]);
-                    oacc[dt][nt] = M::mma(vop, Plo[nt], oacc[dt][nt]);
-                }
-            }
-        }
-    };
-    auto compute = [&](uint32_t t, int buf) {
-        const char* kl = lds_k[buf];
-        const char* vl = lds_v[buf];
-        const uint32_t tpos = t * BN;
-        f32x4 s0[2][2], s1[2][2];
-        pvec P0[2], P1[2];
-        vec L0[2], L1[2];
-        qk(kl, 0, s0);
-        qk(kl, 1, s1);
-        softmax(tpos, s0, P0, L0);
-        interleave_mfma_valu<8 * KSTEPS / 2, 6>();
-        pv(vl, 0, P0, L0);
-        softmax(tpos + 32, s1, P1, L1);
-        interleave_mfma_valu<DTILES * 2, 6>();
-        pv(vl, 1, P1, L1);
-    };
-
-    // Two register stages: the loads of tile t+2 are in flight while tile t is
-    // consumed and tile t+1 (loaded one iteration earlier) is written to LDS.
-    // The barrier after each LDS write also votes whether that tile holds V
-    // values outside the f16 range.
-    u32x4 st0[CPT], st1[CPT];
-    load_tile(0, st0);
-    bool any_ovf = __syncthreads_or(store_tile(0, st0));
-    if (ntiles > 1) load_tile(1, st1);
-    for (uint32_t t = 0; t < ntiles; t += 2) {
-        // even tile t in buffer 0; st1 holds tile t+1
-        if (t + 2 < ntiles) load_tile(t + 2, st0);
-        if (t < wave_tiles) compute(t, 0);
-        bool f = false;
-        if (t + 1 < ntiles) f = store_tile(1, st1);
-        any_ovf |= __syncthreads_or(f);
-        if (t + 1 >= ntiles) break;
-        // odd tile t+1 in buffer 1; st0 holds tile t+2
-        if (t + 3 < ntiles) load_tile(t + 3, st1);
-        if (t + 1 < wave_tiles) compute(t + 1, 1);
-        f = false;
-        if (t + 2 < ntiles) f = store_tile(0, st0);
-        any_ovf |= __syncthreads_or(f);
-    }
-    if constexpr (!EXACT) {
-        if (a.flags && tid == 0) a.flags[wg_id] = any_ovf ? 1u : 0u;
-        if (any_ovf) return;  // the exact pass owns this workgroup's rows
-    }
-
-    if (!wave_live) return;
-    // ---- normalise and store: lane holds query q0+16nt+li, dims 16dt+4lg+j ------------
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        float l = lrun[nt];
-        l = sum_xor16(l);
-        l = sum_xor32(l);
-        const uint32_t qr = q0 + 16 * nt + li;
-        if (qr >= T) continue;
-        const float inv = 1.0f / l;
-        const size_t obase = ((size_t)qr * a.q_heads + head) * D;
-#pragma unroll
-        for (int dt = 0; dt < DTILES; ++dt)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) store_any(a.out, obase + 16 * dt + 4 * lg + j, oacc[dt][nt][j] * inv, a.out_dtype);
+// The exact pass after the pipelined kernel (bf16 caches), a few workgroups
+// walking the query blocks.  Usually no V value is outside the f16 range:
+// every workgroup then exits after one scan of the tile flags that the V^T
+// pre-pass wrote for this call's tiles, so the launch costs little more than
+// its dispatch.  Otherwise each flagged block runs on the exact path.
+template <int D, int HW, int QW>
+__global__ __launch_bounds__(512, 1) void prefill_exact_pass_kernel(PrefillArgs a, uint32_t blocks) {
+    __shared__ __attribute__((aligned(16))) char lds[prefill_rows_lds_bytes<D>()];
+    const uint32_t tiles = (a.start + a.tokens + 63) / 64;
+    bool any = false;
+    for (uint32_t i = threadIdx.x; i < a.kv_heads * tiles; i += blockDim.x)
+        any |= a.tile_flags[(size_t)(i / tiles) * a.tile_flag_stride + i % tiles] != 0;
+    if (!__syncthreads_or(any)) return;
+    for (uint32_t b = blockIdx.x; b < blocks; b += gridDim.x) {
+        prefill_rows<D, BF16, HW, QW, true>(a, lds, b, 0, b);
+        __syncthreads();  // the next block overwrites the LDS tiles
     }
 }
+
+// workgroups of the exact pass after the pipelined kernel: one per CU at most
+constexpr uint32_t kExactPassWgs = 256;
 
 // fp32 and mixed K/V caches run causal rows on the decode kernels (every query
 // row streams its own prefix: fine for the K <= 4 verifier rows, quadratic in
@@ -486,8 +104,13 @@ hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint3
         if (!bf) {
             hipLaunchKernelGGL((prefill_attention_kernel<64, F16, 2, 4, false>), grid, dim3(512), 0, st, a);
         } else {
-            if (!pp) hipLaunchKernelGGL((prefill_attention_kernel<64, BF16, 2, 4, false>), grid, dim3(512), 0, st, a);
-            hipLaunchKernelGGL((prefill_attention_kernel<64, BF16, 2, 4, true>), grid, dim3(512), 0, st, a);
+            if (pp) {
+                const uint32_t wgs = grid.x < kExactPassWgs ? grid.x : kExactPassWgs;
+                hipLaunchKernelGGL((prefill_exact_pass_kernel<64, 2, 4>), dim3(wgs), dim3(512), 0, st, a, grid.x);
+            } else {
+                hipLaunchKernelGGL((prefill_attention_kernel<64, BF16, 2, 4, false>), grid, dim3(512), 0, st, a);
+                hipLaunchKernelGGL((prefill_attention_kernel<64, BF16, 2, 4, true>), grid, dim3(512), 0, st, a);
+            }
         }
     } else if (s.head_dim == 128 && s.group == 8) {
         a.qblocks = (tokens + 31) / 32;
@@ -496,8 +119,13 @@ hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint3
         if (!bf) {
             hipLaunchKernelGGL((prefill_attention_kernel<128, F16, 8, 1, false>), grid, dim3(512), 0, st, a);
         } else {
-            if (!pp) hipLaunchKernelGGL((prefill_attention_kernel<128, BF16, 8, 1, false>), grid, dim3(512), 0, st, a);
-            hipLaunchKernelGGL((prefill_attention_kernel<128, BF16, 8, 1, true>), grid, dim3(512), 0, st, a);
+            if (pp) {
+                const uint32_t wgs = grid.x < kExactPassWgs ? grid.x : kExactPassWgs;
+                hipLaunchKernelGGL((prefill_exact_pass_kernel<128, 8, 1>), dim3(wgs), dim3(512), 0, st, a, grid.x);
+            } else {
+                hipLaunchKernelGGL((prefill_attention_kernel<128, BF16, 8, 1, false>), grid, dim3(512), 0, st, a);
+                hipLaunchKernelGGL((prefill_attention_kernel<128, BF16, 8, 1, true>), grid, dim3(512), 0, st, a);
+            }
         }
     } else {
         return hipErrorNotSupported;

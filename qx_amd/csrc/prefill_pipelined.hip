@@ -11,7 +11,8 @@
 //    slot 8g+4+j holds position 16+4g+j.  bf16 values are rounded to f16
 //    (exact inside the f16 range); a tile holding a value outside the finite
 //    f16 range gets a flag, and the query rows that reach such a tile are
-//    left to the exact bf16 kernel (prefill_attention.hip).
+//    left to the exact bf16 pass (prefill_exact_pass_kernel in
+//    prefill_attention.hip, the body in prefill_rows.h).
 //
 // 2. prefill_pipe_kernel: 8 waves share one K/V head.  K and V^T tiles are
 //    copied HBM -> LDS by buffer_load_dwordx4 ... lds (no VGPR staging),

@@ -124,13 +124,14 @@ def test_prefill_last_row_equals_decode(ctx, shape, dtype):
             assert rel_err(pre[t].cpu().numpy(), dec[0].cpu().numpy()) <= TOL_16, t
 
 
-@pytest.mark.parametrize("shape", [abi.SHAPE_GRANITE, abi.SHAPE_QWEN3])
-def test_bf16_values_outside_f16_range_take_the_exact_pass(ctx, shape):
+@pytest.mark.parametrize("shape,T", [(abi.SHAPE_GRANITE, 300), (abi.SHAPE_QWEN3, 300), (abi.SHAPE_QWEN3, 4096)])
+def test_bf16_values_outside_f16_range_take_the_exact_pass(ctx, shape, T):
     """bf16 V tiles are multiplied in f16; a value beyond the f16 range must
-    route its workgroup to the exact bf16 pass and still match the oracle."""
-    log("prefill overflow path", shape)
+    route its workgroup to the exact bf16 pass and still match the oracle.
+    T = 300 splits each block's KV range into chunks, T = 4096 does not;
+    Qwen's pipelined kernel runs the exact rows itself."""
+    log("prefill overflow path", shape, T)
     info = rt.shape_info(shape)
-    T = 300
     rng = np.random.default_rng(77)
     arena = rt.KvArena(ctx, shape, 1, 1, T, abi.BF16)
     q = torch.empty((T, info.q_heads, info.head_dim), dtype=torch.bfloat16, device="cuda:0")
@@ -148,7 +149,7 @@ def test_bf16_values_outside_f16_range_take_the_exact_pass(ctx, shape):
     with rt.Graph(ctx) as g:
         out = rt.prefill_attention(g, arena, 0, 0, q, out_dtype=torch.float32)
         kk, vv = arena.gather(g, 0, 0, 0, T)
-    rows = np.array([0, 4, 5, 6, 100, 249, 250, 251, 299], np.uint32)
+    rows = np.array([0, 4, 5, 6, 100, 249, 250, 251, 299] + ([2047, 4095] if T > 300 else []), np.uint32)
     if shape == abi.SHAPE_QWEN3:
         _, ref = O.qwen_prefill_rows(bits(q), bits(kk), bits(vv), 0, rows, O.BF16)
     else:
