@@ -32,23 +32,26 @@ __device__ __forceinline__ f32x4 ldg4_nt(const float* p) {
 // rms_norm of the 1024-wide hidden vector (crates/qx-runtime/src/lib.rs:2406-2414),
 // recomputed by every wave from its own column slices: sum of squares in
 // fma, consensus rsqrt(mean + eps), y = x * scale * w.
+// The norm weights are loaded with the hidden slices, before the reduction,
+// so both requests are in flight together.
 __device__ __forceinline__ void normalize_slices(const float* hidden, const float* weight, int lane, f32x4 (&n)[4]) {
-    f32x4 x[4];
-    float ss = 0.0f;
+    f32x4 x[4], w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         x[i] = ldg4(hidden + 256 * i + 4 * lane);
+        w[i] = ldg4(weight + 256 * i + 4 * lane);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int c = 0; c < 4; ++c) ss = __builtin_fmaf(x[i][c], x[i][c], ss);
-    }
     ss = group_sum<64>(ss);
     const float scale = consensus_rsqrt(ss / (float)kHidden + kRmsEps);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const f32x4 w = ldg4(weight + 256 * i + 4 * lane);
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) n[i][c] = x[i][c] * scale * w[c];
-    }
+        for (int c = 0; c < 4; ++c) n[i][c] = x[i][c] * scale * w[i][c];
 }
 
 __device__ __forceinline__ float row_dot_loaded(const f32x4 (&w)[4], const f32x4 (&n)[4]) {
@@ -60,22 +63,12 @@ __device__ __forceinline__ float row_dot_loaded(const f32x4 (&w)[4], const f32x4
     return group_sum<64>(d);
 }
 
-__device__ __forceinline__ float row_dot(const float* row, const f32x4 (&n)[4], int lane) {
-    f32x4 w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = ldg4_nt(row + 256 * i + 4 * lane);
-    return row_dot_loaded(w, n);
-}
-
 // grid 256 workgroups x 4 waves.  Workgroup b: head block hb = b / 8 (0-15 q,
 // 16-23 k, 24-31 v), pair group pg = b % 8; wave w owns pair p = 4*pg + w.
 __global__ __launch_bounds__(256) void granite_qkv_rope_kernel(KvLayer kv, GraniteBlockArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int hb = blockIdx.x >> 3, pg = blockIdx.x & 7;
     const int p = pg * 4 + wave;
-    f32x4 n[4];
-    normalize_slices(a.hidden_in, a.input_norm, lane, n);
-
     const float* w;
     int head;
     if (hb < 16) {
@@ -88,8 +81,18 @@ __global__ __launch_bounds__(256) void granite_qkv_rope_kernel(KvLayer kv, Grani
         w = a.wv;
         head = hb - 24;
     }
-    const float x = row_dot(w + (size_t)(head * 64 + p) * kHidden, n, lane);
-    const float y = row_dot(w + (size_t)(head * 64 + 32 + p) * kHidden, n, lane);
+    // the two weight rows are requested first: their HBM latency overlaps
+    // the loads and the reduction of the norm
+    f32x4 wx[4], wy[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        wx[i] = ldg4_nt(w + (size_t)(head * 64 + p) * kHidden + 256 * i + 4 * lane);
+        wy[i] = ldg4_nt(w + (size_t)(head * 64 + 32 + p) * kHidden + 256 * i + 4 * lane);
+    }
+    f32x4 n[4];
+    normalize_slices(a.hidden_in, a.input_norm, lane, n);
+    const float x = row_dot_loaded(wx, n);
+    const float y = row_dot_loaded(wy, n);
     if (lane != 0) return;
     const size_t slot = (size_t)head * kv.head_stride + (size_t)a.position * 64;
     if (hb >= 24) {
@@ -119,10 +122,13 @@ __global__ __launch_bounds__(256) void granite_qkv_rope_kernel(KvLayer kv, Grani
 __global__ __launch_bounds__(256) void granite_out_residual_kernel(GraniteBlockArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + wave;
-    f32x4 n[4];
+    f32x4 w[4], n[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) n[i] = ldg4(a.attention + 256 * i + 4 * lane);
-    const float proj = row_dot(a.wo + (size_t)row * kHidden, n, lane);
+    for (int i = 0; i < 4; ++i) {
+        w[i] = ldg4_nt(a.wo + (size_t)row * kHidden + 256 * i + 4 * lane);
+        n[i] = ldg4(a.attention + 256 * i + 4 * lane);
+    }
+    const float proj = row_dot_loaded(w, n);
     if (lane == 0) a.hidden_out[row] = __builtin_fmaf(kResidual, proj, a.hidden_in[row]);
 }
 
