@@ -179,6 +179,55 @@ __device__ __forceinline__ void chunk_leaf(uint32_t idx, Load load, uint32_t (&o
     }
 }
 
+// The same digest with the chunk in two 128-byte pieces: the first (groups
+// 0..7) is loaded into registers up front, the second (groups 8..15) was
+// copied into LDS beforehand; staged(k) returns its group 8 + k.  Every
+// group of a piece is requested in one burst, so each 128-byte line is
+// fetched from HBM once; a line read piece by piece over several
+// compressions may leave L2 in between and be fetched again.
+template <class Dom, class Load, class Staged>
+__device__ __forceinline__ void chunk_leaf_staged(uint32_t idx, Load load, Staged staged, uint32_t (&out)[8]) {
+    constexpr Prefix pre = Dom::prefix();
+    constexpr int P = Dom::len + 20;
+    static_assert(P == pre.len && P <= 48, "framing length");
+    static_assert(last_group<P>(0) < 8, "block 0 reads the first piece only");
+    uint32_t pw[12];
+#pragma unroll
+    for (int i = 0; i < 12; ++i) pw[i] = pre.w[i];
+    constexpr int ib = Dom::len + 8;
+    constexpr int sh = 8 * (ib % 4);
+    pw[ib / 4] |= idx << sh;
+    if constexpr (sh != 0) pw[ib / 4 + 1] |= idx >> (32 - sh);
+    constexpr int total = P + 256;
+    constexpr int blocks = (total + 63) / 64;
+    u32x4 g[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) g[i] = load(i);
+    iv_init(out);
+    bool landed = false;
+#pragma unroll
+    for (int b = 0; b < blocks; ++b) {
+        // the staged groups of block b + 1, read one block ahead
+        if (b + 1 < blocks) {
+            const int lo = last_group<P>(b) + 1 > 8 ? last_group<P>(b) + 1 : 8;
+            const int hi = last_group<P>(b + 1);
+            if (hi >= lo && !landed) {
+                // the copy into LDS was issued before the register loads
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                landed = true;
+            }
+#pragma unroll
+            for (int i = lo; i <= hi; ++i) g[i] = staged(i - 8);
+        }
+        uint32_t m[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) m[i] = stream_word<P>(16 * b + i, pw, g);
+        const uint32_t len = b + 1 < blocks ? 64u : (uint32_t)(total - 64 * (blocks - 1));
+        const uint32_t flags = (b == 0 ? kFlagStart : 0u) | (b + 1 == blocks ? kFlagEnd | kFlagRoot : 0u);
+        compress(out, m, len, flags);
+    }
+}
+
 // parent = BLAKE3(left || right): one full block
 __device__ __forceinline__ void parent_digest(const uint32_t (&l)[8], const uint32_t (&r)[8], uint32_t (&out)[8]) {
     uint32_t m[16];
@@ -300,12 +349,28 @@ struct KvLeafArgs {
     uint8_t* out;
 };
 
-// CH = chunks per row (4 or 8): 64 / CH leaves per wave, 4 waves per block
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void global_void;
+
+// Copy bytes [128, 256) of a lane's chunk into LDS: eight 16-byte
+// direct-to-LDS loads, group 8 + k of lane l landing at stage[k][l].
+template <class Addr>
+__device__ __forceinline__ void stage_second_piece(Addr addr, u32x4 (*stage)[64]) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        __builtin_amdgcn_global_load_lds((global_void*)addr(8 + k), (lds_void*)&stage[k][0], 16, 0, 0);
+}
+
+// CH = chunks per row (4 or 8): 64 / CH leaves per wave, 4 waves per block.
+// Each wave stages the second half of its lanes' chunks in 8 KB of LDS
+// (32 KB per block, three blocks per CU).
 template <int CH>
 __global__ __launch_bounds__(256, 3) void kv_leaf_hash_kernel(KvLeafArgs a) {
+    __shared__ u32x4 stage_all[4][8][64];
     constexpr int LPW = 64 / CH;
     const int lane = threadIdx.x & 63;
     const int gl = lane % CH;
+    u32x4 (*stage)[64] = stage_all[__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)];
     const uint64_t total = (uint64_t)a.sequences * a.count;
     const uint64_t leaf = ((uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * LPW + lane / CH;
     const bool live = leaf < total;
@@ -316,12 +381,17 @@ __global__ __launch_bounds__(256, 3) void kv_leaf_hash_kernel(KvLeafArgs a) {
     const char* kb = a.keys + s * a.seq_stride_bytes_k;
     const char* vb = a.values + s * a.seq_stride_bytes_v;
     uint32_t kd[8], vd[8], node[8], d[8];
-    chunk_leaf<KeyChunkDomain>((uint32_t)gl, [&](int i) {
-        return *reinterpret_cast<const u32x4*>(row_byte(kb, a.head_stride_bytes_k, a.head_shift_k, row_off, 256u * gl + 16u * i));
-    }, kd);
-    chunk_leaf<ValueChunkDomain>((uint32_t)gl, [&](int i) {
-        return *reinterpret_cast<const u32x4*>(row_byte(vb, a.head_stride_bytes_v, a.head_shift_v, row_off, 256u * gl + 16u * i));
-    }, vd);
+    auto kaddr = [&](int i) { return row_byte(kb, a.head_stride_bytes_k, a.head_shift_k, row_off, 256u * gl + 16u * i); };
+    auto vaddr = [&](int i) { return row_byte(vb, a.head_stride_bytes_v, a.head_shift_v, row_off, 256u * gl + 16u * i); };
+    auto staged = [&](int k) { return stage[k][lane]; };
+    stage_second_piece(kaddr, stage);
+    chunk_leaf_staged<KeyChunkDomain>((uint32_t)gl, [&](int i) { return *reinterpret_cast<const u32x4*>(kaddr(i)); },
+                                      staged, kd);
+    // every LDS read of the key piece has returned before the value piece lands there
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    stage_second_piece(vaddr, stage);
+    chunk_leaf_staged<ValueChunkDomain>((uint32_t)gl, [&](int i) { return *reinterpret_cast<const u32x4*>(vaddr(i)); },
+                                        staged, vd);
     kv_roots<CH>(kd, vd, lane, gl, node);
     // lane 0 of the group: key root; lane CH/2: value root
     uint32_t vr[8];
