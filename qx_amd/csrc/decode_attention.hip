@@ -881,6 +881,10 @@ bool decode_dtypes_supported(const ShapeDims& s, int key_dtype, int value_dtype)
     return s.head_dim == 64 && s.group == 2 && (key_dtype == F32 || value_dtype == F32);
 }
 
+static uint32_t qwen_min_chunk(int key_dtype, int value_dtype) {
+    return key_dtype == value_dtype && (key_dtype == F16 || key_dtype == BF16) ? 512u : 256u;
+}
+
 DecodePlan plan_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t sequences, uint32_t length) {
     DecodePlan p{};
     p.waves = kWaves;
@@ -892,10 +896,14 @@ DecodePlan plan_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint3
     // VALU kernel: keep the (m, l, acc) partial small next to the KV bytes it
     // summarises; MFMA kernel (16-bit): one 32-position tile per wave
     uint32_t min_chunk = valu ? kWaves * step : kWaves * 32;
-    // G >= 8 (Qwen): a split of at least 512 positions keeps the G x D fp32
-    // partial small next to the KV bytes it summarises (batch-1 Qwen3 decode
-    // at 4096 positions: 18.8 us per layer at 512, 19.1 at 256, 22.8 at 1024)
-    if (s.group >= 8 && min_chunk < 512) min_chunk = 512;
+    // G >= 8 (Qwen): a split of at least 512 positions on 16-bit caches (256
+    // on the others, tiered values among them, whose INT8 pass costs more per
+    // position) keeps the G x D fp32 partial
+    // small next to the KV bytes it summarises (batch-1 Qwen3 decode at 32768
+    // positions, bf16: 18.8 us per layer at 512, 19.1 at 256, 22.8 at 1024;
+    // tiered: 18.0 us at 256, 20.2 at 512)
+    if (s.group >= 8 && min_chunk < qwen_min_chunk(key_dtype, value_dtype))
+        min_chunk = qwen_min_chunk(key_dtype, value_dtype);
     uint32_t want = (target_wgs + units - 1) / units;
     uint32_t cap = (length + min_chunk - 1) / min_chunk;
     uint32_t splits = want < cap ? want : cap;
@@ -1103,7 +1111,8 @@ uint64_t decode_causal_workspace_bound(const ShapeDims& s, int key_dtype, int va
     const bool valu = valu_path(key_dtype, value_dtype);
     const uint32_t rpw = (uint32_t)rows_per_wave_load(s.head_dim, key_dtype);
     uint32_t min_chunk = valu ? kWaves * rpw * kUnroll : kWaves * 32;
-    if (s.group >= 8 && min_chunk < 512) min_chunk = 512;
+    if (s.group >= 8 && min_chunk < qwen_min_chunk(key_dtype, value_dtype))
+        min_chunk = qwen_min_chunk(key_dtype, value_dtype);
     const uint32_t want = (2048 + units - 1) / units;
     const uint32_t cap = (capacity + min_chunk - 1) / min_chunk;
     uint32_t bound = want < cap ? want : cap;
