@@ -479,7 +479,7 @@ def bench_kv_hash(ctx, steps, warmup):
     return {"us_per_layer": ms * 1000.0, "leaves": leaves, "kv_bytes": leaves * 2 * row,
             "gb_per_s": leaves * 2 * row / (ms * 1e-3) / 1e9, "leaves_per_s": leaves / (ms * 1e-3),
             "roofline": {"bound": "valu", "achieved": round(tops, 2), "peak": round(VALU_PEAK_TOPS, 1),
-                         "unit": "Top/s", "frac": round(tops / VALU_PEAK_TOPS, 4), "traffic": None},
+                         "unit": "Top/s", "frac": round(tops / VALU_PEAK_TOPS, 4), "traffic": load_traffic("kvhash")},
             "note": "kv_leaf_hash_v1 (BLAKE3) of all 256 x 4096 fp16 token rows of one Granite layer; "
                     "ops = 48 compressions x 784 32-bit ops per leaf"}
 

@@ -178,13 +178,17 @@ def test_cfg4_batched_fp16_decode_full_size(ctx):
     with rt.Graph(ctx) as g:
         out = rt.attention(g, arena, 0, q, L)
     assert torch.isfinite(out).all()
+    worst = 0.0
     for s in (0, 1, 128, 255):
         with rt.Graph(ctx) as g:
             kk, vv = arena.gather(g, 0, s, 0, L)
         ref_cache = O.KvCache(L)
         ref_cache.extend(kk.float().cpu().numpy(), vv.float().cpu().numpy())
         r = O.granite_attend(q[s].cpu().numpy().ravel(), ref_cache, L)
-        assert rel_err(out[s].cpu().numpy().ravel(), r) <= TOL_16
+        e = rel_err(out[s].cpu().numpy().ravel(), r)
+        worst = max(worst, e)
+        assert e <= TOL_16
+    log(f"  cfg4 worst max-abs/rms {worst:.3e} over sequences 0, 1, 128, 255")
 
 
 def test_split_and_unsplit_agree(ctx):
