@@ -124,12 +124,15 @@ def test_prefill_last_row_equals_decode(ctx, shape, dtype):
             assert rel_err(pre[t].cpu().numpy(), dec[0].cpu().numpy()) <= TOL_16, t
 
 
-@pytest.mark.parametrize("shape,T", [(abi.SHAPE_GRANITE, 300), (abi.SHAPE_QWEN3, 300), (abi.SHAPE_QWEN3, 4096)])
+@pytest.mark.parametrize("shape,T", [(abi.SHAPE_GRANITE, 300), (abi.SHAPE_QWEN3, 300), (abi.SHAPE_QWEN3, 4096),
+                                     (abi.SHAPE_QWEN3, 9000)])
 def test_bf16_values_outside_f16_range_take_the_exact_pass(ctx, shape, T):
     """bf16 V tiles are multiplied in f16; a value beyond the f16 range must
     route its workgroup to the exact bf16 pass and still match the oracle.
-    T = 300 splits each block's KV range into chunks, T = 4096 does not;
-    Qwen's pipelined kernel runs the exact rows itself."""
+    T = 300 splits each block's KV range into chunks, T = 4096 does not.
+    The exact pass after the pipelined kernel runs at most 256 workgroups:
+    at Qwen T = 9000 (1,128 blocks, every block of kv heads 0 and 3
+    flagged) each walks four or five blocks, reusing its LDS."""
     log("prefill overflow path", shape, T)
     info = rt.shape_info(shape)
     rng = np.random.default_rng(77)
@@ -149,7 +152,8 @@ def test_bf16_values_outside_f16_range_take_the_exact_pass(ctx, shape, T):
     with rt.Graph(ctx) as g:
         out = rt.prefill_attention(g, arena, 0, 0, q, out_dtype=torch.float32)
         kk, vv = arena.gather(g, 0, 0, 0, T)
-    rows = np.array([0, 4, 5, 6, 100, 249, 250, 251, 299] + ([2047, 4095] if T > 300 else []), np.uint32)
+    rows = np.array([0, 4, 5, 6, 100, 249, 250, 251, 299] + ([2047, 4095] if T > 300 else []) +
+                    ([6000, T - 1] if T > 4096 else []), np.uint32)
     if shape == abi.SHAPE_QWEN3:
         _, ref = O.qwen_prefill_rows(bits(q), bits(kk), bits(vv), 0, rows, O.BF16)
     else:
