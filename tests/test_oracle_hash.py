@@ -2,12 +2,16 @@
 
 BLAKE3 is the `blake3` crate 1.8.7 (Cargo.lock:656-659, not vendored); the
 commitment framing is crates/qx-commit/src/{hash.rs,state.rs,merkle.rs,execution.rs}.
-Pins: the BLAKE3 specification's empty-input vector and the reference's own
-protocol golden vectors (crates/qx-commit/tests/golden_vectors.rs:66-190),
-which run kv_leaf_hash_v1, state_hash_v1 and BLAKE3 Merkle parents on one-chunk
-trees and one- and two-block inputs.  SHA-256 leaves of those vectors come
-from hashlib.  Multi-chunk trees and inputs of three or more blocks have no
-reference vector: parity unpinned there.
+Pins: the BLAKE3 project's published test vectors (test_vectors.json of the
+BLAKE3 specification repository: input byte i is i mod 251) for 0, 1, 1023
+and 1024 bytes, so one to sixteen 64-byte blocks of a chunk, with the
+partial last block; and the reference's own protocol golden vectors
+(crates/qx-commit/tests/golden_vectors.rs:66-190), which run kv_leaf_hash_v1,
+state_hash_v1 and BLAKE3 Merkle parents on one-chunk trees.  SHA-256 leaves
+of those vectors come from hashlib.  Trees of several 256-byte chunks (token
+rows above 256 bytes) are built from these pinned primitives in state.rs's
+order (crates/qx-commit/src/state.rs:313-348); no reference vector covers a
+multi-chunk tree itself.
 """
 import hashlib
 import struct
@@ -35,8 +39,24 @@ def f32_bytes(values):
     return b"".join(struct.pack("<f", v) for v in values)
 
 
-def test_blake3_empty_input_vector():
-    assert O.blake3(b"").hex() == "af1349b9f5f9a1a6a0404dea36dcc9499bcb25c9adc112b7cc9a93cae41f3262"
+# BLAKE3 test_vectors.json: (input length, first 32 bytes of the hash)
+BLAKE3_PUBLISHED = [
+    (0, "af1349b9f5f9a1a6a0404dea36dcc9499bcb25c9adc112b7cc9a93cae41f3262"),
+    (1, "2d3adedff11b61f14c886e35afa036736dcd87a74d27b5c1510225d0f592e213"),
+    (1023, "10108970eeda3eb932baac1428c7a2163b0e924c9a9e25b35bba72b28f70bd11"),
+    (1024, "42214739f095a406f3fc83deb889744ac00df831c10daa55189b5d121c855af7"),
+]
+
+
+@pytest.mark.parametrize("n,digest", BLAKE3_PUBLISHED)
+def test_blake3_published_vectors(n, digest):
+    assert O.blake3(bytes(i % 251 for i in range(n))).hex() == digest
+
+
+def test_blake3_single_chunk_limit():
+    # the commitment scheme never hashes more than one 1024-byte chunk at once
+    with pytest.raises(RuntimeError, match="input rejected"):
+        O.blake3(bytes(1025))
 
 
 def test_reference_protocol_golden_vectors():
