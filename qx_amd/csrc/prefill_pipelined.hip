@@ -14,21 +14,25 @@
 //    left to the exact bf16 pass (prefill_exact_pass_kernel in
 //    prefill_attention.hip, the body in prefill_rows.h).
 //
-// 2. prefill_pipe_kernel: 8 waves share one K/V head.  K and V^T tiles are
-//    copied HBM -> LDS by buffer_load_dwordx4 ... lds (no VGPR staging),
-//    three stages deep, with XOR swizzles that keep the 16-lane operand
-//    reads free of bank conflicts.  Each round is an MFMA phase (O^T +=
-//    V^T.P^T for tile r-1, S^T = K.Q^T for tile r, operand reads software-
-//    pipelined ahead of the MFMAs) and a softmax phase, with one workgroup
-//    barrier between them.  All waves run the phases in step: on gfx950 the
-//    softmax VALU work slows the LDS operand stream it would overlap with,
-//    and a measured ping-pong arrangement (the two waves of a SIMD half a
-//    round apart) was 5% slower than this.
+// 2. prefill_pipe_kernel: the waves of a workgroup share one K/V head.  K
+//    and V^T tiles are copied HBM -> LDS by buffer_load_dwordx4 ... lds (no
+//    VGPR staging), with XOR swizzles that keep the 16-lane operand reads
+//    free of bank conflicts.  Each round is an MFMA phase (O^T += V^T.P^T
+//    for tile r-1, S^T = K.Q^T for tile r, operand reads software-pipelined
+//    ahead of the MFMAs) and a softmax phase, with one workgroup barrier
+//    between them.  The waves of a workgroup run the phases in step; on
+//    gfx950 the softmax VALU work slows the LDS operand stream it would
+//    overlap with inside one workgroup (a ping-pong of the two waves of a
+//    SIMD, half a round apart, was 5% slower).  Overlap comes from several
+//    independent workgroups per CU instead: Qwen runs two 4-wave workgroups
+//    per query block (heads 0-3 and 4-7 of the group, 64 KB of LDS each, so
+//    two share a CU and drift against each other), Granite three.
 //
 // Stage r (K tile r, V^T tile r-1) is read only in the MFMA phase of round
-// r; its loads are issued at the start of round r-2 into the slot that
-// round r-3 used, and each wave waits for its own loads of stage r+1 before
-// the barrier of round r.
+// r.  With three stages (Granite) its loads are issued at the start of
+// round r-2 into the slot that round r-3 used; with two (Qwen) at the start
+// of round r-1 into the slot round r-2 used.  Each wave waits for its own
+// loads of stage r+1 before the barrier of round r.
 #include <type_traits>
 
 #include "common.h"
@@ -246,14 +250,15 @@ __device__ __forceinline__ void pipe_column(int col, uint32_t wg_t0, uint32_t kv
 }
 
 // Column layout: every wave owns 32 query columns, two 16-column MFMA blocks
-// (nt = 0, 1).  HEADS_PER_WAVE = 1 (Qwen, group 8, NW = 8 waves): wave w is
-// head w of the group, nt selects tokens 16*nt .. of the workgroup's 32
-// tokens.  HEADS_PER_WAVE = 2 (Granite, group 2, NW = 4 waves): nt selects
-// the head, wave w covers tokens 16w .. of the workgroup's 64; three such
-// workgroups share a CU (under 168 VGPRs, 48 KB LDS) and overlap each other's
-// phases.
-template <int D, int DT, int HEADS_PER_WAVE, int NW>
-__global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 3) void prefill_pipe_kernel(PrefillPipeArgs a) {
+// (nt = 0, 1).  HEADS_PER_WAVE = 1 (Qwen, group 8): wave w of the query
+// block (NW = 8 waves in one workgroup, or NW = 4 in each of HALVES = 2
+// workgroups, w = 4 * half + wave) is head w of the group, nt selects tokens
+// 16*nt .. of the block's 32 tokens.  HEADS_PER_WAVE = 2 (Granite, group 2,
+// NW = 4 waves): nt selects the head, wave w covers tokens 16w .. of the
+// workgroup's 64; three such workgroups share a CU (under 168 VGPRs, 48 KB
+// LDS) and overlap each other's phases.
+template <int D, int DT, int HEADS_PER_WAVE, int NW, int HALVES = 1>
+__global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void prefill_pipe_kernel(PrefillPipeArgs a) {
     using M = MfmaT<DT>;
     using MH = MfmaT<F16>;
     using vec = typename M::vec;
@@ -270,10 +275,12 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 3) void prefill_pipe_kernel(
     constexpr int KCH = D / 8;                    // 16-byte chunks per K row
     constexpr int TOKW = HEADS_PER_WAVE == 1 ? 32 : 16;   // tokens per wave
     constexpr int WGT = HEADS_PER_WAVE == 1 ? 32 : 16 * NW;  // tokens per workgroup
-    constexpr int COLS = 32 * NW;                           // query columns per workgroup
+    constexpr int COLS = 32 * NW * HALVES;                  // query columns per query block
+    constexpr int STAGES = HALVES == 2 ? 2 : 3;             // LDS ring depth
     static_assert(LPW * NW == KI + VI, "stage loads must split evenly over the waves");
+    static_assert(HALVES == 1 || (HEADS_PER_WAVE == 1 && NW == 4), "halves: Qwen, 4 waves");
 
-    __shared__ __attribute__((aligned(1024))) char lds[3 * STAGEB];
+    __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGEB];
 
     const int tid = threadIdx.x;
     // readfirstlane: the compiler then knows the wave index (and every branch
@@ -285,17 +292,25 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 3) void prefill_pipe_kernel(
     // block -> (kv head, query block); each XCD serves one kv head (or a
     // fixed share of heads) so the head's K/V stays in that XCD's L2
     const uint32_t nqb = a.qblocks;
-    uint32_t kvh, qidx;
+    uint32_t kvh, qidx, hh;
     if (a.xcd_map) {
         const uint32_t lin = blockIdx.x, xcd = lin & 7, slot = lin >> 3;
         const uint32_t per = 8 / a.kv_heads;
         kvh = xcd / per;
-        qidx = slot * per + (xcd % per);
+        const uint32_t qh = slot * per + (xcd % per);
+        qidx = qh / HALVES;
+        hh = qh % HALVES;
     } else {
-        kvh = blockIdx.x / nqb;
-        qidx = blockIdx.x % nqb;
+        kvh = blockIdx.x / (nqb * HALVES);
+        const uint32_t qh = blockIdx.x % (nqb * HALVES);
+        qidx = qh / HALVES;
+        hh = qh % HALVES;
     }
     const uint32_t qblock = nqb - 1 - qidx;  // longest rows first
+    // HALVES = 2: two workgroups of 4 waves share a query block, the first
+    // on heads 0-3 of the group, the second on heads 4-7; a wave's place in
+    // the block (heads, columns, partial slots) is its virtual index vwave
+    const int vwave = (int)hh * NW + wave;
     const uint32_t T = a.tokens;
     const uint32_t wg_t0 = qblock * WGT;
     const uint32_t kv_len = a.start + min(T, wg_t0 + WGT);
@@ -314,7 +329,8 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 3) void prefill_pipe_kernel(
     int col_head[2];
     uint32_t col_tok[2];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) pipe_column<HEADS_PER_WAVE, NW>(wave * 32 + nt * 16 + li, wg_t0, kvh, a.group, col_tok[nt], col_head[nt]);
+    for (int nt = 0; nt < 2; ++nt)
+        pipe_column<HEADS_PER_WAVE, NW * HALVES>(vwave * 32 + nt * 16 + li, wg_t0, kvh, a.group, col_tok[nt], col_head[nt]);
     const bool wave_live = w_t0 < T;
     const uint32_t w_last = min(T - 1, w_t0 + TOKW - 1);
     const uint32_t wave_n = wave_live ? (a.start + w_last) / kTile + 1 : 0;
@@ -359,7 +375,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 3) void prefill_pipe_kernel(
     const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, kv_len * KROWB);
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vtbase, n * VTILEB);
     auto issue_stage = [&](uint32_t r) {
-        char* sb = lds + (r % 3) * STAGEB;
+        char* sb = lds + (r % STAGES) * STAGEB;
         const uint32_t kt = t0 + min(r, m - 1);
         const uint32_t vtile = t0 + (r == 0 ? 0u : min(r - 1, m - 1));
 #pragma unroll
@@ -422,7 +438,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 3) void prefill_pipe_kernel(
         constexpr int B0 = DO_PV ? 0 : NPV;          // first operand index
         constexpr int B1 = DO_QK ? NPV + NQK : NPV;  // one past the last
         constexpr int N = B1 - B0;
-        const char* st = lds + (r % 3) * STAGEB;
+        const char* st = lds + (r % STAGES) * STAGEB;
         // operand i: PV (i < NPV): half = i / DTILES, dt = i % DTILES;
         //            QK: ks = (i - NPV) / 4, mt = (i - NPV) % 4
         auto read = [&](int i) -> u32x4 {
@@ -545,15 +561,21 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 3) void prefill_pipe_kernel(
                 for (int k = 0; k < 8; ++k) P[half][nt][k] = (_Float16)S[2 * half + (k >> 2)][nt][k & 3];
     };
 
-    // prologue: stages 0 and 1 in flight, stage 0 complete
+    // prologue: stage 0 complete (and stage 1 in flight with three stages)
     issue_stage(0);
-    issue_stage(1);  // m >= 1: stage 1 exists
-    wait_vmcnt<LPW>();
+    if constexpr (STAGES == 3) {
+        issue_stage(1);  // m >= 1: stage 1 exists
+        wait_vmcnt<LPW>();
+    } else {
+        wait_vmcnt<0>();
+    }
     phase_barrier();
 
     for (uint32_t r = 0; r <= m; ++r) {
-        const bool more = r + 2 <= m;
-        if (more) issue_stage(r + 2);
+        // three stages: stage r+2 goes into the slot round r-1 read; two
+        // stages: stage r+1 does
+        const bool more = r + STAGES - 1 <= m;
+        if (more) issue_stage(r + STAGES - 1);
         // MFMA phase: P.V of tile r-1, then S = Q.K of tile r (tiles counted
         // from t0).  Round 0 runs P.V with P = 0, and round wave_m computes a
         // Q.K that no softmax reads: one code path for every round the wave
@@ -562,8 +584,9 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 3) void prefill_pipe_kernel(
         __builtin_amdgcn_s_setprio(1);
         if (r <= wave_m) mfma_phase(r, std::true_type{}, std::true_type{});
         __builtin_amdgcn_s_setprio(0);
-        // stage r+1 complete; stage r+2 (issued above) may still be in flight
-        if (more) wait_vmcnt<LPW>();
+        // stage r+1 complete; with three stages stage r+2 (issued above) may
+        // still be in flight
+        if (STAGES == 3 && more) wait_vmcnt<LPW>();
         else wait_vmcnt<0>();
         phase_barrier();
         // softmax phase of tile r (no LDS access: the next round's MFMA phase
@@ -577,7 +600,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 3) void prefill_pipe_kernel(
         const size_t slot = (((size_t)kvh * nqb + qblock) * a.max_chunks + chunk) * COLS;
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-            const size_t colx = slot + wave * 32 + nt * 16 + li;
+            const size_t colx = slot + vwave * 32 + nt * 16 + li;
             if (lg == 0) {
                 a.part_ml[2 * colx] = mrun[nt] * c;
                 a.part_ml[2 * colx + 1] = lacc[nt][0];
@@ -685,12 +708,13 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillPipeArgs a)
 // ---------------------------------------------------------------------------
 uint32_t prefill_pipe_vt_tiles(uint32_t capacity) { return (capacity + kTile - 1) / kTile; }
 
-// waves per workgroup, tokens per workgroup, query columns per workgroup
+// waves, tokens and query columns per query block (Qwen's block is two
+// workgroups of four waves, Granite's one workgroup)
 static int pipe_waves(const ShapeDims& s) { return s.head_dim == 128 ? 8 : 4; }
 static uint32_t pipe_tokens_per_wg(const ShapeDims& s) { return s.head_dim == 128 ? 32 : 16 * pipe_waves(s); }
 static uint32_t pipe_columns(const ShapeDims& s) { return 32 * pipe_waves(s); }
 
-// Fewer workgroups than this split their blocks' KV ranges (at most
+// Fewer query blocks than this split their KV ranges (at most
 // kMaxPipeChunks chunks) so that short prompts still fill the CUs.
 constexpr uint32_t kSplitBelowWgs = 512;
 
@@ -777,7 +801,8 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
     a.kv_heads = s.kv_heads;
     const uint32_t wgt = pipe_tokens_per_wg(s);
     a.qblocks = (tokens + wgt - 1) / wgt;
-    a.xcd_map = (8 % s.kv_heads == 0) && ((uint64_t)a.qblocks * s.kv_heads) % 8 == 0;
+    const uint32_t halves = s.head_dim == 128 ? 2u : 1u;  // Qwen: two 4-wave workgroups per query block
+    a.xcd_map = (8 % s.kv_heads == 0) && ((uint64_t)a.qblocks * s.kv_heads * halves) % 8 == 0;
     a.chunk_tiles = pipe_chunk_tiles(s, start, tokens);
     a.max_chunks = kMaxPipeChunks;
     const uint64_t slots = (uint64_t)a.qblocks * s.kv_heads * kMaxPipeChunks * pipe_columns(s);
@@ -785,10 +810,10 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
     a.part_o = a.part_ml + 2 * slots;
     // chunks of the longest block (the last one; with start it is the longest)
     const uint32_t chunks = a.chunk_tiles ? (tiles + a.chunk_tiles - 1) / a.chunk_tiles : 1;
-    dim3 grid(a.qblocks * s.kv_heads, chunks);
+    dim3 grid(a.qblocks * s.kv_heads * halves, chunks);
     if (s.head_dim == 128) {
-        if (bf) hipLaunchKernelGGL((prefill_pipe_kernel<128, BF16, 1, 8>), grid, dim3(512), 0, st, a);
-        else hipLaunchKernelGGL((prefill_pipe_kernel<128, F16, 1, 8>), grid, dim3(512), 0, st, a);
+        if (bf) hipLaunchKernelGGL((prefill_pipe_kernel<128, BF16, 1, 4, 2>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((prefill_pipe_kernel<128, F16, 1, 4, 2>), grid, dim3(256), 0, st, a);
     } else {
         if (bf) hipLaunchKernelGGL((prefill_pipe_kernel<64, BF16, 2, 4>), grid, dim3(256), 0, st, a);
         else hipLaunchKernelGGL((prefill_pipe_kernel<64, F16, 2, 4>), grid, dim3(256), 0, st, a);
