@@ -350,43 +350,42 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
     const char* kbase = reinterpret_cast<const char*>(a.keys) + (size_t)kvh * a.head_stride * 2;
     const char* vtbase = reinterpret_cast<const char*>(a.vt) + (size_t)kvh * a.vt_tiles * VTILEB;
 
-    // Direct loads: stage load j (1 KB) is issued by wave j / LPW.  Loads
-    // j < KI copy RPI rows of the K tile, the rest copy 8 rows (d) of the V^T
-    // tile.  The per-lane part of each source address is fixed: the row in
-    // the tile and the (swizzled) 16-byte chunk.
+    // Direct loads: stage load j (1 KB) is issued by wave j / LPW, so a wave
+    // issues only K loads (j < KI: RPI rows of the K tile each) or only V^T
+    // loads (8 rows d of the V^T tile each).  A lane's byte offset inside
+    // the tile (row and swizzled 16-byte chunk) is fixed for the kernel; the
+    // tile's base goes into a buffer resource built in scalar registers each
+    // round, so issuing a stage costs no VALU instruction.  K rows at or past
+    // kv_len (the last tile's tail) fall outside the resource and are not
+    // read; the causal mask drops those positions.
     constexpr int RPI = 1024 / KROWB;
-    int ld_row[LPW];       // K: row in the tile
-    uint32_t ld_off[LPW];  // K: chunk byte offset in the row; V^T: byte offset in the tile
+    static_assert(KI % LPW == 0, "a wave issues K loads only or V^T loads only");
+    const bool k_wave = wave * LPW < KI;
+    uint32_t ld_off[LPW];  // byte offset of the lane's 16 bytes in the tile
 #pragma unroll
     for (int k = 0; k < LPW; ++k) {
         const int j = wave * LPW + k;
-        if (j < KI) {
+        if (k_wave) {
             const int row = j * RPI + lane / KCH;
             const int swz = D == 128 ? (row & 15) : ((row >> 1) & 7);
-            ld_row[k] = row;
-            ld_off[k] = (uint32_t)(((lane % KCH) ^ swz) * 16);
+            ld_off[k] = (uint32_t)(row * KROWB + ((lane % KCH) ^ swz) * 16);
         } else {
             const int d = (j - KI) * 8 + (lane >> 3);
-            ld_row[k] = 0;
             ld_off[k] = (uint32_t)(d * 128 + ((lane & 7) ^ ((d >> 1) & 7)) * 16);
         }
     }
-    // resources over exactly the rows this workgroup may read
-    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, kv_len * KROWB);
-    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vtbase, n * VTILEB);
     auto issue_stage = [&](uint32_t r) {
         char* sb = lds + (r % STAGES) * STAGEB;
-        const uint32_t kt = t0 + min(r, m - 1);
-        const uint32_t vtile = t0 + (r == 0 ? 0u : min(r - 1, m - 1));
+        if (k_wave) {
+            const uint32_t kt = t0 + min(r, m - 1);
+            const __amdgpu_buffer_rsrc_t rs = make_rsrc(kbase + (size_t)kt * KTILEB, (kv_len - kt * kTile) * KROWB);
 #pragma unroll
-        for (int k = 0; k < LPW; ++k) {
-            const int j = wave * LPW + k;
-            if (j < KI) {
-                const uint32_t pos = min(kt * kTile + ld_row[k], kv_len - 1);
-                lds_dma16(krs, pos * KROWB + ld_off[k], sb + j * 1024);
-            } else {
-                lds_dma16(vrs, vtile * VTILEB + ld_off[k], sb + KTILEB + (j - KI) * 1024);
-            }
+            for (int k = 0; k < LPW; ++k) lds_dma16(rs, ld_off[k], sb + (wave * LPW + k) * 1024);
+        } else {
+            const uint32_t vtile = t0 + (r == 0 ? 0u : min(r - 1, m - 1));
+            const __amdgpu_buffer_rsrc_t rs = make_rsrc(vtbase + (size_t)vtile * VTILEB, VTILEB);
+#pragma unroll
+            for (int k = 0; k < LPW; ++k) lds_dma16(rs, ld_off[k], sb + KTILEB + (wave * LPW + k - KI) * 1024);
         }
     };
     auto kswz = [](int row) { return D == 128 ? (row & 15) : ((row >> 1) & 7); };
