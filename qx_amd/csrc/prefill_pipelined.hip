@@ -70,7 +70,12 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-__device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+// IEEE-754 maximum (NaN-propagating): gfx950 has it as one three-input
+// instruction (v_maximum3_f32) that needs no quieting of its inputs, which
+// fmaxf's NaN rule costs on values the compiler cannot prove canonical (the
+// masked scores).  Scores are finite or -inf here.
+__device__ __forceinline__ float max2f(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float max3f(float a, float b, float c) { return max2f(max2f(a, b), c); }
 
 }  // namespace
 
@@ -374,8 +379,13 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
             ld_off[k] = (uint32_t)(d * 128 + ((lane & 7) ^ ((d >> 1) & 7)) * 16);
         }
     }
-    auto issue_stage = [&](uint32_t r) {
-        char* sb = lds + (r % STAGES) * STAGEB;
+    auto issue_stage = [&](uint32_t r) __attribute__((always_inline)) {
+        // the slot offset passes through an empty asm so that the compiler
+        // derives the eight LDS destinations in the round (scalar adds)
+        // instead of keeping all of them live in SGPRs across the loop
+        uint32_t sb_off = (r % STAGES) * STAGEB;
+        asm volatile("" : "+s"(sb_off));
+        char* sb = lds + sb_off;
         if (k_wave) {
             const uint32_t kt = t0 + min(r, m - 1);
             const __amdgpu_buffer_rsrc_t rs = make_rsrc(kbase + (size_t)kt * KTILEB, (kv_len - kt * kTile) * KROWB);
@@ -431,13 +441,16 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
     constexpr int NPV = 2 * DTILES;      // V^T operands of one tile
     constexpr int NQK = 4 * KSTEPS;      // K operands of one tile
     constexpr int PREF = 6;
-    auto mfma_phase = [&](uint32_t r, auto pv_on, auto qk_on) {
+    // The stage slot is a compile-time constant (the round loop is unrolled
+    // by STAGES), so it folds into the reads' immediate offsets and the
+    // per-lane addresses stay loop-invariant.
+    auto mfma_phase = [&](auto slot, auto pv_on, auto qk_on) __attribute__((always_inline)) {
         constexpr bool DO_PV = decltype(pv_on)::value;
         constexpr bool DO_QK = decltype(qk_on)::value;
         constexpr int B0 = DO_PV ? 0 : NPV;          // first operand index
         constexpr int B1 = DO_QK ? NPV + NQK : NPV;  // one past the last
         constexpr int N = B1 - B0;
-        const char* st = lds + (r % STAGES) * STAGEB;
+        const char* st = lds + decltype(slot)::value * STAGEB;
         // operand i: PV (i < NPV): half = i / DTILES, dt = i % DTILES;
         //            QK: ks = (i - NPV) / 4, mt = (i - NPV) % 4
         auto read = [&](int i) -> u32x4 {
@@ -498,7 +511,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
         __builtin_amdgcn_sched_group_barrier(0x008, TAIL, 0);
     };
     // softmax of tile t (scores in S) -> probabilities in P
-    auto softmax = [&](uint32_t t) {
+    auto softmax = [&](uint32_t t) __attribute__((always_inline)) {
         if (t * kTile + kTile - 1 > w_qpos_min) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
@@ -519,7 +532,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
             const float a2 = max3f(S[1][nt][2], S[1][nt][3], S[2][nt][0]);
             const float a3 = max3f(S[2][nt][1], S[2][nt][2], S[2][nt][3]);
             const float a4 = max3f(S[3][nt][0], S[3][nt][1], S[3][nt][2]);
-            lm[nt] = fmaxf(max3f(a0, a1, a2), max3f(a3, a4, S[3][nt][3]));
+            lm[nt] = max2f(max3f(a0, a1, a2), max3f(a3, a4, S[3][nt][3]));
             need |= lm[nt] > thr[nt];
         }
         if (__any(need)) {
@@ -570,7 +583,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
     }
     phase_barrier();
 
-    for (uint32_t r = 0; r <= m; ++r) {
+    auto round = [&](uint32_t r, auto slot) __attribute__((always_inline)) {
         // three stages: stage r+2 goes into the slot round r-1 read; two
         // stages: stage r+1 does
         const bool more = r + STAGES - 1 <= m;
@@ -581,7 +594,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
         // takes part in.  A wave that runs ahead into this phase while its
         // SIMD partner is still in softmax takes issue priority.
         __builtin_amdgcn_s_setprio(1);
-        if (r <= wave_m) mfma_phase(r, std::true_type{}, std::true_type{});
+        if (r <= wave_m) mfma_phase(slot, std::true_type{}, std::true_type{});
         __builtin_amdgcn_s_setprio(0);
         // stage r+1 complete; with three stages stage r+2 (issued above) may
         // still be in flight
@@ -591,6 +604,13 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
         // softmax phase of tile r (no LDS access: the next round's MFMA phase
         // needs no second barrier)
         if (r < wave_m) softmax(t0 + r);
+    };
+    // round r reads slot r % STAGES
+    for (uint32_t r = 0; r <= m; r += STAGES) {
+        round(r, std::integral_constant<int, 0>{});
+        if (r + 1 <= m) round(r + 1, std::integral_constant<int, 1>{});
+        if constexpr (STAGES == 3)
+            if (r + 2 <= m) round(r + 2, std::integral_constant<int, 2>{});
     }
 
     if (!wave_live) return;
