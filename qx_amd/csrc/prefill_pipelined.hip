@@ -45,7 +45,7 @@ namespace qxh {
 namespace {
 
 constexpr int kTile = 64;          // positions per K/V tile
-constexpr float kLazyBits = 8.0f;  // rescale when a max grows by more than 2^8
+constexpr float kLazyP = 256.0f;  // rescale when a max grows by more than 2^8 (a probability above 256)
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -76,6 +76,9 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 // masked scores).  Scores are finite or -inf here.
 __device__ __forceinline__ float max2f(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 __device__ __forceinline__ float max3f(float a, float b, float c) { return max2f(max2f(a, b), c); }
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ h2 max2h(h2 a, h2 b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ h2 max3h(h2 a, h2 b, h2 c) { return max2h(max2h(a, b), c); }
 
 }  // namespace
 
@@ -417,9 +420,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     const float c = a.scale_log2;
-    const float lazy_raw = kLazyBits / c;       // threshold in raw q.k units
     float mrun[2] = {-1.0e30f, -1.0e30f};       // running max of raw q.k
-    float thr[2] = {-1.0e30f, -1.0e30f};        // rescale when a score exceeds this
     // Row sums ride on the matrix core: lacc[nt] += ones . P^T gives every
     // lane the full column sum (all four entries equal), so the sum sees the
     // same f16 probabilities as P.V and needs no VALU adds or lane reduction.
@@ -523,54 +524,68 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
                         if (t * kTile + 16 * mt + 4 * lg + j > qpos) S[mt][nt][j] = -INFINITY;
             }
         }
-        float lm[2];
-        bool need = false;
+        // Probabilities from the running max, three batches (scale/shift,
+        // exp2, f16 packing) kept apart so that no exp2 waits on the fma
+        // issued right before it.  The scores stay in S for the rare redo.
+        auto probs = [&]() __attribute__((always_inline)) {
+            const float moff[2] = {-mrun[0] * c, -mrun[1] * c};
+            float X[4][2][4];
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            const float a0 = max3f(S[0][nt][0], S[0][nt][1], S[0][nt][2]);
-            const float a1 = max3f(S[0][nt][3], S[1][nt][0], S[1][nt][1]);
-            const float a2 = max3f(S[1][nt][2], S[1][nt][3], S[2][nt][0]);
-            const float a3 = max3f(S[2][nt][1], S[2][nt][2], S[2][nt][3]);
-            const float a4 = max3f(S[3][nt][0], S[3][nt][1], S[3][nt][2]);
-            lm[nt] = max2f(max3f(a0, a1, a2), max3f(a3, a4, S[3][nt][3]));
-            need |= lm[nt] > thr[nt];
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) X[mt][nt][j] = __builtin_fmaf(S[mt][nt][j], c, moff[nt]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) X[mt][nt][j] = fast_exp2(X[mt][nt][j]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int half = 0; half < 2; ++half)
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) P[half][nt][k] = (_Float16)X[2 * half + (k >> 2)][nt][k & 3];
+        };
+        probs();
+        // Lazy rescale, decided on the packed probabilities: a score more
+        // than 2^8 above its column's running max leaves a probability
+        // above kLazyP (or inf; the first tile's -1e30 start always does).
+        // Eight packed three-input maxima cover all 32 probabilities of the
+        // lane, half the instructions of a max over the fp32 scores.
+        h2 v[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const hvec& src = P[q >> 3][(q >> 2) & 1];
+            v[q] = h2{src[2 * (q & 3)], src[2 * (q & 3) + 1]};
         }
+        const h2 r0 = max3h(v[0], v[1], v[2]), r1 = max3h(v[3], v[4], v[5]), r2 = max3h(v[6], v[7], v[8]);
+        const h2 r3 = max3h(v[9], v[10], v[11]), r4 = max3h(v[12], v[13], v[14]);
+        const h2 pr = max3h(max3h(r0, r1, r2), r3, max2h(r4, v[15]));
+        const bool need = pr[0] > (_Float16)kLazyP || pr[1] > (_Float16)kLazyP;
         if (__any(need)) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
-                const float m = max_xor32(max_xor16(lm[nt]));
+                const float a0 = max3f(S[0][nt][0], S[0][nt][1], S[0][nt][2]);
+                const float a1 = max3f(S[0][nt][3], S[1][nt][0], S[1][nt][1]);
+                const float a2 = max3f(S[1][nt][2], S[1][nt][3], S[2][nt][0]);
+                const float a3 = max3f(S[2][nt][1], S[2][nt][2], S[2][nt][3]);
+                const float a4 = max3f(S[3][nt][0], S[3][nt][1], S[3][nt][2]);
+                const float lm = max2f(max3f(a0, a1, a2), max3f(a3, a4, S[3][nt][3]));
+                const float m = max_xor32(max_xor16(lm));
                 const float mnew = fmaxf(mrun[nt], m);
                 const float alpha = fast_exp2((mrun[nt] - mnew) * c);
                 mrun[nt] = mnew;
-                thr[nt] = mnew + lazy_raw;
                 lacc[nt] *= alpha;
 #pragma unroll
                 for (int dt = 0; dt < DTILES; ++dt) oacc[dt][nt] *= alpha;
             }
+            probs();
         }
-        // Three batches (scale/shift, exp2, f16 packing), kept apart so that
-        // no exp2 waits on the fma issued right before it.
-        const float moff[2] = {-mrun[0] * c, -mrun[1] * c};
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) S[mt][nt][j] = __builtin_fmaf(S[mt][nt][j], c, moff[nt]);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) S[mt][nt][j] = fast_exp2(S[mt][nt][j]);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int half = 0; half < 2; ++half)
-#pragma unroll
-                for (int k = 0; k < 8; ++k) P[half][nt][k] = (_Float16)S[2 * half + (k >> 2)][nt][k & 3];
     };
 
     // prologue: stage 0 complete (and stage 1 in flight with three stages)
