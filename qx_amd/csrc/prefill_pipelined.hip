@@ -677,7 +677,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
 // merge of split-KV partials: out = sum_c O_c 2^(m_c - M) / sum_c l_c 2^(m_c - M)
 // grid (Hkv * qblocks, 32 NW / CPB), block 256 = CPB columns x D/4 threads
 // ---------------------------------------------------------------------------
-constexpr int kMaxPipeChunks = 4;
+constexpr int kMaxPipeChunks = 2;
 
 template <int D, int HEADS_PER_WAVE, int NW>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillPipeArgs a) {
@@ -748,22 +748,30 @@ static int pipe_waves(const ShapeDims& s) { return s.head_dim == 128 ? 8 : 4; }
 static uint32_t pipe_tokens_per_wg(const ShapeDims& s) { return s.head_dim == 128 ? 32 : 16 * pipe_waves(s); }
 static uint32_t pipe_columns(const ShapeDims& s) { return 32 * pipe_waves(s); }
 
-// Fewer query blocks than this split their KV ranges (at most
-// kMaxPipeChunks chunks) so that short prompts still fill the CUs.
+// Granite prompts with fewer query blocks than this split each block's KV
+// range into at most kMaxPipeChunks chunks of at least kMinChunkTiles tiles,
+// merged by prefill_combine_kernel, so that the longest block's chain of
+// rounds halves.  Measured (Granite f16, us per prefill, no split / two
+// chunks of >= 4 tiles / four chunks): T=512 12.9 / 14.3 / 14.4, T=1024
+// 19.5 / 18.1 / 22.2, T=2048 32.8 / 32.3 / 35.3.  Qwen never splits: with 8
+// query heads per kv head a block's partials (256 columns x 128 floats per
+// chunk) outweigh the K/V tiles they summarise (T=1024: 32.3 us unsplit
+// against 42.9 with two chunks and 46.6 with four; T=2048: 58.6 / 76.5 / 90).
 constexpr uint32_t kSplitBelowWgs = 512;
+constexpr uint32_t kMinChunkTiles = 8;
 
 static bool pipe_split_possible(const ShapeDims& s, uint32_t tokens) {
     const uint32_t wgt = pipe_tokens_per_wg(s);
-    return (uint64_t)(tokens + wgt - 1) / wgt * s.kv_heads < kSplitBelowWgs;
+    return s.group < 8 && (uint64_t)(tokens + wgt - 1) / wgt * s.kv_heads < kSplitBelowWgs;
 }
 
-// Chunk size in tiles: a quarter of the longest block's range (at least 4
-// tiles), so no block has more than kMaxPipeChunks chunks.
+// Chunk size in tiles: half the longest block's range, at least
+// kMinChunkTiles (a shorter chunk does not pay for the merge).
 static uint32_t pipe_chunk_tiles(const ShapeDims& s, uint32_t start, uint32_t tokens) {
     if (!pipe_split_possible(s, tokens)) return 0;
     const uint32_t n_max = (start + tokens + kTile - 1) / kTile;
     const uint32_t q = (n_max + kMaxPipeChunks - 1) / kMaxPipeChunks;
-    return q < 4 ? 4 : q;
+    return q < kMinChunkTiles ? kMinChunkTiles : q;
 }
 
 static uint64_t pipe_part_bytes(const ShapeDims& s, uint32_t tokens) {
@@ -856,8 +864,7 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
     if (chunks > 1) {
         const uint32_t cpb = 256 / (s.head_dim / 4);
         dim3 cgrid(a.qblocks * s.kv_heads, pipe_columns(s) / cpb);
-        if (s.head_dim == 128) hipLaunchKernelGGL((prefill_combine_kernel<128, 1, 8>), cgrid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((prefill_combine_kernel<64, 2, 4>), cgrid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((prefill_combine_kernel<64, 2, 4>), cgrid, dim3(256), 0, st, a);  // Granite only
         *dispatches = 3;
     }
     return hipGetLastError();
