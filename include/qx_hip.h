@@ -343,15 +343,19 @@ QXH_API int32_t qxh_encode_attention_for_layer_no_alloc(qxh_graph* graph, qxh_kv
  * The reference runs prompts as repeated decode (crates/qx-runtime/src/lib.rs:1341-1353);
  * its K-wide verifier attention (encode_attention_batch_with_plan,
  * crates/qx-metal/src/lib.rs:8206-8267) is the multi-query counterpart.
- * fp16/bf16 caches run on MFMA with fp32 accumulation; P.V runs in f16.  For
- * tokens >= 64 the call first rewrites the layer's V rows [0, start_position +
- * tokens) into an f16 V^T scratch inside `workspace`, then runs the pipelined
- * MFMA kernel; shorter calls (K-wide verifier) use a single-pass kernel.  For
- * bf16 caches, rows that reach a V value outside the f16 range are recomputed
- * by an exact bf16 pass.  `workspace` must hold qxh_prefill_workspace_bytes:
- * for tokens >= 64 that is kv_heads x capacity (rounded up to 64) x head_dim x
- * 2 bytes plus per-tile flags, for any start_position; for shorter bf16 calls
- * it is the per-workgroup flags; zero for shorter fp16 calls. */
+ * fp16/bf16 caches run on MFMA with fp32 accumulation.  A call of a few rows
+ * (up to 8, or while rows x context is small: the K-wide verifier) runs each
+ * row as a causal decode, split over the context like qxh_encode_attention.
+ * Longer calls first rewrite the layer's V rows [0, start_position + tokens)
+ * into an f16 V^T scratch inside `workspace`, then run the pipelined MFMA
+ * kernel (P.V in f16), splitting the KV range of each query block over the
+ * CUs when there are few blocks.  For bf16 caches, rows that reach a V value
+ * outside the f16 range are recomputed by an exact bf16 pass.  fp32 and mixed
+ * caches always run causal decode rows.  `workspace` must hold
+ * qxh_prefill_workspace_bytes, which covers every start_position: for the
+ * pipelined kernel kv_heads x capacity (rounded up to 64) x head_dim x 2 bytes
+ * plus per-tile flags and the split partials, for decode rows the split
+ * partials of every row. */
 QXH_API int32_t qxh_prefill_workspace_bytes(const qxh_kv_cache* cache, uint32_t tokens, uint64_t* bytes);
 QXH_API int32_t qxh_encode_prefill_attention(qxh_graph* graph, qxh_kv_cache* cache, uint32_t layer, uint32_t sequence,
                                      uint32_t start_position, uint32_t tokens, const void* query,

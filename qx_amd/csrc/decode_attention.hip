@@ -43,7 +43,8 @@ struct DecodeArgs {
     int query_dtype;
     int out_dtype;
     float qscale;          // softmax scale * log2(e)
-    // causal rows (VALU kernel only): when set, blockIdx.z is query row t of
+    // causal rows (VALU kernel, and the MFMA kernel for equal 16-bit caches
+    // without tiered values): when set, blockIdx.z is query row t of
     // one sequence (seq_stride 0) and row t attends [0, min(length, causal_start + t + 1))
     uint32_t causal;
     uint32_t causal_start;
@@ -565,8 +566,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
     const int lg = lane >> 4, li = lane & 15;
     const uint32_t split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
     const uint32_t hkv = gridDim.y;
+    // causal rows: blockIdx.z is query row t, attending [0, causal_start + t + 1)
+    const uint32_t length = a.causal ? min(a.length, a.causal_start + seq + 1) : a.length;
     const uint32_t r0 = split * a.chunk;
-    const uint32_t r1 = min(a.length, r0 + a.chunk);
+    const uint32_t r1 = min(length, r0 + a.chunk);
     const uint32_t span = r1 > r0 ? r1 - r0 : 0u;
     const uint32_t wspan = ((span + WAVES - 1) / WAVES + 31) / 32 * 32;
     const uint32_t w0 = r0 + wave * wspan;
@@ -868,7 +871,7 @@ static bool valu_path(int key_dtype, int value_dtype) { return key_dtype == F32 
 
 // Tiered values with 16-bit keys on the Qwen shape (G = 8) decode on the MFMA
 // kernel, where the VALU kernel's eight per-row dot reductions make it
-// compute-bound; causal rows and fp32 keys stay on the VALU kernel.
+// compute-bound; their causal rows and fp32 keys stay on the VALU kernel.
 static bool tiered_on_mfma(const ShapeDims& s, int key_dtype, int value_dtype) {
     return value_dtype == I8T && key_dtype != F32 && s.group >= 8;
 }
@@ -977,7 +980,6 @@ static hipError_t launch_decode_impl(const ShapeDims& s, const KvLayer& kv, cons
     const int kd = kv.key_dtype, vd = kv.value_dtype;
     const dim3 block(64 * kWaves);
     if (!decode_dtypes_supported(s, kd, vd)) return hipErrorNotSupported;
-    if (a.causal && !valu_path(kd, vd)) return hipErrorNotSupported;
     if (s.head_dim == 64 && s.group == 2) {
         if (kd == vd && kd == F32) launch_valu<64, 2, F32, F32>(a, grid, st);
         else if (kd == vd && kd == F16) hipLaunchKernelGGL((decode_mfma_kernel<64, 2, F16, kWaves>), grid, block, 0, st, a);

@@ -133,7 +133,7 @@ DecodePlan plan_block_decode(const ShapeDims& s, int key_dtype, int value_dtype,
 hipError_t launch_block_decode_attention(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t length,
                                          const float* query, float* out, void* workspace, hipStream_t st);
 // pipelined path (prefill_pipelined.hip): V^T pre-pass + pipelined MFMA kernel
-bool prefill_pipe_supported(const ShapeDims& s, uint32_t tokens);
+bool prefill_pipe_supported(const ShapeDims& s);
 uint32_t prefill_pipe_vt_tiles(uint32_t capacity);
 uint64_t prefill_pipe_workspace_bytes(const ShapeDims& s, uint32_t capacity, uint32_t tokens);
 hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t start, uint32_t tokens, const void* query,

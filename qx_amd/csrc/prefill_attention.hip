@@ -1,14 +1,8 @@
-// Causal prefill attention on gfx950 MFMA: the kernels over prefill_rows
-// (prefill_rows.h) and the routing of every prefill call.
+// Causal prefill attention: the routing of every prefill call, and the exact
+// pass over prefill_rows (prefill_rows.h) behind the pipelined kernel.
 #include "prefill_rows.h"
 
 namespace qxh {
-
-template <int D, int DT, int HW, int QW, bool EXACT>
-__global__ __launch_bounds__(512, 1) void prefill_attention_kernel(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) char lds[prefill_rows_lds_bytes<D>()];
-    prefill_rows<D, DT, HW, QW, EXACT>(a, lds, blockIdx.x, blockIdx.z, blockIdx.x + gridDim.x * blockIdx.z);
-}
 
 // The exact pass after the pipelined kernel (bf16 caches), a few workgroups
 // walking the query blocks.  Usually no V value is outside the f16 range:
@@ -24,7 +18,7 @@ __global__ __launch_bounds__(512, 1) void prefill_exact_pass_kernel(PrefillArgs 
         any |= a.tile_flags[(size_t)(i / tiles) * a.tile_flag_stride + i % tiles] != 0;
     if (!__syncthreads_or(any)) return;
     for (uint32_t b = blockIdx.x; b < blocks; b += gridDim.x) {
-        prefill_rows<D, BF16, HW, QW, true>(a, lds, b, 0, b);
+        prefill_rows<D, HW, QW>(a, lds, b);
         __syncthreads();  // the next block overwrites the LDS tiles
     }
 }
@@ -32,51 +26,69 @@ __global__ __launch_bounds__(512, 1) void prefill_exact_pass_kernel(PrefillArgs 
 // workgroups of the exact pass after the pipelined kernel: one per CU at most
 constexpr uint32_t kExactPassWgs = 256;
 
-// fp32 and mixed K/V caches run causal rows on the decode kernels (every query
-// row streams its own prefix: fine for the K <= 4 verifier rows, quadratic in
-// bytes for long prefills); equal 16-bit dtypes take the MFMA prefill.
-static bool prefill_on_decode(const KvLayer& kv) { return kv.key_dtype == F32 || kv.key_dtype != kv.value_dtype; }
+// Causal rows on the split-K decode kernels, for fp32 and mixed K/V caches
+// and for short prompts on any cache: every query row streams its own
+// prefix, split over the CUs like a decode.  That is quadratic in bytes for
+// long prompts but has no fixed cost beyond a decode's, while the pipelined
+// MFMA prefill (equal 16-bit K/V) first rewrites the layer's whole V prefix
+// into the f16 V^T scratch.  Measured per call (us; causal rows / pipelined):
+// Qwen bf16 at 1020 cached positions 14 / 31 for 1-8 rows, 31 / 32 for 63;
+// at 8188, 42 / 56 for 16 rows; at 32764, 19 / 71 for one row, 71 / 71 for 8,
+// 142 / 69 for 16.  Granite f16 at 3840: 18 / 17 for 16 rows, 48 / 20 for 63.
+// Rows run on the decode kernels up to 8 of them, or while rows x context
+// stays under the measured crossover (about 150000 for Qwen, 40000 for
+// Granite, whose rows are cheaper per position than its pipelined call).
+// The former short-prompt kernel, one 8-head workgroup per kv head, took
+// 1.31 ms for 1-16 rows at 32764 Qwen positions.
+constexpr uint32_t kDecodeRowsAlways = 8;
+static uint64_t decode_rows_budget(const ShapeDims& s) { return s.group >= 8 ? 150000u : 40000u; }
 
-// Tiered values with 16-bit keys take the pipelined MFMA prefill (T >= 64),
-// its V^T pre-pass reading the tiers; the shorter verifier rows stay on the
-// decode kernels.
-static bool tiered_on_pipe(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t tokens) {
-    return value_dtype == I8T && key_dtype != F32 && prefill_pipe_supported(s, tokens);
+static bool rows_on_decode(const ShapeDims& s, uint32_t start, uint32_t tokens) {
+    return tokens <= kDecodeRowsAlways ||
+           (tokens < 64 && (uint64_t)tokens * (start + tokens) <= decode_rows_budget(s));
 }
 
+static bool prefill_on_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t start, uint32_t tokens) {
+    return key_dtype == F32 || key_dtype != value_dtype || !prefill_pipe_supported(s) || rows_on_decode(s, start, tokens);
+}
+
+// Tiered values with 16-bit keys take the pipelined MFMA prefill when the
+// rows would (its V^T pre-pass reading the tiers); the others stay on the
+// decode kernels.
+static bool tiered_on_pipe(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t start, uint32_t tokens) {
+    return value_dtype == I8T && key_dtype != F32 && prefill_pipe_supported(s) && !rows_on_decode(s, start, tokens);
+}
+
+// Covers every start position: below 64 rows a call may take either path.
 uint64_t prefill_workspace_bytes(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t capacity,
                                  uint32_t tokens) {
-    if (tiered_on_pipe(s, key_dtype, value_dtype, tokens)) return prefill_pipe_workspace_bytes(s, capacity, tokens);
-    if (key_dtype == F32 || key_dtype != value_dtype)
-        return decode_causal_workspace_bound(s, key_dtype, value_dtype, capacity, tokens);
-    const int kv_dtype = key_dtype;
-    if (prefill_pipe_supported(s, tokens)) return prefill_pipe_workspace_bytes(s, capacity, tokens);
-    if (kv_dtype != BF16) return 0;
-    const uint32_t qb = s.head_dim == 64 ? (tokens + 127) / 128 : (tokens + 31) / 32;
-    return (uint64_t)qb * s.kv_heads * sizeof(uint32_t);
+    const bool pipe_dtypes = key_dtype != F32 && (key_dtype == value_dtype || value_dtype == I8T) &&
+                             prefill_pipe_supported(s);
+    const uint64_t rows = decode_causal_workspace_bound(s, key_dtype, value_dtype, capacity, tokens);
+    if (!pipe_dtypes || tokens <= kDecodeRowsAlways) return rows;
+    const uint64_t pipe = prefill_pipe_workspace_bytes(s, capacity, tokens);
+    return tokens < 64 && rows > pipe ? rows : pipe;
 }
 
 hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint32_t start_position, uint32_t tokens,
                                     const void* query, int query_dtype, void* out, int out_dtype, void* workspace,
                                     hipStream_t st, int* dispatches) {
     *dispatches = 0;
-    if (tiered_on_pipe(s, kv.key_dtype, kv.value_dtype, tokens)) {
+    if (tiered_on_pipe(s, kv.key_dtype, kv.value_dtype, start_position, tokens)) {
         if (kv.key_dtype != query_dtype) return hipErrorNotSupported;
         return launch_prefill_pipe(s, kv, start_position, tokens, query, query_dtype, out, out_dtype, workspace, st,
                                    dispatches);
     }
-    if (prefill_on_decode(kv)) {
+    if (prefill_on_decode(s, kv.key_dtype, kv.value_dtype, start_position, tokens)) {
         const DecodePlan p = plan_decode_causal(s, kv.key_dtype, kv.value_dtype, start_position, tokens);
         return launch_decode_causal_rows(s, kv, p, start_position, tokens, query, query_dtype, out, out_dtype, workspace,
                                          st, dispatches);
     }
     if (kv.key_dtype != query_dtype) return hipErrorNotSupported;
-    const bool pp = prefill_pipe_supported(s, tokens);
-    if (pp) {
-        hipError_t e = launch_prefill_pipe(s, kv, start_position, tokens, query, query_dtype, out, out_dtype, workspace,
-                                         st, dispatches);
-        if (e != hipSuccess || query_dtype != BF16) return e;
-    }
+    hipError_t e = launch_prefill_pipe(s, kv, start_position, tokens, query, query_dtype, out, out_dtype, workspace, st,
+                                       dispatches);
+    if (e != hipSuccess || query_dtype != BF16) return e;
+    // bf16: the exact pass, for the rows the pipelined kernel left behind
     PrefillArgs a{};
     a.query = query;
     a.keys = kv.keys;
@@ -89,48 +101,25 @@ hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint3
     a.group = s.group;
     a.out_dtype = out_dtype;
     a.scale_log2 = s.scale * kLog2e;
-    a.flags = reinterpret_cast<uint32_t*>(workspace);
     a.kv_heads = s.kv_heads;
-    if (pp) {
-        // exact pass only, for the rows the pipelined kernel left behind
-        a.tile_flags = reinterpret_cast<const uint32_t*>(workspace);
-        a.tile_flag_stride = prefill_pipe_vt_tiles(kv.capacity);
-    }
-    const bool bf = query_dtype == BF16;
+    a.tile_flags = reinterpret_cast<const uint32_t*>(workspace);
+    a.tile_flag_stride = prefill_pipe_vt_tiles(kv.capacity);
     if (s.head_dim == 64 && s.group == 2) {
         a.qblocks = (tokens + 127) / 128;
         a.xcd_map = (8 % s.kv_heads == 0) && ((uint64_t)a.qblocks * s.kv_heads) % 8 == 0;
-        dim3 grid(a.qblocks * s.kv_heads, 1, 1);
-        if (!bf) {
-            hipLaunchKernelGGL((prefill_attention_kernel<64, F16, 2, 4, false>), grid, dim3(512), 0, st, a);
-        } else {
-            if (pp) {
-                const uint32_t wgs = grid.x < kExactPassWgs ? grid.x : kExactPassWgs;
-                hipLaunchKernelGGL((prefill_exact_pass_kernel<64, 2, 4>), dim3(wgs), dim3(512), 0, st, a, grid.x);
-            } else {
-                hipLaunchKernelGGL((prefill_attention_kernel<64, BF16, 2, 4, false>), grid, dim3(512), 0, st, a);
-                hipLaunchKernelGGL((prefill_attention_kernel<64, BF16, 2, 4, true>), grid, dim3(512), 0, st, a);
-            }
-        }
+        const uint32_t blocks = a.qblocks * s.kv_heads;
+        hipLaunchKernelGGL((prefill_exact_pass_kernel<64, 2, 4>), dim3(blocks < kExactPassWgs ? blocks : kExactPassWgs),
+                           dim3(512), 0, st, a, blocks);
     } else if (s.head_dim == 128 && s.group == 8) {
         a.qblocks = (tokens + 31) / 32;
         a.xcd_map = (8 % s.kv_heads == 0) && ((uint64_t)a.qblocks * s.kv_heads) % 8 == 0;
-        dim3 grid(a.qblocks * s.kv_heads, 1, 1);
-        if (!bf) {
-            hipLaunchKernelGGL((prefill_attention_kernel<128, F16, 8, 1, false>), grid, dim3(512), 0, st, a);
-        } else {
-            if (pp) {
-                const uint32_t wgs = grid.x < kExactPassWgs ? grid.x : kExactPassWgs;
-                hipLaunchKernelGGL((prefill_exact_pass_kernel<128, 8, 1>), dim3(wgs), dim3(512), 0, st, a, grid.x);
-            } else {
-                hipLaunchKernelGGL((prefill_attention_kernel<128, BF16, 8, 1, false>), grid, dim3(512), 0, st, a);
-                hipLaunchKernelGGL((prefill_attention_kernel<128, BF16, 8, 1, true>), grid, dim3(512), 0, st, a);
-            }
-        }
+        const uint32_t blocks = a.qblocks * s.kv_heads;
+        hipLaunchKernelGGL((prefill_exact_pass_kernel<128, 8, 1>), dim3(blocks < kExactPassWgs ? blocks : kExactPassWgs),
+                           dim3(512), 0, st, a, blocks);
     } else {
         return hipErrorNotSupported;
     }
-    *dispatches += bf ? (pp ? 1 : 2) : 1;
+    *dispatches += 1;
     return hipGetLastError();
 }
 

@@ -677,7 +677,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
 // merge of split-KV partials: out = sum_c O_c 2^(m_c - M) / sum_c l_c 2^(m_c - M)
 // grid (Hkv * qblocks, 32 NW / CPB), block 256 = CPB columns x D/4 threads
 // ---------------------------------------------------------------------------
-constexpr int kMaxPipeChunks = 2;
+constexpr uint32_t kMaxPipeChunks = 32;
 
 template <int D, int HEADS_PER_WAVE, int NW>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillPipeArgs a) {
@@ -695,10 +695,12 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillPipeArgs a)
     if (nchunks <= 1) return;  // written directly by the attention kernel
     if (a.flags) {
         // the attention kernel wrote no partials for a block that reaches a
-        // flagged tile: the exact pass owns its rows
+        // flagged tile: the exact pass owns its rows (the test is uniform over
+        // the workgroup: every wave reads the same flags)
         const uint32_t* f = a.flags + (size_t)kvh * a.vt_tiles;
-        for (uint32_t i = 0; i < n; ++i)
-            if (f[i]) return;
+        bool bad = false;
+        for (uint32_t i = threadIdx.x & 63; i < n; i += 64) bad |= f[i] != 0;
+        if (__any(bad)) return;
     }
     const int col = blockIdx.y * CPB + threadIdx.x / D4, d4 = threadIdx.x % D4;
     uint32_t tok;
@@ -706,30 +708,36 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillPipeArgs a)
     pipe_column<HEADS_PER_WAVE, NW>(col, wg_t0, kvh, a.group, tok, head);
     if (tok >= T) return;
     const size_t slot = ((size_t)kvh * nqb + qblock) * a.max_chunks * COLS + col;
-    float mc[kMaxPipeChunks], lc[kMaxPipeChunks];
-    f32x4 oc[kMaxPipeChunks];
-#pragma unroll
-    for (int k = 0; k < kMaxPipeChunks; ++k) {
-        mc[k] = -1.0e30f;
-        lc[k] = 0.0f;
-        oc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if ((uint32_t)k < nchunks) {
-            const size_t cx = slot + (size_t)k * COLS;
-            mc[k] = a.part_ml[2 * cx];
-            lc[k] = a.part_ml[2 * cx + 1];
-            oc[k] = *reinterpret_cast<const f32x4*>(a.part_o + cx * D + 4 * d4);
-        }
-    }
-    float M = mc[0];
-#pragma unroll
-    for (int k = 1; k < kMaxPipeChunks; ++k) M = fmaxf(M, mc[k]);
-    float L = 0.0f;
+    // chunks in batches of four loads in flight, folded into a running
+    // (M, L, O) at each batch's max
+    float M = -1.0e30f, L = 0.0f;
     f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t k0 = 0; k0 < nchunks; k0 += 4) {
+        float mc[4], lc[4];
+        f32x4 oc[4];
 #pragma unroll
-    for (int k = 0; k < kMaxPipeChunks; ++k) {
-        const float f = fast_exp2(mc[k] - M);
-        L = __builtin_fmaf(lc[k], f, L);
-        O += oc[k] * f;
+        for (int k = 0; k < 4; ++k) {
+            mc[k] = -1.0e30f;
+            lc[k] = 0.0f;
+            oc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (k0 + k < nchunks) {
+                const size_t cx = slot + (size_t)(k0 + k) * COLS;
+                mc[k] = a.part_ml[2 * cx];
+                lc[k] = a.part_ml[2 * cx + 1];
+                oc[k] = *reinterpret_cast<const f32x4*>(a.part_o + cx * D + 4 * d4);
+            }
+        }
+        const float Mn = fmaxf(fmaxf(M, fmaxf(mc[0], mc[1])), fmaxf(mc[2], mc[3]));
+        const float f0 = fast_exp2(M - Mn);
+        L *= f0;
+        O *= f0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float f = fast_exp2(mc[k] - Mn);
+            L = __builtin_fmaf(lc[k], f, L);
+            O += oc[k] * f;
+        }
+        M = Mn;
     }
     const float inv = 1.0f / L;
     const size_t obase = ((size_t)tok * a.q_heads + head) * D + 4 * d4;
@@ -748,36 +756,50 @@ static int pipe_waves(const ShapeDims& s) { return s.head_dim == 128 ? 8 : 4; }
 static uint32_t pipe_tokens_per_wg(const ShapeDims& s) { return s.head_dim == 128 ? 32 : 16 * pipe_waves(s); }
 static uint32_t pipe_columns(const ShapeDims& s) { return 32 * pipe_waves(s); }
 
-// Granite prompts with fewer query blocks than this split each block's KV
-// range into at most kMaxPipeChunks chunks of at least kMinChunkTiles tiles,
-// merged by prefill_combine_kernel, so that the longest block's chain of
-// rounds halves.  Measured (Granite f16, us per prefill, no split / two
-// chunks of >= 4 tiles / four chunks): T=512 12.9 / 14.3 / 14.4, T=1024
-// 19.5 / 18.1 / 22.2, T=2048 32.8 / 32.3 / 35.3.  Qwen never splits: with 8
-// query heads per kv head a block's partials (256 columns x 128 floats per
-// chunk) outweigh the K/V tiles they summarise (T=1024: 32.3 us unsplit
-// against 42.9 with two chunks and 46.6 with four; T=2048: 58.6 / 76.5 / 90).
-constexpr uint32_t kSplitBelowWgs = 512;
-constexpr uint32_t kMinChunkTiles = 8;
+// Split KV.  A prompt whose query blocks leave CUs idle (fewer workgroups
+// than kTargetWgs) splits each block's KV range into chunks of at least
+// min_chunk_tiles(s) tiles, as many as fill kTargetWgs (at most
+// kMaxPipeChunks); prefill_combine_kernel merges the chunks' partials.  The
+// chunk floor keeps a block's partials (per query column: m, l and D floats;
+// 256 columns for Qwen, 128 for Granite) small next to the K/V tiles a chunk
+// reads: 8 tiles for Granite, 32 for Qwen, whose 8 query heads per kv head
+// make its partials 8 times larger per tile.  Measured at start 0 (us per
+// prefill; no split / two chunks / four chunks): Granite f16 T=512 12.9 /
+// 14.3 / 14.4, T=1024 19.5 / 18.1 / 22.2, T=2048 32.8 / 32.3 / 35.3; Qwen bf16
+// T=1024 32.3 / 42.9 / 46.6, T=2048 58.6 / 76.5 / 90.  Long contexts are where
+// splitting pays: a 64-token Qwen prompt over 32704 cached positions is 16
+// workgroups of 513 rounds each without it.
+constexpr uint32_t kTargetWgs = 512;
+static uint32_t pipe_wgs_per_block(const ShapeDims& s) { return s.head_dim == 128 ? 2u : 1u; }
+static uint32_t min_chunk_tiles(const ShapeDims& s) { return s.head_dim == 128 ? 32u : 8u; }
 
-static bool pipe_split_possible(const ShapeDims& s, uint32_t tokens) {
+static uint32_t pipe_blocks(const ShapeDims& s, uint32_t tokens) {
     const uint32_t wgt = pipe_tokens_per_wg(s);
-    return s.group < 8 && (uint64_t)(tokens + wgt - 1) / wgt * s.kv_heads < kSplitBelowWgs;
+    return (tokens + wgt - 1) / wgt * s.kv_heads;
 }
 
-// Chunk size in tiles: half the longest block's range, at least
-// kMinChunkTiles (a shorter chunk does not pay for the merge).
+// most chunks a block of a `tokens`-row prompt can take, whatever its start
+static uint32_t pipe_max_chunks(const ShapeDims& s, uint32_t tokens) {
+    const uint64_t wgs = (uint64_t)pipe_blocks(s, tokens) * pipe_wgs_per_block(s);
+    if (wgs >= kTargetWgs) return 1;
+    const uint32_t want = (uint32_t)((kTargetWgs + wgs - 1) / wgs);
+    return want < kMaxPipeChunks ? want : kMaxPipeChunks;
+}
+
+// Chunk size in tiles for this call, 0 for no split.
 static uint32_t pipe_chunk_tiles(const ShapeDims& s, uint32_t start, uint32_t tokens) {
-    if (!pipe_split_possible(s, tokens)) return 0;
+    const uint32_t want = pipe_max_chunks(s, tokens);
     const uint32_t n_max = (start + tokens + kTile - 1) / kTile;
-    const uint32_t q = (n_max + kMaxPipeChunks - 1) / kMaxPipeChunks;
-    return q < kMinChunkTiles ? kMinChunkTiles : q;
+    const uint32_t fit = n_max / min_chunk_tiles(s);
+    const uint32_t chunks = want < fit ? want : fit;
+    if (chunks <= 1) return 0;
+    return (n_max + chunks - 1) / chunks;
 }
 
 static uint64_t pipe_part_bytes(const ShapeDims& s, uint32_t tokens) {
-    if (!pipe_split_possible(s, tokens)) return 0;
-    const uint64_t slots = (uint64_t)(tokens + pipe_tokens_per_wg(s) - 1) / pipe_tokens_per_wg(s) * s.kv_heads *
-                           kMaxPipeChunks * pipe_columns(s);
+    const uint32_t mc = pipe_max_chunks(s, tokens);
+    if (mc <= 1) return 0;
+    const uint64_t slots = (uint64_t)pipe_blocks(s, tokens) * mc * pipe_columns(s);
     return slots * 2 * 4 + slots * s.head_dim * 4;
 }
 
@@ -791,8 +813,8 @@ uint64_t prefill_pipe_workspace_bytes(const ShapeDims& s, uint32_t capacity, uin
     return pipe_flag_bytes(s, tiles) + (uint64_t)s.kv_heads * tiles * s.head_dim * kTile * 2 + pipe_part_bytes(s, tokens);
 }
 
-bool prefill_pipe_supported(const ShapeDims& s, uint32_t tokens) {
-    return tokens >= kTile && ((s.head_dim == 128 && s.group == 8) || (s.head_dim == 64 && s.group == 2));
+bool prefill_pipe_supported(const ShapeDims& s) {
+    return (s.head_dim == 128 && s.group == 8) || (s.head_dim == 64 && s.group == 2);
 }
 
 hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t start, uint32_t tokens, const void* query,
@@ -843,11 +865,11 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
     a.kv_heads = s.kv_heads;
     const uint32_t wgt = pipe_tokens_per_wg(s);
     a.qblocks = (tokens + wgt - 1) / wgt;
-    const uint32_t halves = s.head_dim == 128 ? 2u : 1u;  // Qwen: two 4-wave workgroups per query block
+    const uint32_t halves = pipe_wgs_per_block(s);  // Qwen: two 4-wave workgroups per query block
     a.xcd_map = (8 % s.kv_heads == 0) && ((uint64_t)a.qblocks * s.kv_heads * halves) % 8 == 0;
     a.chunk_tiles = pipe_chunk_tiles(s, start, tokens);
-    a.max_chunks = kMaxPipeChunks;
-    const uint64_t slots = (uint64_t)a.qblocks * s.kv_heads * kMaxPipeChunks * pipe_columns(s);
+    a.max_chunks = pipe_max_chunks(s, tokens);
+    const uint64_t slots = (uint64_t)a.qblocks * s.kv_heads * a.max_chunks * pipe_columns(s);
     a.part_ml = reinterpret_cast<float*>(parts);
     a.part_o = a.part_ml + 2 * slots;
     // chunks of the longest block (the last one; with start it is the longest)
@@ -864,7 +886,8 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
     if (chunks > 1) {
         const uint32_t cpb = 256 / (s.head_dim / 4);
         dim3 cgrid(a.qblocks * s.kv_heads, pipe_columns(s) / cpb);
-        hipLaunchKernelGGL((prefill_combine_kernel<64, 2, 4>), cgrid, dim3(256), 0, st, a);  // Granite only
+        if (s.head_dim == 128) hipLaunchKernelGGL((prefill_combine_kernel<128, 1, 8>), cgrid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((prefill_combine_kernel<64, 2, 4>), cgrid, dim3(256), 0, st, a);
         *dispatches = 3;
     }
     return hipGetLastError();

@@ -1,4 +1,4 @@
-// Causal prefill attention on gfx950 MFMA (v_mfma_f32_16x16x32_{f16,bf16},
+// The exact bf16 causal prefill rows on gfx950 MFMA (v_mfma_f32_16x16x32_bf16,
 // fp32 accumulate), FlashAttention-2 style with the transposed formulation:
 //
 //   S^T[pos][q] = K[pos][:] . Q^T[:][q]      A = K tile (LDS), B = Q^T (registers)
@@ -13,28 +13,22 @@
 // position map is the same for both operands, so the contraction is exact
 // whatever the hardware's internal k order is.
 //
+// This is the exact pass behind the pipelined prefill: the pipelined kernel
+// runs P.V in f16 on an f16 copy of V, and a query block whose rows reach a
+// 64-position tile holding a bf16 value outside the f16 range is left to this
+// body, which keeps V in bf16 and splits P into bf16 hi + lo parts (together
+// they reproduce p to ~2^-16; rounding P to bf16 alone would cost ~7e-3 of
+// output RMS).
+//
 // Work decomposition: a workgroup of 8 waves shares one K/V head.  Each wave
 // owns 32 queries (two 16-column blocks) of one query head; the workgroup
 // covers HW heads of the GQA group x QW query blocks (Qwen: the 8 heads of a
 // group; Granite: 2 heads x 4 query blocks).  K/V tiles of 64 positions are
 // staged through double-buffered, padded LDS by all 512 threads, with the
-// global loads of tile t+2 in flight while tile t is consumed.  Tiles above the causal diagonal are never
-// loaded; the diagonal tile is masked per element.  Query blocks are issued
-// last-first so the longest rows start first.
-//
-// Precision of P.V: rounding the probabilities to bf16 would cost ~7e-3 of
-// output RMS, so P.V always runs in f16 (P to f16 costs ~8e-4).  bf16 value
-// tiles are converted to f16 while they are staged into LDS (exact inside the
-// f16 range).  A tile holding any value outside that range is voted at the
-// staging barrier; such a workgroup records a flag and leaves its rows to a
-// second, exact pass (EXACT = true) that keeps V in bf16 and splits P into
-// bf16 hi + lo parts.  The exact kernel's other workgroups exit at once.
-//
-// The body is a device function (prefill_rows) so that the pipelined kernel
-// can run the exact pass itself on the workgroups that need it.
+// global loads of tile t+2 in flight while tile t is consumed.  Tiles above
+// the causal diagonal are never loaded; the diagonal tile is masked per
+// element.
 #pragma once
-
-#include <type_traits>
 
 #include "common.h"
 #include "internal.h"
@@ -54,12 +48,11 @@ struct PrefillArgs {
     int group;
     int out_dtype;
     float scale_log2;      // softmax scale * log2(e)
-    uint32_t* flags;       // per-workgroup "V outside the f16 range" votes (bf16 caches)
     uint32_t qblocks;      // query blocks per head
     uint32_t kv_heads;
     uint32_t xcd_map;      // 1: XCD-aware block -> (head, query block) mapping
-    // exact pass after the pipelined kernel: per-(kv head, 64-position tile)
-    // flags of the V^T pre-pass replace the per-workgroup votes
+    // per-(kv head, 64-position tile) flags of the pipelined kernel's V^T
+    // pre-pass: a value outside the f16 range
     const uint32_t* tile_flags;
     uint32_t tile_flag_stride;  // tiles per kv head
 };
@@ -76,23 +69,8 @@ __device__ __forceinline__ void interleave_mfma_valu() {
 
 // A running max may lag the true max by up to this many binary orders of
 // magnitude before the accumulators are rescaled; probabilities then stay
-// below 2^8, well inside the f16 range.
+// below 2^8.
 constexpr float kLazyRescale = 8.0f;
-
-// Convert 8 packed bf16 to 8 packed f16 (RNE; exact for |v| in the f16 normal
-// range).  Sets `ovf` when a value is not representable as a finite f16.
-__device__ __forceinline__ u32x4 bf16x8_to_f16x8(const u32x4& v, bool& ovf) {
-    u32x4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float lo = __uint_as_float(v[i] << 16);
-        const float hi = __uint_as_float(v[i] & 0xffff0000u);
-        ovf |= !(__builtin_fabsf(lo) <= 65504.0f) || !(__builtin_fabsf(hi) <= 65504.0f);
-        const _Float16 a = (_Float16)lo, b = (_Float16)hi;
-        r[i] = (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-    }
-    return r;
-}
 
 // LDS of prefill_rows<D, ...>: two padded K tiles, then two padded V tiles.
 template <int D>
@@ -100,21 +78,15 @@ constexpr int prefill_rows_lds_bytes() {
     return 2 * 64 * (D * 2 + 16) + 2 * 64 * (D * 2 + 32);
 }
 
-// The rows of one workgroup of 512 threads: `lin_block` is the linear block
-// index that the XCD-aware mapping reads (the x block index of a kernel of
-// this shape), `zblk` selects the head group (the z block index), `wg_id` the
-// workgroup's vote slot in a.flags.  `lds` holds prefill_rows_lds_bytes<D>()
-// bytes, 16-byte aligned.  Every thread of the workgroup must call it (it
-// synchronises).
-template <int D, int DT, int HW, int QW, bool EXACT>
-__device__ __forceinline__ void prefill_rows(const PrefillArgs& a, char* lds, uint32_t lin_block, uint32_t zblk,
-                                             uint32_t wg_id) {
-    using M = MfmaT<DT>;             // Q.K operands (the cache dtype)
-    using MH = MfmaT<F16>;           // P.V operands: f16 probabilities and f16 values
+// The rows of one query block (block index `lin_block`, which the XCD-aware
+// mapping reads), in a workgroup of 512 threads.  The block returns at once
+// unless one of the tiles its rows reach is flagged.  `lds` holds
+// prefill_rows_lds_bytes<D>() bytes, 16-byte aligned.  Every thread of the
+// workgroup must call it (it synchronises).
+template <int D, int HW, int QW>
+__device__ __forceinline__ void prefill_rows(const PrefillArgs& a, char* lds, uint32_t lin_block) {
+    using M = MfmaT<BF16>;           // Q.K and P.V operands: bf16
     using vec = typename M::vec;
-    using hvec = typename MH::vec;
-    // probability operand: f16 on the fast pass, the cache dtype on the exact pass
-    using pvec = typename std::conditional<EXACT, vec, hvec>::type;
     constexpr int WAVES = 8;
     constexpr int KSTEPS = D / 32;      // 32-dim k-steps of Q.K
     constexpr int DTILES = D / 16;      // 16-dim output tiles
@@ -129,16 +101,9 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs& a, char* lds, ui
     static_assert(CPT >= 1 && CPT * 64 * WAVES == 2 * CHUNKS, "tile staging must divide evenly");
 
     static_assert(2 * (KTILEB + VTILEB) == prefill_rows_lds_bytes<D>(), "LDS layout");
-    // K tile of buffer i at lds + i * KTILEB; V tile (f16 on the fast pass, the
-    // cache dtype on the exact pass) at lds + 2 * KTILEB + i * VTILEB
+    // K tile of buffer i at lds + i * KTILEB; V tile at lds + 2 * KTILEB + i * VTILEB
     auto lds_k = [&](int i) { return lds + i * KTILEB; };
     auto lds_v = [&](int i) { return lds + 2 * KTILEB + i * VTILEB; };
-
-    if constexpr (EXACT) {
-        // only workgroups whose fast pass met a V value outside the f16 range
-        // (no vote array: the caller already knows this workgroup needs it)
-        if (!a.tile_flags && a.flags && a.flags[wg_id] == 0) return;
-    }
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -163,7 +128,7 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs& a, char* lds, ui
         }
     }
     const int kvh = (int)kvh_u;
-    const int head = kvh * a.group + (int)zblk * HW + (wave % HW);
+    const int head = kvh * a.group + (wave % HW);
     const int qsub = wave / HW;
     const uint32_t qblock = nqb - 1 - qidx;  // longest rows first
     const uint32_t T = a.tokens;
@@ -177,15 +142,13 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs& a, char* lds, ui
     const uint32_t wave_tiles = (wave_kv + BN - 1) / BN;
     const float c = a.scale_log2;
 
-    if constexpr (EXACT) {
-        if (a.tile_flags) {
-            // rows of this workgroup reach tiles [0, ntiles); the pipelined
-            // kernel left them here iff one of those tiles is flagged
-            const uint32_t* f = a.tile_flags + (size_t)kvh * a.tile_flag_stride;
-            bool bad = false;
-            for (uint32_t i = lane; i < ntiles; i += 64) bad |= f[i] != 0;
-            if (!__syncthreads_or(bad)) return;
-        }
+    {
+        // rows of this workgroup reach tiles [0, ntiles); the pipelined
+        // kernel left them here iff one of those tiles is flagged
+        const uint32_t* f = a.tile_flags + (size_t)kvh * a.tile_flag_stride;
+        bool bad = false;
+        for (uint32_t i = lane; i < ntiles; i += 64) bad |= f[i] != 0;
+        if (!__syncthreads_or(bad)) return;
     }
 
     const char* kbase = reinterpret_cast<const char*>(a.keys) + (size_t)kvh * a.head_stride * 2;
@@ -227,24 +190,16 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs& a, char* lds, ui
             }
         }
     };
-    // returns true when some V value of this thread's chunks is not a finite f16
-    auto store_tile = [&](int buf, const u32x4 (&st)[CPT]) -> bool {
-        bool ovf = false;
+    auto store_tile = [&](int buf, const u32x4 (&st)[CPT]) {
 #pragma unroll
         for (int cc = 0; cc < CPT; ++cc) {
             const int idx = tid + cc * 64 * WAVES;
             const int which = idx / CHUNKS;
             const int rem = idx % CHUNKS;
             const int row = rem / (D / 8), col = rem % (D / 8);
-            if (which == 0) {
-                *reinterpret_cast<u32x4*>(lds_k(buf) + row * KROWB + col * 16) = st[cc];
-            } else {
-                u32x4 h = st[cc];
-                if constexpr (DT == BF16 && !EXACT) h = bf16x8_to_f16x8(st[cc], ovf);
-                *reinterpret_cast<u32x4*>(lds_v(buf) + row * VROWB + col * 16) = h;
-            }
+            char* dst = which == 0 ? lds_k(buf) + row * KROWB : lds_v(buf) + row * VROWB;
+            *reinterpret_cast<u32x4*>(dst + col * 16) = st[cc];
         }
-        return ovf;
     };
 
     const uint32_t qpos_base = a.start + q0;  // position of this wave's first query row
@@ -272,10 +227,9 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs& a, char* lds, ui
     };
     // Online softmax of one 32-position sub-tile.  The running max is lazy: it
     // moves (and the accumulators are rescaled) only when some query's tile
-    // max exceeds it by more than 2^kLazyRescale.  Probabilities are produced
-    // packed for the P.V operand; their sum comes from v_dot2 on the packed
-    // values, so l and the P.V product see the same rounded probabilities.
-    auto softmax = [&](uint32_t spos, f32x4 (&S)[2][2], pvec (&P)[2], vec (&Plo)[2]) {
+    // max exceeds it by more than 2^kLazyRescale.  Each probability leaves as
+    // bf16 hi + lo parts for the two P.V products; l sums the fp32 values.
+    auto softmax = [&](uint32_t spos, f32x4 (&S)[2][2], vec (&P)[2], vec (&Plo)[2]) {
         if (spos + 31 > qpos_base) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
@@ -316,29 +270,15 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs& a, char* lds, ui
             for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) p[mt * 4 + j] = fast_exp2(__builtin_fmaf(S[mt][nt][j], c, moff));
-            if constexpr (!EXACT) {
-                typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-                float l = lrun[nt];
+            float l = lrun[nt];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const h2 pr = {(_Float16)p[2 * k], (_Float16)p[2 * k + 1]};
-                    P[nt][2 * k] = pr[0];
-                    P[nt][2 * k + 1] = pr[1];
-                    l = __builtin_amdgcn_fdot2(pr, h2{(_Float16)1.0f, (_Float16)1.0f}, l, false);
-                }
-                lrun[nt] = l;
-            } else {
-                // exact pass: cache-dtype hi + lo parts reproduce p to ~2^-16
-                float l = lrun[nt];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const auto h = M::cvt(p[k]);
-                    P[nt][k] = h;
-                    Plo[nt][k] = M::cvt(p[k] - (float)h);
-                    l += p[k];
-                }
-                lrun[nt] = l;
+            for (int k = 0; k < 8; ++k) {
+                const auto h = M::cvt(p[k]);
+                P[nt][k] = h;
+                Plo[nt][k] = M::cvt(p[k] - (float)h);
+                l += p[k];
             }
+            lrun[nt] = l;
         }
     };
     // lane (lg, li) addresses row base + li/4, dims 16*dt + 4*(li%4); after the
@@ -352,23 +292,14 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs& a, char* lds, ui
         const i16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p1));
         return __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
     };
-    auto pv = [&](const char* vl, int sub, const pvec (&P)[2], const vec (&Plo)[2]) {
-        if constexpr (!EXACT) {
+    auto pv = [&](const char* vl, int sub, const vec (&P)[2], const vec (&Plo)[2]) {
 #pragma unroll
-            for (int dt = 0; dt < DTILES; ++dt) {
-                const hvec vop = __builtin_bit_cast(hvec, vt_operand(vl, sub, dt));
+        for (int dt = 0; dt < DTILES; ++dt) {
+            const vec vop = __builtin_bit_cast(vec, vt_operand(vl, sub, dt));
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = MH::mma(vop, P[nt], oacc[dt][nt]);
-            }
-        } else {
-#pragma unroll
-            for (int dt = 0; dt < DTILES; ++dt) {
-                const vec vop = __builtin_bit_cast(vec, vt_operand(vl, sub, dt));
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
-                    oacc[dt][nt] = M::mma(vop, P[nt], oacc[dt][nt]);
-                    oacc[dt][nt] = M::mma(vop, Plo[nt], oacc[dt][nt]);
-                }
+            for (int nt = 0; nt < 2; ++nt) {
+                oacc[dt][nt] = M::mma(vop, P[nt], oacc[dt][nt]);
+                oacc[dt][nt] = M::mma(vop, Plo[nt], oacc[dt][nt]);
             }
         }
     };
@@ -377,8 +308,7 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs& a, char* lds, ui
         const char* vl = lds_v(buf);
         const uint32_t tpos = t * BN;
         f32x4 s0[2][2], s1[2][2];
-        pvec P0[2], P1[2];
-        vec L0[2], L1[2];
+        vec P0[2], P1[2], L0[2], L1[2];
         qk(kl, 0, s0);
         qk(kl, 1, s1);
         softmax(tpos, s0, P0, L0);
@@ -391,30 +321,23 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs& a, char* lds, ui
 
     // Two register stages: the loads of tile t+2 are in flight while tile t is
     // consumed and tile t+1 (loaded one iteration earlier) is written to LDS.
-    // The barrier after each LDS write also votes whether that tile holds V
-    // values outside the f16 range.
     u32x4 st0[CPT], st1[CPT];
     load_tile(0, st0);
-    bool any_ovf = __syncthreads_or(store_tile(0, st0));
+    store_tile(0, st0);
+    __syncthreads();
     if (ntiles > 1) load_tile(1, st1);
     for (uint32_t t = 0; t < ntiles; t += 2) {
         // even tile t in buffer 0; st1 holds tile t+1
         if (t + 2 < ntiles) load_tile(t + 2, st0);
         if (t < wave_tiles) compute(t, 0);
-        bool f = false;
-        if (t + 1 < ntiles) f = store_tile(1, st1);
-        any_ovf |= __syncthreads_or(f);
+        if (t + 1 < ntiles) store_tile(1, st1);
+        __syncthreads();
         if (t + 1 >= ntiles) break;
         // odd tile t+1 in buffer 1; st0 holds tile t+2
         if (t + 3 < ntiles) load_tile(t + 3, st1);
         if (t + 1 < wave_tiles) compute(t + 1, 1);
-        f = false;
-        if (t + 2 < ntiles) f = store_tile(0, st0);
-        any_ovf |= __syncthreads_or(f);
-    }
-    if constexpr (!EXACT) {
-        if (a.flags && tid == 0) a.flags[wg_id] = any_ovf ? 1u : 0u;
-        if (any_ovf) return;  // the exact pass owns this workgroup's rows
+        if (t + 2 < ntiles) store_tile(0, st0);
+        __syncthreads();
     }
 
     if (!wave_live) return;

@@ -37,7 +37,9 @@ def bits(t):
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("T,start", [(2048, 0), (100, 0), (77, 30), (1, 5), (33, 0), (200, 900)])
+# (20, 3000): the pipelined kernel with the KV range split into 5 chunks;
+# (6, 3000): causal rows on the MFMA decode kernel, split over the context
+@pytest.mark.parametrize("T,start", [(2048, 0), (100, 0), (77, 30), (1, 5), (33, 0), (200, 900), (20, 3000), (6, 3000)])
 def test_granite_prefill_fp16(ctx, T, start):
     log("granite prefill", T, start)
     rng = np.random.default_rng(T * 31 + start)
@@ -74,7 +76,10 @@ def test_granite_prefill_fp16(ctx, T, start):
     assert e <= TOL_16
 
 
-@pytest.mark.parametrize("T,start", [(8192, 0), (300, 0), (129, 64)])
+# (40, 8150) and (300, 8000): the pipelined kernel with each block's KV range
+# split into 4 chunks; (9, 8150) and (4, 32764): causal rows on the MFMA
+# decode kernel (64 splits per row at 32768 positions)
+@pytest.mark.parametrize("T,start", [(8192, 0), (300, 0), (129, 64), (40, 8150), (300, 8000), (9, 8150), (4, 32764)])
 def test_qwen_prefill_bf16(ctx, T, start):
     log("qwen prefill", T, start)
     rng = np.random.default_rng(T + 7 * start)
@@ -168,15 +173,19 @@ def test_bf16_values_outside_f16_range_take_the_exact_pass(ctx, shape, T):
 
 
 def test_prefill_rejects_rows_beyond_cursor_and_a_query_dtype_the_mfma_path_lacks(ctx):
-    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, 64, abi.F16)
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, 128, abi.F16)
     arena.set_len(10)
     q = torch.zeros((11, 16, 64), dtype=torch.float16, device="cuda:0")
     with rt.Graph(ctx) as g:
         with pytest.raises(abi.QxhError, match="beyond committed length"):
             rt.prefill_attention(g, arena, 0, 0, q)
-        # 16-bit caches take the MFMA prefill, whose query is the cache dtype
+    # prompts of at least one 64-position tile on 16-bit caches take the MFMA
+    # prefill, whose query is the cache dtype (shorter ones run causal rows on
+    # the decode kernels, which read any query dtype)
+    arena.set_len(64)
+    with rt.Graph(ctx) as g:
         with pytest.raises(abi.QxhError) as ei:
-            rt.prefill_attention(g, arena, 0, 0, torch.zeros((10, 16, 64), device="cuda:0"))
+            rt.prefill_attention(g, arena, 0, 0, torch.zeros((64, 16, 64), device="cuda:0"))
         assert ei.value.code == abi.QXH_ERR_UNSUPPORTED
 
 
