@@ -194,7 +194,7 @@ typedef struct {
     int32_t value_dtype;  /* qxh_dtype of stored V */
     uint32_t layers;
     uint32_t sequences;
-    uint32_t capacity;    /* positions per cache */
+    uint32_t capacity;    /* positions per cache, at most 4194304 (2^22) */
     uint32_t value_window; /* QXH_I8_TIERED: binary16 positions per (sequence, kv head), a power of
                               two in [32, 65536]; 0 for every other value dtype */
 } qxh_kv_desc;

@@ -404,6 +404,8 @@ extern "C" int32_t qxh_buffer_read(qxh_buffer_view v, void* data, uint64_t bytes
 // ---------------------------------------------------------------------------
 // KV cache
 // ---------------------------------------------------------------------------
+constexpr uint32_t kMaxCapacity = 1u << 22;
+
 static int32_t check_desc(const qxh_kv_desc* d, ShapeDims* dims) {
     QXH_REQUIRE(d, QXH_ERR_INVALID_ARGUMENT, "null KV descriptor");
     QXH_REQUIRE(shape_dims(d->shape, dims), QXH_ERR_INVALID_ARGUMENT, "unknown shape %d", d->shape);
@@ -411,6 +413,10 @@ static int32_t check_desc(const qxh_kv_desc* d, ShapeDims* dims) {
                 QXH_ERR_INVALID_ARGUMENT, "invalid KV dtype (%d, %d)", d->key_dtype, d->value_dtype);
     QXH_REQUIRE(d->layers > 0 && d->sequences > 0 && d->capacity > 0, QXH_ERR_INVALID_ARGUMENT,
                 "KV layers, sequences and capacity must be positive");
+    // the decode and prefill kernels address one kv head's rows through
+    // buffer resources, whose byte ranges are 32-bit
+    QXH_REQUIRE(d->capacity <= kMaxCapacity, QXH_ERR_INVALID_ARGUMENT, "KV capacity %u exceeds %u positions",
+                d->capacity, kMaxCapacity);
     if (d->value_dtype == QXH_I8_TIERED) {
         const uint32_t w = d->value_window;
         QXH_REQUIRE(w >= 32 && w <= 65536 && (w & (w - 1)) == 0, QXH_ERR_INVALID_ARGUMENT,

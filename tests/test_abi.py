@@ -115,6 +115,17 @@ def test_value_window_needs_tiered_values():
     assert "value_window" in abi.last_error()
 
 
+def test_capacity_is_bounded():
+    # one kv head's rows must fit the kernels' 32-bit buffer ranges: 2^22 positions at most
+    n = ctypes.c_uint64()
+    desc = abi.KvDesc(abi.SHAPE_QWEN3, abi.F32, abi.F32, 1, 1, 1 << 22)
+    assert abi.lib().qxh_kv_cache_bytes(ctypes.byref(desc), ctypes.byref(n)) == 0
+    assert n.value == 2 * 4 * (1 << 22) * 128 * 4
+    desc = abi.KvDesc(abi.SHAPE_QWEN3, abi.F32, abi.F32, 1, 1, (1 << 22) + 1)
+    assert abi.lib().qxh_kv_cache_bytes(ctypes.byref(desc), ctypes.byref(n)) == abi.QXH_ERR_INVALID_ARGUMENT
+    assert "capacity" in abi.last_error()
+
+
 def test_invalid_descriptors_are_rejected():
     n = ctypes.c_uint64()
     for desc in (abi.KvDesc(abi.SHAPE_GRANITE, 5, 0, 1, 1, 8), abi.KvDesc(abi.SHAPE_GRANITE, 0, 0, 0, 1, 8),
