@@ -185,13 +185,31 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
     const uint16_t* vring = reinterpret_cast<const uint16_t*>(a.value_ring) + (size_t)seq * a.ring_seq_stride +
                             (size_t)kvh * a.ring_head_stride;
 
+    // The query slice, pre-scaled.  An fp32 query (the block path's rotated
+    // q) is read with 16-byte loads and no per-element dtype branches.
     float q[G][EPL];
+    auto load_q = [&]() __attribute__((always_inline)) {
+        const size_t q0 = ((size_t)seq * hkv * G + kvh * G) * D + lcol;
+        if (a.query_dtype == F32) {
+            f32x4 raw[G][EPL / 4];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+            for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < EPL; ++e)
-            q[g][e] = load_any(a.query, ((size_t)seq * hkv * G + kvh * G + g) * D + lcol + e, a.query_dtype) *
-                      a.qscale;
+                for (int c = 0; c < EPL / 4; ++c)
+                    raw[g][c] = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(a.query) + q0 +
+                                                                 (size_t)g * D + 4 * c);
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) q[g][e] = raw[g][e / 4][e % 4] * a.qscale;
+        } else {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < EPL; ++e)
+                    q[g][e] = load_any(a.query, q0 + (size_t)g * D + e, a.query_dtype) * a.qscale;
+        }
+    };
 
     float m[G], l[G], acc[G][EPL];
 #pragma unroll
@@ -206,8 +224,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
     // value rows come from: 0 the plain value dtype, 1 the INT8 tier, 2 the f16
     // window of a tiered cache (the two tiered passes split the rows at the
     // boundary, so no load carries a per-row tier test).
-    auto pass = [&](uint32_t begin, uint32_t end, auto tier_tag) {
+    // PQ: the query is read after the first step's K/V loads are issued, so
+    // its latency overlaps theirs instead of preceding them.
+    auto pass = [&](uint32_t begin, uint32_t end, auto tier_tag, auto peel_q) {
         constexpr int TIER = decltype(tier_tag)::value;
+        constexpr bool PQ = decltype(peel_q)::value;
         using VSlice = typename std::conditional<
             TIER == 1, TieredCodes<EPL>,
             typename std::conditional<TIER == 2, RowSlice<F16, EPL>, RowSlice<VDT, EPL>>::type>::type;
@@ -225,6 +246,9 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
                     vr[u].template load<NT>(reinterpret_cast<const char*>(vring + (size_t)(rc & a.window_mask) * D + lcol));
                 else
                     vr[u].template load<NT>(vb + ((size_t)rc * D + lcol) * VEB);
+            }
+            if constexpr (PQ) {
+                if (base == begin) load_q();
             }
             float s[UNROLL][G];
 #pragma unroll
@@ -268,11 +292,12 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
         }
     };
     if constexpr (VDT == I8T) {
+        load_q();
         const uint32_t cut = min(max(a.tier, w0), w1);
-        pass(w0, cut, std::integral_constant<int, 1>{});
-        pass(cut, w1, std::integral_constant<int, 2>{});
+        pass(w0, cut, std::integral_constant<int, 1>{}, std::false_type{});
+        pass(cut, w1, std::integral_constant<int, 2>{}, std::false_type{});
     } else {
-        pass(w0, w1, std::integral_constant<int, 0>{});
+        pass(w0, w1, std::integral_constant<int, 0>{}, std::true_type{});
     }
 
     // merge the RPW row groups of the wave (lanes sharing lcol)
@@ -583,10 +608,6 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
     const uint32_t length = a.causal ? min(a.length, a.causal_start + seq + 1) : a.length;
     const uint32_t r0 = split * a.chunk;
     const uint32_t r1 = min(length, r0 + a.chunk);
-    const uint32_t span = r1 > r0 ? r1 - r0 : 0u;
-    const uint32_t wspan = ((span + WAVES - 1) / WAVES + 31) / 32 * 32;
-    const uint32_t w0 = r0 + wave * wspan;
-    const uint32_t w1 = min(r1, w0 + wspan);
     const float c = a.qscale;  // softmax scale * log2(e), applied to q.k in fp32
 
     const size_t head_off = (size_t)seq * a.seq_stride + (size_t)kvh * a.head_stride;
@@ -732,19 +753,25 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
         }
     };
     if constexpr (TV) {
+        // each wave its own run of rows, cut at the tier boundary
         load_q();
+        const uint32_t span = r1 > r0 ? r1 - r0 : 0u;
+        const uint32_t wspan = ((span + WAVES - 1) / WAVES + 31) / 32 * 32;
+        const uint32_t w0 = r0 + wave * wspan;
+        const uint32_t w1 = min(r1, w0 + wspan);
         const uint32_t cut = min(max(a.tier, w0), w1);
         pass(w0, cut, std::integral_constant<int, 1>{});
         pass(cut, w1, std::integral_constant<int, 2>{});
-    } else if (w1 > w0) {
-        // 16-bit caches: the wave's rows [w0, w1) as one buffer range, so a
+    } else if (r1 > r0) {
+        // 16-bit caches: the workgroup's rows [r0, r1) as one buffer range, so a
         // tile's loads past the end return zeros without a memory request and
         // the next tile's loads go out, unconditionally, before this tile's math
         // (a conditional prefetch would make the compiler wait for every load
         // before the math, or sink the loads into the branch that uses them).
-        // Rows past `end` read as zeros; their scores are masked to -inf.
-        const __amdgpu_buffer_rsrc_t krs = dec_rsrc(kb + (size_t)w0 * D * 2, (w1 - w0) * D * 2);
-        const __amdgpu_buffer_rsrc_t vrs = dec_rsrc(vb + (size_t)w0 * D * 2, (w1 - w0) * D * 2);
+        // Rows past `end` read as zeros; their scores are masked to -inf.  Wave
+        // w takes tiles w, w + WAVES, ...: the waves sweep the range together.
+        const __amdgpu_buffer_rsrc_t krs = dec_rsrc(kb + (size_t)r0 * D * 2, (r1 - r0) * D * 2);
+        const __amdgpu_buffer_rsrc_t vrs = dec_rsrc(vb + (size_t)r0 * D * 2, (r1 - r0) * D * 2);
         auto bload_tile = [&](uint32_t t, u32x4 (&kr)[2][KSTEPS], u32x4 (&vr)[VCH]) __attribute__((always_inline)) {
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt)
@@ -757,18 +784,22 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
                 vr[cc] = bload16<true>(vrs, ((t * 32 + chunk / (D / 8)) * D + (chunk % (D / 8)) * 8) * 2);
             }
         };
-        const uint32_t n = (w1 - w0 + 31) / 32;
-        u32x4 kr0[2][KSTEPS], vr0[VCH], kr1[2][KSTEPS], vr1[VCH];
-        float vs_unused[VCH];
-        bload_tile(0, kr0, vr0);
-        load_q();  // after the first tile's loads: the query's latency hides under theirs
-        for (uint32_t t = 0; t < n; t += 2) {
-            bload_tile(t + 1, kr1, vr1);
-            __builtin_amdgcn_sched_barrier(0);  // the prefetch goes out before this tile's math
-            compute(w0 + 32 * t, w1, std::integral_constant<int, 0>{}, kr0, vr0, vs_unused);
-            bload_tile(t + 2, kr0, vr0);
-            __builtin_amdgcn_sched_barrier(0);
-            if (t + 1 < n) compute(w0 + 32 * (t + 1), w1, std::integral_constant<int, 0>{}, kr1, vr1, vs_unused);
+        const uint32_t ntiles = (r1 - r0 + 31) / 32;
+        const uint32_t n = ntiles > (uint32_t)wave ? (ntiles - wave + WAVES - 1) / WAVES : 0u;
+        if (n > 0) {
+            u32x4 kr0[2][KSTEPS], vr0[VCH], kr1[2][KSTEPS], vr1[VCH];
+            float vs_unused[VCH];
+            bload_tile(wave, kr0, vr0);
+            load_q();  // after the first tile's loads: the query's latency hides under theirs
+            for (uint32_t j = 0; j < n; j += 2) {
+                const uint32_t t = wave + j * WAVES;
+                bload_tile(t + WAVES, kr1, vr1);
+                __builtin_amdgcn_sched_barrier(0);  // the prefetch goes out before this tile's math
+                compute(r0 + 32 * t, r1, std::integral_constant<int, 0>{}, kr0, vr0, vs_unused);
+                bload_tile(t + 2 * WAVES, kr0, vr0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (j + 1 < n) compute(r0 + 32 * (t + WAVES), r1, std::integral_constant<int, 0>{}, kr1, vr1, vs_unused);
+            }
         }
     }
 
