@@ -18,21 +18,29 @@ constexpr uint32_t kBlockMergeMaxSplits = kBlockMergeBatch;
 typedef float merge_v4 __attribute__((ext_vector_type(4)));
 
 // One batch of up to 16 splits folded into the running (M, L, A): every load
-// of the batch is requested before any is used.
+// of the batch is requested before any is used.  The loads are unconditional
+// (entries past `splits` re-read the last split and are weighed at zero): a
+// load under a branch makes the compiler wait for it, and for every earlier
+// request (the caller's weight rows among them), at the branch's end.
 __device__ __forceinline__ void merge_batch(const float* ml, const float* acc, uint32_t p0, uint32_t s0,
                                             uint32_t splits, uint32_t d0, float& M, float& L, merge_v4& A) {
     float m[kBlockMergeBatch], l[kBlockMergeBatch];
     merge_v4 a[kBlockMergeBatch];
 #pragma unroll
     for (uint32_t i = 0; i < kBlockMergeBatch; ++i) {
-        m[i] = -1.0e30f;
-        l[i] = 0.0f;
-        a[i] = merge_v4{0.f, 0.f, 0.f, 0.f};
-        if (s0 + i < splits) {
-            const uint32_t p = p0 + 2 * (s0 + i);
-            m[i] = ml[2 * p];
-            l[i] = ml[2 * p + 1];
-            a[i] = *reinterpret_cast<const merge_v4*>(acc + (size_t)p * 64 + d0);
+        const uint32_t p = p0 + 2 * min(s0 + i, splits - 1);
+        const float2 v = *reinterpret_cast<const float2*>(ml + 2 * p);
+        m[i] = v.x;
+        l[i] = v.y;
+        a[i] = *reinterpret_cast<const merge_v4*>(acc + (size_t)p * 64 + d0);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every request out before the first use
+#pragma unroll
+    for (uint32_t i = 0; i < kBlockMergeBatch; ++i) {
+        if (s0 + i >= splits) {
+            m[i] = -1.0e30f;
+            l[i] = 0.0f;
+            a[i] = merge_v4{0.f, 0.f, 0.f, 0.f};
         }
     }
     float Mn = M;

@@ -891,17 +891,25 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeA
     for (uint32_t s0 = sub; s0 < S; s0 += NSUB * kBatch) {
         float m[kBatch], l[kBatch];
         f32x4 v[kBatch];
+        // unconditional loads (entries past the last split re-read it and are
+        // weighed at zero): a load under a branch is waited for at the
+        // branch's end, which would serialise the batch's round trips
 #pragma unroll
         for (int b = 0; b < kBatch; ++b) {
-            const uint32_t sp = s0 + (uint32_t)b * NSUB;
+            const uint32_t sp = min(s0 + (uint32_t)b * NSUB, S - 1);
             const size_t pi = p0 + (size_t)sp * G;
-            m[b] = kNegBig;
-            l[b] = 0.0f;
-            v[b] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (sp < S) {  // predicated: no request for splits past the end
-                m[b] = a.ws_ml[2 * pi];
-                l[b] = a.ws_ml[2 * pi + 1];
-                v[b] = *reinterpret_cast<const f32x4*>(a.ws_acc + pi * D + 4 * d4);
+            const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + 2 * pi);
+            m[b] = ml.x;
+            l[b] = ml.y;
+            v[b] = *reinterpret_cast<const f32x4*>(a.ws_acc + pi * D + 4 * d4);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every request out before the first use
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            if (s0 + (uint32_t)b * NSUB >= S) {
+                m[b] = kNegBig;
+                l[b] = 0.0f;
+                v[b] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
         }
         float mb = M;
