@@ -129,13 +129,22 @@ __global__ __launch_bounds__(256) void qwen_out_kernel(QwenBlockArgs a) {
 __global__ __launch_bounds__(256) void qwen_residual_norm_kernel(QwenBlockArgs a) {
     __shared__ float wave_sums[4];
     const int t = threadIdx.x;
+    // every load before the first store: the stores may alias the inputs as
+    // far as the compiler knows, so interleaving them would serialise the
+    // eight loads of each array into eight round trips
+    uint16_t hb[8], pb[8];
     float x[8], w[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const int i = t + 256 * k;
-        x[k] = round_f16(f16_bits_to_float(a.hidden[i]) + f16_bits_to_float(a.projection[i]));
-        a.hidden_after[i] = f16_bits(x[k]);
+        hb[k] = a.hidden[i];
+        pb[k] = a.projection[i];
         w[k] = a.post_norm[i];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        x[k] = round_f16(f16_bits_to_float(hb[k]) + f16_bits_to_float(pb[k]));
+        a.hidden_after[t + 256 * k] = f16_bits(x[k]);
     }
     const float inv = qwen_inverse_rms(square_sum_256(x, wave_sums));
 #pragma unroll

@@ -63,10 +63,18 @@ __global__ __launch_bounds__(256) void granite_rope_append_kernel(KvLayer kv, Ro
 // heads, [q_heads, q_heads + kv_heads) key heads.  With `kv.keys` null the
 // key is rotated in place (the reference's in-place encode_qwen_qk_norm_rope).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void qwen_norm_rope_append_kernel(KvLayer kv, RopeAppendArgs a, int q_heads,
-                                                                    int kv_heads, void* key_inplace) {
+// Every load of a wave is requested before the first use: the input rows in
+// their dtype (a template, so no per-element dtype branch waits), the value
+// row (the key row again when there is no value to append, so the load needs
+// no branch), the frequencies, then the norm weights.
+template <int IDT>
+__device__ __forceinline__ void qwen_norm_rope_append(const KvLayer& kv, const RopeAppendArgs& a, int q_heads,
+                                                      int kv_heads, void* key_inplace) {
+    using T = typename Elem<IDT>::T;
     constexpr int D = 128, P = 64;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // readfirstlane: the head (and so every pointer chosen by it) is known to
+    // be wave-uniform, so the choice stays in scalar registers
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int head = blockIdx.x * 4 + wave;
     if (head >= q_heads + kv_heads) return;
     const uint32_t t = blockIdx.y, s = blockIdx.z;
@@ -75,28 +83,31 @@ __global__ __launch_bounds__(256) void qwen_norm_rope_append_kernel(KvLayer kv, 
     const bool is_q = head < q_heads;
     if (is_q && !a.query_out) return;  // no rotated query wanted (the query may be null)
     const int h = is_q ? head : head - q_heads;
-    const void* src = is_q ? a.query : a.key;
+    const T* src = reinterpret_cast<const T*>(is_q ? a.query : a.key);
     const size_t base = is_q ? (tok * q_heads + h) * D : (tok * kv_heads + h) * D;
-    const float xl = load_any(src, base + lane, a.input_dtype);
-    const float xr = load_any(src, base + P + lane, a.input_dtype);
-    float ss = xl * xl + xr * xr;
-    ss = group_sum<64>(ss);
-    const float inv_rms = 1.0f / __builtin_sqrtf(ss / 128.0f + 1.0e-6f);
+    const bool append_v = !is_q && !key_inplace && kv.values;  // null values: a tiered cache (tiered_v.hip)
+    const T* vsrc = append_v ? reinterpret_cast<const T*>(a.value) : src;
+    const float xl = to_f32(src[base + lane]);
+    const float xr = to_f32(src[base + P + lane]);
+    const float vl = to_f32(vsrc[base + lane]);
+    const float vr = to_f32(vsrc[base + P + lane]);
+    const float freq = a.qwen_inv_freq[lane];
     const float* norm = is_q ? a.query_norm : a.key_norm;
     const float nl = norm ? norm[lane] : 1.0f;
     const float nr = norm ? norm[P + lane] : 1.0f;
+    float ss = xl * xl + xr * xr;
+    ss = group_sum<64>(ss);
+    const float inv_rms = 1.0f / __builtin_sqrtf(ss / 128.0f + 1.0e-6f);
     const float left = xl * inv_rms * nl;
     const float right = xr * inv_rms * nr;
-    const float angle = (float)pos * a.qwen_inv_freq[lane];
+    const float angle = (float)pos * freq;
     float sn, cs;
     sincosf(angle, &sn, &cs);
     const float o_l = left * cs - right * sn;
     const float o_r = right * cs + left * sn;
     if (is_q) {
-        if (a.query_out) {
-            store_any(a.query_out, base + lane, o_l, a.output_dtype);
-            store_any(a.query_out, base + P + lane, o_r, a.output_dtype);
-        }
+        store_any(a.query_out, base + lane, o_l, a.output_dtype);
+        store_any(a.query_out, base + P + lane, o_r, a.output_dtype);
         return;
     }
     if (key_inplace) {
@@ -107,9 +118,16 @@ __global__ __launch_bounds__(256) void qwen_norm_rope_append_kernel(KvLayer kv, 
     const size_t dst = (size_t)s * kv.sequence_stride + (size_t)h * kv.head_stride + (size_t)pos * D;
     store_any(kv.keys, dst + lane, o_l, kv.key_dtype);
     store_any(kv.keys, dst + P + lane, o_r, kv.key_dtype);
-    if (!kv.values) return;  // a tiered value cache, written by tiered_v.hip
-    store_any(kv.values, dst + lane, load_any(a.value, base + lane, a.input_dtype), kv.value_dtype);
-    store_any(kv.values, dst + P + lane, load_any(a.value, base + P + lane, a.input_dtype), kv.value_dtype);
+    if (!append_v) return;
+    store_any(kv.values, dst + lane, vl, kv.value_dtype);
+    store_any(kv.values, dst + P + lane, vr, kv.value_dtype);
+}
+
+__global__ __launch_bounds__(256) void qwen_norm_rope_append_kernel(KvLayer kv, RopeAppendArgs a, int q_heads,
+                                                                    int kv_heads, void* key_inplace) {
+    if (a.input_dtype == F32) qwen_norm_rope_append<F32>(kv, a, q_heads, kv_heads, key_inplace);
+    else if (a.input_dtype == F16) qwen_norm_rope_append<F16>(kv, a, q_heads, kv_heads, key_inplace);
+    else qwen_norm_rope_append<BF16>(kv, a, q_heads, kv_heads, key_inplace);
 }
 
 // ---------------------------------------------------------------------------
