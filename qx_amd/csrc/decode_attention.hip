@@ -1143,12 +1143,15 @@ hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const 
     return launch_decode_impl(s, kv, p, a, sequences, workspace, st, dispatches);
 }
 
-// Granite attention block, fp32 and mixed caches: at most 16 splits of 16
+// Granite attention block, fp32 and mixed caches: at most 16 splits of 8
 // waves each, so the o-projection kernels can merge the partials themselves
 // (16 x 16 heads x 66 floats = 67 KB at most, read by each of 64
-// workgroups).  Measured at ctx 4096: 32 splits of 8 waves speed the
-// attention up by ~1 us but double the merge's reads, a net loss.
-constexpr int kBlockWaves = 16;
+// workgroups).  Measured at ctx 4096 (cfg 2, us per token): 8 waves of two
+// 16-row steps 360-364, 16 waves of one step 364-369 (the cross-wave merge
+// over twice the waves costs more than the second step), 4 waves 385; 32
+// splits of 8 waves speed the attention up by ~1 us but double the merge's
+// reads, a net loss.
+constexpr int kBlockWaves = 8;
 constexpr uint32_t kBlockMaxSplits = kBlockMergeMaxSplits;  // what the o kernels' merge unrolls
 
 bool block_decode_fused(int key_dtype, int value_dtype) { return valu_path(key_dtype, value_dtype); }
