@@ -133,19 +133,21 @@ __global__ __launch_bounds__(256) void granite_out_residual_kernel(GraniteBlockA
 }
 
 // fp32 and mixed caches: the attention launch left split partials; every
-// workgroup merges them (block_merge.h) before its rows.  grid 64 workgroups
-// x 4 waves, wave w of workgroup b owns rows 16 b + 4 w .. + 3; its weights
-// are requested before the merge so the two latencies overlap.
+// workgroup merges them (block_merge.h) before its rows.  grid 1024 / (4 RPW)
+// workgroups x 4 waves, wave w of workgroup b owns rows 4 RPW b + RPW w .. +
+// RPW - 1; its weights are requested before the merge so the two latencies
+// overlap.
+template <int RPW>
 __global__ __launch_bounds__(256) void granite_out_merge_residual_kernel(GraniteBlockArgs a) {
     __shared__ __attribute__((aligned(16))) float s_att[kHidden];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row0 = blockIdx.x * 16 + wave * 4;
-    f32x4 w[4][4];
+    const int row0 = blockIdx.x * 4 * RPW + wave * RPW;
+    f32x4 w[RPW][4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < RPW; ++r)
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[r][i] = ldg4_nt(a.wo + (size_t)(row0 + r) * kHidden + 256 * i + 4 * lane);
-    const float resid = lane < 4 ? a.hidden_in[row0 + lane] : 0.0f;
+    const float resid = lane < RPW ? a.hidden_in[row0 + lane] : 0.0f;
     merge_granite_attention(a.parts.ml, a.parts.acc, a.parts.splits, a.attention, s_att);
     __syncthreads();
     if (blockIdx.x == 0 && a.parts.splits > 1)
@@ -153,17 +155,26 @@ __global__ __launch_bounds__(256) void granite_out_merge_residual_kernel(Granite
     f32x4 n[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) n[i] = *reinterpret_cast<const f32x4*>(s_att + 256 * i + 4 * lane);
-    float out[4];
+    float out[RPW];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) out[r] = row_dot_loaded(w[r], n);
-    if (lane < 4) {
-        const float proj = lane == 0 ? out[0] : lane == 1 ? out[1] : lane == 2 ? out[2] : out[3];
+    for (int r = 0; r < RPW; ++r) out[r] = row_dot_loaded(w[r], n);
+    if (lane < RPW) {
+        float proj = out[0];
+#pragma unroll
+        for (int r = 1; r < RPW; ++r)
+            if (lane == r) proj = out[r];
         a.hidden_out[row0 + lane] = __builtin_fmaf(kResidual, proj, resid);
     }
 }
 
+// One row per wave, 256 workgroups: every workgroup repeats the 67 KB merge
+// from L2, but the 4 MB of o weights stream over four times the CUs (cfg 2
+// per token: 4 rows per wave 360 us, 2 rows 347.5, 1 row 345).
+constexpr int kOutRowsPerWave = 1;
+
 hipError_t launch_granite_out_merge_residual(const GraniteBlockArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL(granite_out_merge_residual_kernel, dim3(kHidden / 16), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(granite_out_merge_residual_kernel<kOutRowsPerWave>, dim3(kHidden / (4 * kOutRowsPerWave)),
+                       dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

@@ -192,11 +192,12 @@ __global__ __launch_bounds__(256) void granite_q4_out_residual_kernel(GraniteQ4A
 // fp32 and mixed caches: merge the attention launch's split partials in
 // every workgroup (block_merge.h), then the Q4 o rows.  grid 64 workgroups x
 // 8 waves, two rows per wave (16 rows per workgroup).
-__global__ __launch_bounds__(512) void granite_q4_out_merge_residual_kernel(GraniteQ4Args a) {
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void granite_q4_out_merge_residual_kernel(GraniteQ4Args a) {
     __shared__ float s_in[kHidden];
-    __shared__ u32x4 s_codes[8][64];
+    __shared__ u32x4 s_codes[WAVES][64];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, l = lane & 31;
-    const int row = blockIdx.x * 16 + 2 * wave + (lane >> 5);
+    const int row = blockIdx.x * 2 * WAVES + 2 * wave + (lane >> 5);
     const u32x4 grp = *reinterpret_cast<const u32x4*>(a.wo.packed + (size_t)row * (kHidden / 2) + l * 16);
     const float scale = f16_bits_to_float(a.wo.scales[row * (kHidden / 32) + l]);
     const float resid = a.hidden_in[row];
@@ -204,7 +205,7 @@ __global__ __launch_bounds__(512) void granite_q4_out_merge_residual_kernel(Gran
     merge_granite_attention(a.parts.ml, a.parts.acc, a.parts.splits, a.attention, s_in);
     __syncthreads();
     if (blockIdx.x == 0 && a.parts.splits > 1)
-        for (int o = t; o < kHidden; o += 512) a.attention[o] = s_in[o];
+        for (int o = t; o < kHidden; o += 64 * WAVES) a.attention[o] = s_in[o];
     const float sum = ordered_sum32(
         q4_fold32(reinterpret_cast<const uint8_t*>(&s_codes[wave][lane & 32]), scale, s_in, l, 0.0f));
     if (l == 0) a.hidden_out[row] = __builtin_fmaf(kResidual, sum, resid);
@@ -213,7 +214,8 @@ __global__ __launch_bounds__(512) void granite_q4_out_merge_residual_kernel(Gran
 }  // namespace
 
 hipError_t launch_granite_q4_out_merge_residual(const GraniteQ4Args& a, hipStream_t st) {
-    hipLaunchKernelGGL(granite_q4_out_merge_residual_kernel, dim3(kHidden / 16), dim3(512), 0, st, a);
+    constexpr int W = 4;  // 128 workgroups of 8 rows (64 of 16 rows: cfg2q4 410 against 397 us per token)
+    hipLaunchKernelGGL(granite_q4_out_merge_residual_kernel<W>, dim3(kHidden / (2 * W)), dim3(64 * W), 0, st, a);
     return hipGetLastError();
 }
 
