@@ -148,8 +148,13 @@ __device__ __forceinline__ void merge_step(float (&m)[G], float (&l)[G], float (
     }
 }
 
-template <int D, int G, int KDT, int VDT, int WAVES, int UNROLL, bool NT>
+// HSPLIT > 1: the G * HSPLIT query heads of a kv head are computed by
+// HSPLIT workgroups of G heads each (blockIdx.y = kv head * HSPLIT + part),
+// which read the same K/V rows (the second read mostly from L2): twice the
+// workgroups for a grid that would leave CUs idle, same partial layout.
+template <int D, int G, int KDT, int VDT, int WAVES, int UNROLL, bool NT, int HSPLIT = 1>
 __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs a) {
+    constexpr int GM = G * HSPLIT;  // query heads per kv head in memory
     constexpr int EB = Elem<KDT>::bytes;
     constexpr int VEB = Elem<VDT>::bytes;
     constexpr int EPL = 16 / EB;
@@ -166,8 +171,9 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
     const int lane = threadIdx.x & 63;
     const int lrow = lane / LPR;
     const int lcol = (lane % LPR) * EPL;
-    const uint32_t split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
-    const uint32_t hkv = gridDim.y;
+    const uint32_t split = blockIdx.x, kvh = blockIdx.y / HSPLIT, seq = blockIdx.z;
+    const uint32_t g0 = (blockIdx.y % HSPLIT) * G;  // first query head of this workgroup in the group
+    const uint32_t hkv = gridDim.y / HSPLIT;
 
     const uint32_t length = a.causal ? min(a.length, a.causal_start + seq + 1) : a.length;
     const uint32_t r0 = split * a.chunk;
@@ -189,7 +195,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
     // q) is read with 16-byte loads and no per-element dtype branches.
     float q[G][EPL];
     auto load_q = [&]() __attribute__((always_inline)) {
-        const size_t q0 = ((size_t)seq * hkv * G + kvh * G) * D + lcol;
+        const size_t q0 = ((size_t)seq * hkv * GM + kvh * GM + g0) * D + lcol;
         if (a.query_dtype == F32) {
             f32x4 raw[G][EPL / 4];
 #pragma unroll
@@ -335,9 +341,9 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(DecodeArgs
             A = __builtin_fmaf(sm_acc[w][g][d], f, A);
         }
         if (a.splits == 1) {
-            store_any(a.out, ((size_t)seq * hkv * G + kvh * G + g) * D + d, A / L, a.out_dtype);
+            store_any(a.out, ((size_t)seq * hkv * GM + kvh * GM + g0 + g) * D + d, A / L, a.out_dtype);
         } else {
-            const size_t p = (((size_t)seq * hkv + kvh) * a.splits + split) * G + g;
+            const size_t p = (((size_t)seq * hkv + kvh) * a.splits + split) * GM + g0 + g;
             a.ws_acc[p * D + d] = A;
             if (d == 0) {
                 a.ws_ml[2 * p] = M;
@@ -1183,10 +1189,16 @@ DecodePlan plan_block_decode(const ShapeDims& s, int key_dtype, int value_dtype,
     return p;
 }
 
+// Two workgroups per (split, kv head), one query head each: 256 workgroups
+// instead of 128 on 256 CUs, the twin's K/V reads served by the same XCD's
+// L2 (cfg 2 346 -> 329.5 us per token, cfg2q4 397.5 -> 381).
+constexpr int kBlockHeadSplit = 2;
+
 template <int KDT, int VDT>
 static void launch_block_valu(const DecodeArgs& a, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL((decode_attention_kernel<64, 2, KDT, VDT, kBlockWaves, kUnroll, true>), grid,
-                       dim3(64 * kBlockWaves), 0, st, a);
+    hipLaunchKernelGGL((decode_attention_kernel<64, 2 / kBlockHeadSplit, KDT, VDT, kBlockWaves, kUnroll, true,
+                                                kBlockHeadSplit>),
+                       grid, dim3(64 * kBlockWaves), 0, st, a);
 }
 
 hipError_t launch_block_decode_attention(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t length,
@@ -1197,7 +1209,7 @@ hipError_t launch_block_decode_attention(const ShapeDims& s, const KvLayer& kv, 
         a.ws_ml = reinterpret_cast<float*>(workspace);
         a.ws_acc = a.ws_ml + 2 * (uint64_t)s.kv_heads * p.splits * s.group;
     }
-    const dim3 grid(p.splits, s.kv_heads, 1);
+    const dim3 grid(p.splits, s.kv_heads * kBlockHeadSplit, 1);
     const int kd = kv.key_dtype, vd = kv.value_dtype;
     if (kd == F32 && vd == F32) launch_block_valu<F32, F32>(a, grid, st);
     else if (kd == F32 && vd == F16) launch_block_valu<F32, F16>(a, grid, st);
