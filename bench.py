@@ -514,14 +514,128 @@ def bench_prefill(ctx, steps, warmup, shape_name):
     # adds a fixed launch cost per replay that a single call does not amortise
     g = rt.Graph(ctx, stream)
     ms = timed(lambda: rt.prefill_attention(g, arena, 0, 0, qo[0], out=out, workspace=ws), steps, warmup, stream)
-    g.finish()
     flops = 4.0 * info.head_dim * info.q_heads * T * (T + 1) / 2
     tflops = flops / (ms * 1e-3) / 1e12
     peak = MFMA_PEAK_TFLOPS["f16" if dtype == abi.F16 else "bf16"]
+
+    # the prompt's front end: RoPE of q and k (Qwen: per-head RMSNorm first)
+    # and the K/V append of all T rows, one launch (the cursor rewinds on the
+    # host between steps)
+    def front():
+        arena.set_len(0)
+        rt.rope_kv_batch(g, arena, 0, 0, q, k, v, query_out=qo)
+
+    ms_fe = timed(front, steps, warmup, stream)
+    g.finish()
+    eb = 2
+    fe_bytes = 2 * T * (info.q_heads + 2 * info.kv_heads) * info.head_dim * eb
     return {"us_per_prefill": ms * 1000.0, "tokens": T, "flop": flops,
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
                          "frac": round(tflops / peak, 4), "traffic": None},
-            "note": "causal attention only (RoPE/append excluded), eager stream launches; flop = 4*D*Hq*T(T+1)/2"}
+            "frontend": {"us": round(ms_fe * 1000.0, 2), "bytes": fe_bytes,
+                         "roofline": roofline_hbm(fe_bytes, ms_fe, None),
+                         "note": "RoPE of q and k" + (" after per-head RMSNorm" if shape != abi.SHAPE_GRANITE else "") +
+                                 ", K/V append of every prompt row, one launch (qxh_encode_rope_kv_batch); bytes = "
+                                 "q, k, v read + rotated q, cache K, cache V written"},
+            "prompt_total_us": round((ms + ms_fe) * 1000.0, 2),
+            "note": "us_per_prefill/roofline: causal attention only, eager stream launches; flop = 4*D*Hq*T(T+1)/2; "
+                    "prompt_total_us = front end + attention"}
+
+
+# ---------------------------------------------------------------------------
+# Long prompt on the reference's canonical KV plan (Fp32KFp16V: fp32 keys,
+# f16 values) and on fp32 K/V: cfg 3's Granite prompt of 2048 tokens, fp32
+# queries, causal attention through qxh_encode_prefill_attention.
+# ---------------------------------------------------------------------------
+def bench_prefill_fp32(ctx, steps, warmup):
+    import torch
+    from qx_amd import abi
+    from qx_amd import runtime as rt
+
+    T = 2048
+    stream = torch.cuda.current_stream()
+    res = {}
+    for name, kdt, vdt in (("fp32k_f16v", abi.F32, abi.F16), ("fp32", abi.F32, abi.F32)):
+        arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, T, kdt, vdt)
+        q = torch.empty((1, T, 16, 64), device="cuda:0")
+        k = torch.empty((1, T, 8, 64), device="cuda:0")
+        v = torch.empty_like(k)
+        qo = torch.empty_like(q)
+        out = torch.empty((T, 16, 64), device="cuda:0")
+        with rt.Graph(ctx, stream) as g:
+            for i, t in enumerate((q, k, v)):
+                rt.fill_normal(g, t, seed=300 + i)
+            rt.rope_kv_batch(g, arena, 0, 0, q, k, v, query_out=qo)
+        ws = torch.empty(max(rt.prefill_workspace_bytes(arena, T), 1), dtype=torch.uint8, device="cuda:0")
+        g = rt.Graph(ctx, stream)
+        ms = timed(lambda: rt.prefill_attention(g, arena, 0, 0, qo[0], out=out, workspace=ws), steps, warmup, stream)
+        g.finish()
+        flops = 4.0 * 64 * 16 * T * (T + 1) / 2
+        tflops = flops / (ms * 1e-3) / 1e12
+        res[name] = {"us_per_prefill": round(ms * 1000.0, 1), "tflops": round(tflops, 2),
+                     "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 157.3, "unit": "TFLOP/s",
+                                  "frac": round(tflops / 157.3, 4), "traffic": None}}
+        del arena, ws
+        torch.cuda.empty_cache()
+    res["note"] = ("Granite causal prefill of 2048 tokens, fp32 queries and outputs; peak = dense fp32 MFMA "
+                   "(157.3 TFLOP/s); flop = 4*D*Hq*T(T+1)/2")
+    return res
+
+
+# ---------------------------------------------------------------------------
+# The reference's isolated decode-attention sweep (--v2-attention-sweep:
+# Granite, one layer, batch 1, fp32 K/V at ctx 32..512, one attention per
+# command buffer, median of the GPU times) and its K/V-precision table at ctx
+# 512 (fp32 K/V, fp16 K, fp16 V): here one attention launch per graph, timed
+# per launch with HIP events on the stream it runs on (median of >= 50), and
+# the host wall time of begin -> finish of that graph.
+# ---------------------------------------------------------------------------
+def bench_attention_sweep(ctx, steps, warmup):
+    import statistics
+
+    import torch
+    from qx_amd import abi
+    from qx_amd import runtime as rt
+
+    reps = max(50, steps)
+    stream = torch.cuda.current_stream()
+    cases = [(f"fp32_ctx{L}", L, abi.F32, abi.F32) for L in (32, 64, 128, 256, 512)]
+    cases += [("fp16k_ctx512", 512, abi.F16, abi.F32), ("fp16v_ctx512", 512, abi.F32, abi.F16)]
+    eb = {abi.F32: 4, abi.F16: 2}
+    res = {}
+    for name, L, kdt, vdt in cases:
+        arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, L, kdt, vdt)
+        q = torch.empty((1, 16, 64), device="cuda:0")
+        out = torch.empty_like(q)
+        with rt.Graph(ctx, stream) as g:
+            arena.fill_normal(g, seed=31, length=L)
+            rt.fill_normal(g, q, seed=32)
+        ws = torch.empty(max(rt.attention_workspace_bytes(arena, 1, L), 1), dtype=torch.uint8, device="cuda:0")
+        for _ in range(warmup):
+            with rt.Graph(ctx, stream) as g:
+                rt.attention(g, arena, 0, q, L, out=out, workspace=ws)
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        walls = []
+        for e0, e1 in ev:
+            t0 = time.perf_counter()
+            g = rt.Graph(ctx, stream)
+            e0.record(stream)
+            rt.attention(g, arena, 0, q, L, out=out, workspace=ws)
+            e1.record(stream)
+            g.finish()
+            walls.append((time.perf_counter() - t0) * 1e6)
+        torch.cuda.synchronize()
+        gpu = statistics.median(e0.elapsed_time(e1) * 1000.0 for e0, e1 in ev)
+        nbytes = L * 8 * 64 * (eb[kdt] + eb[vdt]) + 2 * 16 * 64 * 4
+        res[name] = {"context": L, "gpu_median_us": round(gpu, 2), "wall_median_us": round(statistics.median(walls), 2),
+                     "bytes": nbytes, "roofline": roofline_hbm(nbytes, gpu / 1000.0, None)}
+        del arena, ws
+    res["note"] = (f"Granite, 1 layer, batch 1, attention only (qxh_encode_attention_for_layer), {reps} samples "
+                   "per case; gpu = HIP events around the launch on its stream, wall = host time of graph "
+                   "begin -> finish; the reference publishes 54.63-67.75 us GPU medians for the same cases on "
+                   "an Apple M5 Pro")
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -746,6 +860,48 @@ def cpu_cfg5b(O, np, threads, secs):
                   f"(x{_prefill_scale(rows_all, T):.2f})")
 
 
+def cpu_frontends(O, np, threads, secs):
+    """The prompt front ends on the CPU: apply_granite_rope of cfg 3's 2048
+    tokens and cpu_qk_norm_rope of cfg 5b's 8192 (bf16), as C loops over
+    token rows (the K/V append is a row copy, included in neither).  1 thread:
+    a run of rows scaled to the prompt; all cores: the prompt's rows split
+    over the threads (independent tokens)."""
+    g = np.random.default_rng(8)
+    q = g.standard_normal((2048, 1024), dtype=np.float32)
+    k = g.standard_normal((2048, 512), dtype=np.float32)
+    tg, ng = _timed_loop(lambda: O.apply_granite_rope_rows(q[:256], k[:256], 0), secs / 4)
+    n = 2048 // threads
+    wg = _threaded([lambda i=i: O.apply_granite_rope_rows(q[i * n:(i + 1) * n], k[i * n:(i + 1) * n], i * n)
+                    for i in range(threads)], 1)
+    qb = O.to_bits16(g.standard_normal((8192, 4096), dtype=np.float32), O.BF16)
+    kb = O.to_bits16(g.standard_normal((8192, 512), dtype=np.float32), O.BF16)
+    ones = np.ones(128, np.float32)
+    tq, nq = _timed_loop(lambda: O.qwen_qk_norm_rope_rows(qb[:256], kb[:256], ones, ones, 0, O.BF16), secs / 4)
+    m = 8192 // threads
+    wq = _threaded([lambda i=i: O.qwen_qk_norm_rope_rows(qb[i * m:(i + 1) * m], kb[i * m:(i + 1) * m], ones, ones,
+                                                         i * m, O.BF16) for i in range(threads)], 1)
+    return {"cfg3": _entry(tg * 8 * 1e6, "us/prompt", f"{ng} runs of 256 rows (qxo_apply_granite_rope_rows), x8",
+                           wg * 2048 / (n * threads) * 1e6, threads,
+                           f"{n * threads} of 2048 rows over {threads} threads, scaled to 2048"),
+            "cfg5b": _entry(tq * 32 * 1e6, "us/prompt", f"{nq} runs of 256 bf16 rows (qxo_qwen_qk_norm_rope_rows), "
+                            f"x32", wq * 8192 / (m * threads) * 1e6, threads,
+                            f"{m * threads} of 8192 rows over {threads} threads, scaled to 8192")}
+
+
+def cpu_sweep(O, np, threads, secs):
+    """granite_attend of one fp32 layer at the sweep's contexts (1 thread)."""
+    g = np.random.default_rng(9)
+    out = {}
+    for L in (32, 64, 128, 256, 512):
+        c = O.KvCache(L)
+        c.extend(g.standard_normal((L, 8, 64), dtype=np.float32), g.standard_normal((L, 8, 64), dtype=np.float32))
+        q = g.standard_normal(1024, dtype=np.float32)
+        t, n = _timed_loop(lambda: O.granite_attend(q, c, L), secs / 5, 16)
+        out[f"fp32_ctx{L}"] = round(t * 1e6, 2)
+    return {"value": out, "unit": "us/layer", "cores": 1, "kind": "port",
+            "sample": "single-thread granite_attend (fp32 K/V) per context, repeated for ~0.4 s each"}
+
+
 def cpu_kv_hash(O, np, threads, secs):
     """kv_leaf_hash_v1 of fp16 Granite token rows (1 KiB K + 1 KiB V), a C loop."""
     R = 2048
@@ -766,7 +922,7 @@ def cpu_baselines(names=None, secs=2.0):
 
     threads, affinity, nproc = cpu_threads()
     fns = {"cfg1": cpu_cfg1, "cfg2": cpu_cfg2, "cfg3": cpu_cfg3, "cfg4": cpu_cfg4, "cfg5a": cpu_cfg5a,
-           "cfg5b": cpu_cfg5b, "kvhash": cpu_kv_hash}
+           "cfg5b": cpu_cfg5b, "kvhash": cpu_kv_hash, "frontend": cpu_frontends, "sweep": cpu_sweep}
     out = {}
     for name, fn in fns.items():
         if names and name not in names:
@@ -829,7 +985,8 @@ def run(ctx, args):
                          ("cfg2q4", lambda c, k, w: bench_cfg2(c, k, w, q4=True)),
                          ("cfg3", lambda c, k, w: bench_prefill(c, k, w, "cfg3")),
                          ("cfg5a", bench_cfg5a), ("qwenblock", bench_qwen_block), ("cfg5b", lambda c, k, w: bench_prefill(c, k, w, "cfg5b")),
-                         ("kvhash", bench_kv_hash), ("tieredv", bench_tiered_v)):
+                         ("kvhash", bench_kv_hash), ("tieredv", bench_tiered_v), ("sweep", bench_attention_sweep),
+                         ("prefill_fp32", bench_prefill_fp32)):
             if only and name not in only:
                 continue
             try:
@@ -841,10 +998,15 @@ def run(ctx, args):
             torch.cuda.empty_cache()
     if head and isinstance(detail.get("hbm_probe"), dict) and "read_gb_per_s" in detail["hbm_probe"]:
         head["frac_of_hbm_probe"] = round(head["roofline"]["achieved"] / detail["hbm_probe"]["read_gb_per_s"], 4)
-    cpu = {} if args.no_cpu else cpu_baselines(set(only) | {"cfg4"} if only else None)
+    wanted = (set(only) | {"cfg4"} | ({"frontend"} if only & {"cfg3", "cfg5b"} else set())) if only else None
+    cpu = {} if args.no_cpu else cpu_baselines(wanted)
     for name, entry in cpu.items():
         if name in detail and isinstance(detail[name], dict) and "error" not in detail[name]:
             detail[name]["cpu_baseline"] = entry
+    for name, entry in (cpu.get("frontend") or {}).items():
+        fe = detail.get(name, {}).get("frontend") if isinstance(detail.get(name), dict) else None
+        if isinstance(fe, dict) and isinstance(entry, dict):
+            fe["cpu_baseline"] = entry
     headline_cpu = None
     if "cfg4" in cpu:
         headline_cpu = dict(cpu["cfg4"])

@@ -52,9 +52,24 @@ fn f16_bits_to_f32(bits: u16) -> f32 {
 // context
 // ---------------------------------------------------------------------------
 
+/// The library context itself.  Everything that keeps a pointer to it (KV
+/// arenas and their workspaces, graphs, submitted graphs) holds a clone of
+/// this `Rc`, so the context is destroyed only after the last of them.
+pub struct ContextInner {
+    raw: *mut ffi::QxhContext,
+}
+
+impl Drop for ContextInner {
+    fn drop(&mut self) {
+        unsafe {
+            ffi::qxh_context_destroy(self.raw);
+        }
+    }
+}
+
 /// `MetalContext` counterpart: the device binding, its stream and metrics.
 pub struct HipContext {
-    raw: *mut ffi::QxhContext,
+    inner: Rc<ContextInner>,
 }
 
 impl HipContext {
@@ -66,17 +81,17 @@ impl HipContext {
     pub fn with_device(device: i32) -> Result<Self, String> {
         let mut raw = ptr::null_mut();
         check(unsafe { ffi::qxh_context_create(device, &mut raw) })?;
-        Ok(Self { raw })
+        Ok(Self { inner: Rc::new(ContextInner { raw }) })
     }
 
     pub fn raw(&self) -> *mut ffi::QxhContext {
-        self.raw
+        self.inner.raw
     }
 
     /// `MetalContext::metrics` (crates/qx-metal/src/lib.rs:9604-9618).
     pub fn metrics(&self) -> Result<ffi::QxhMetrics, String> {
         let mut m = ffi::QxhMetrics { graphs: 0, dispatches: 0, gpu_ms: 0.0 };
-        check(unsafe { ffi::qxh_context_metrics(self.raw, &mut m) })?;
+        check(unsafe { ffi::qxh_context_metrics(self.raw(), &mut m) })?;
         Ok(m)
     }
 
@@ -84,16 +99,16 @@ impl HipContext {
     /// the context's stream.
     pub fn begin_decode(&self) -> Result<DecodeGraph, String> {
         let mut stream = ptr::null_mut();
-        check(unsafe { ffi::qxh_context_stream(self.raw, &mut stream) })?;
+        check(unsafe { ffi::qxh_context_stream(self.raw(), &mut stream) })?;
         let mut raw = ptr::null_mut();
-        check(unsafe { ffi::qxh_graph_begin(self.raw, stream, &mut raw) })?;
-        Ok(DecodeGraph { raw })
+        check(unsafe { ffi::qxh_graph_begin(self.raw(), stream, &mut raw) })?;
+        Ok(DecodeGraph { raw, _context: self.inner.clone() })
     }
 
     /// `allocate_runtime_buffer` (crates/qx-metal/src/lib.rs:9847-9860).
     pub fn allocate_runtime_buffer(&self, length: usize) -> Result<RuntimeBuffer, String> {
         let mut view = ffi::QxhBufferView { buffer: ptr::null_mut(), offset: 0, length: 0 };
-        check(unsafe { ffi::qxh_buffer_alloc(self.raw, length as u64, &mut view) })?;
+        check(unsafe { ffi::qxh_buffer_alloc(self.raw(), length as u64, &mut view) })?;
         Ok(RuntimeBuffer::Device { allocation: Rc::new(Allocation { raw: view.buffer }), view })
     }
 
@@ -152,7 +167,7 @@ impl HipContext {
         let mut k_out = vec![0u16; key.len()];
         check(unsafe {
             ffi::qxh_run_qwen_qk_norm_rope(
-                self.raw,
+                self.raw(),
                 query.as_ptr(),
                 query.len(),
                 key.as_ptr(),
@@ -180,7 +195,7 @@ impl HipContext {
         let mut out = vec![0u16; 32 * 128];
         check(unsafe {
             ffi::qxh_run_qwen_gqa_attention(
-                self.raw,
+                self.raw(),
                 query.as_ptr(),
                 query.len(),
                 key_cache.as_ptr(),
@@ -192,14 +207,6 @@ impl HipContext {
             )
         })?;
         Ok(out)
-    }
-}
-
-impl Drop for HipContext {
-    fn drop(&mut self) {
-        unsafe {
-            ffi::qxh_context_destroy(self.raw);
-        }
     }
 }
 
@@ -321,8 +328,9 @@ pub struct ArenaInner {
     desc: ffi::QxhKvDesc,
     layout: ffi::QxhKvLayout,
     layer_bytes: u64,
-    context: *mut ffi::QxhContext,
     workspace: RefCell<Option<RuntimeBuffer>>,
+    // dropped after Drop::drop has destroyed the cache, which reads the context
+    context: Rc<ContextInner>,
 }
 
 impl Drop for ArenaInner {
@@ -337,7 +345,7 @@ impl Drop for ArenaInner {
 impl HipKvArena {
     pub fn new(context: &HipContext, desc: ffi::QxhKvDesc) -> Result<Self, String> {
         let mut raw = ptr::null_mut();
-        check(unsafe { ffi::qxh_kv_cache_create(context.raw, &desc, ptr::null_mut(), 0, &mut raw) })?;
+        check(unsafe { ffi::qxh_kv_cache_create(context.raw(), &desc, ptr::null_mut(), 0, &mut raw) })?;
         let mut layout = ffi::QxhKvLayout {
             keys: ptr::null_mut(),
             values: ptr::null_mut(),
@@ -364,8 +372,8 @@ impl HipKvArena {
                 desc,
                 layout,
                 layer_bytes,
-                context: context.raw,
                 workspace: RefCell::new(None),
+                context: context.inner.clone(),
             }),
         })
     }
@@ -415,7 +423,7 @@ impl ArenaInner {
         let mut slot = self.workspace.borrow_mut();
         if slot.as_ref().map_or(true, |w| (w.len() as u64) < bytes) {
             let mut view = ffi::QxhBufferView { buffer: ptr::null_mut(), offset: 0, length: 0 };
-            check(unsafe { ffi::qxh_buffer_alloc(self.context, bytes, &mut view) })?;
+            check(unsafe { ffi::qxh_buffer_alloc(self.context.raw, bytes, &mut view) })?;
             *slot = Some(RuntimeBuffer::Device { allocation: Rc::new(Allocation { raw: view.buffer }), view });
         }
         let w = slot.as_ref().unwrap();
@@ -440,9 +448,10 @@ impl ArenaInner {
 // ---------------------------------------------------------------------------
 
 /// `DecodeGraph` counterpart (crates/qx-metal/src/lib.rs:1701-1711): ordered
-/// work on the context's stream, single owner.
+/// work on the context's stream, single owner.  It keeps the context alive.
 pub struct DecodeGraph {
     raw: *mut ffi::QxhGraph,
+    _context: Rc<ContextInner>,
 }
 
 /// `SubmittedDecode` counterpart: work that may still be in flight; `wait`
@@ -450,6 +459,7 @@ pub struct DecodeGraph {
 pub struct SubmittedDecode {
     raw: *mut ffi::QxhGraph,
     submit_error: Option<String>,
+    _context: Rc<ContextInner>,
 }
 
 impl DecodeGraph {
@@ -723,10 +733,12 @@ impl DecodeGraph {
 
     /// `DecodeGraph::submit` (crates/qx-metal/src/lib.rs:9404-9415).
     pub fn submit(self) -> SubmittedDecode {
-        let raw = self.raw;
-        std::mem::forget(self);
+        // the graph moves on to SubmittedDecode: no discard, the context's Rc moves with it
+        let this = std::mem::ManuallyDrop::new(self);
+        let raw = this.raw;
+        let context = unsafe { ptr::read(&this._context) };
         let submit_error = check(unsafe { ffi::qxh_graph_submit(raw) }).err();
-        SubmittedDecode { raw, submit_error }
+        SubmittedDecode { raw, submit_error, _context: context }
     }
 
     /// `DecodeGraph::finish` (crates/qx-metal/src/lib.rs:9417-9419).

@@ -164,9 +164,13 @@ QXH_API int32_t qxh_buffer_subregion(qxh_buffer_view parent, uint64_t offset, ui
 /* The device address of a view, for the encoders' pointer arguments. */
 QXH_API int32_t qxh_buffer_device_ptr(qxh_buffer_view view, void** ptr);
 /* write_runtime_buffer: copies `bytes` host bytes to the view's start;
- * more than the view's length is an error. */
+ * more than the view's length is an error.  The copy first waits for all
+ * work on the buffer's device (every stream), so it never changes the input
+ * of a graph still in flight; it is an initialisation-time helper. */
 QXH_API int32_t qxh_buffer_write(qxh_buffer_view view, const void* data, uint64_t bytes);
-/* read_runtime_*: copies `bytes` (at most the view's length) to the host. */
+/* read_runtime_*: copies `bytes` (at most the view's length) to the host,
+ * after all work on the buffer's device has finished (every stream), so it
+ * reads what every submitted graph wrote. */
 QXH_API int32_t qxh_buffer_read(qxh_buffer_view view, void* data, uint64_t bytes);
 
 /* HIP-graph capture of everything encoded between capture_begin and

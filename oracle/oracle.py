@@ -97,6 +97,10 @@ def lib():
         L.qxo_qwen_qk_norm_rope.argtypes = [_u16p, _u16p, _f32p, _f32p, ctypes.c_uint32, ctypes.c_int,
                                             _u16p, _u16p]
         L.qxo_qwen_qk_norm_rope.restype = None
+        L.qxo_qwen_qk_norm_rope_rows.argtypes = [_u16p, _u16p, _f32p, _f32p, ctypes.c_uint32, ctypes.c_uint32,
+                                                 ctypes.c_int, _u16p, _u16p]
+        L.qxo_qwen_qk_norm_rope_rows.restype = None
+        L.qxo_apply_granite_rope_rows.argtypes = [_f32p, _f32p, ctypes.c_uint32, ctypes.c_uint32]
         L.qxo_qwen_inverse_frequency.argtypes = [ctypes.c_uint32]
         L.qxo_qwen_inverse_frequency.restype = ctypes.c_float
         L.qxo_qwen_gqa_attention.argtypes = [_u16p, _u16p, _u16p, ctypes.c_uint32, ctypes.c_int, _u16p, _f32p]
@@ -201,6 +205,16 @@ def apply_granite_rope(query, key, position: int):
     """apply_granite_rope, lib.rs:434-441.  Returns rotated copies."""
     q, k = _f32(query).copy(), _f32(key).copy()
     _check(lib().qxo_apply_granite_rope(_p(q), _p(k), position))
+    return q, k
+
+
+def apply_granite_rope_rows(query, key, start: int):
+    """apply_granite_rope of query [T][1024] and key [T][512] rows at positions
+    start + t, in one C loop (the prompt loop's RoPE, lib.rs:1341-1353)."""
+    q, k = _f32(query).copy(), _f32(key).copy()
+    t = q.shape[0]
+    assert q.shape == (t, 1024) and k.shape == (t, 512)
+    _check(lib().qxo_apply_granite_rope_rows(_p(q), _p(k), t, start))
     return q, k
 
 
@@ -404,6 +418,20 @@ def granite_q4_attention_block(hidden, norm_weight, wq: Q4Matrix, wk: Q4Matrix, 
 
 
 # --- Qwen (tools/qx-qwen-parity/src/main.rs) ---------------------------------
+
+def qwen_qk_norm_rope_rows(query_bits, key_bits, query_norm, key_norm, start: int, fmt: int = F16):
+    """cpu_qk_norm_rope of query [T][4096] and key [T][512] 16-bit rows at
+    positions start + t, in one C loop."""
+    q = np.ascontiguousarray(query_bits, dtype=np.uint16)
+    k = np.ascontiguousarray(key_bits, dtype=np.uint16)
+    t = q.shape[0]
+    assert q.shape == (t, 4096) and k.shape == (t, 512)
+    qn, kn = _f32(query_norm), _f32(key_norm)
+    qo, ko = np.zeros_like(q), np.zeros_like(k)
+    lib().qxo_qwen_qk_norm_rope_rows(_p(q, _u16p), _p(k, _u16p), _p(qn), _p(kn), t, start, fmt, _p(qo, _u16p),
+                                     _p(ko, _u16p))
+    return qo, ko
+
 
 def qwen_qk_norm_rope(query_bits, key_bits, query_norm, key_norm, position: int, fmt: int = F16):
     """cpu_qk_norm_rope, main.rs:1170-1210 (16-bit I/O in `fmt`)."""

@@ -276,6 +276,17 @@ QXO_EXPORT int qxo_apply_granite_rope(float* query, float* key, uint32_t positio
     return 0;
 }
 
+/* apply_granite_rope over `tokens` consecutive rows (the prompt's RoPE as the
+ * reference's prompt loop applies it, crates/qx-runtime/src/lib.rs:1341-1353:
+ * one rotation per token, position start + t).  query [tokens][1024], key
+ * [tokens][512], rotated in place. */
+QXO_EXPORT int qxo_apply_granite_rope_rows(float* query, float* key, uint32_t tokens, uint32_t start) {
+    for (uint32_t t = 0; t < tokens; ++t)
+        if (qxo_apply_granite_rope(query + (size_t)t * G_QH * G_D, key + (size_t)t * G_KVH * G_D, start + t))
+            return 1;
+    return 0;
+}
+
 /* KvCache: crates/qx-runtime/src/lib.rs:349-431.  Position-major fp32 rows
  * [capacity][KV_HEADS][HEAD_DIM] with a length cursor.  `key_format` and
  * `value_format` extend it with the fp16 stores of the Metal cache writers
@@ -488,6 +499,16 @@ QXO_EXPORT void qxo_qwen_qk_norm_rope(const uint16_t* query, const uint16_t* key
                                       uint16_t* key_out) {
     qwen_transform(query, query_out, Q_QH, query_norm, position, fmt);
     qwen_transform(key, key_out, Q_KVH, key_norm, position, fmt);
+}
+
+/* cpu_qk_norm_rope over `tokens` rows at positions start + t (query
+ * [tokens][32][128], key [tokens][4][128] in `fmt`). */
+QXO_EXPORT void qxo_qwen_qk_norm_rope_rows(const uint16_t* query, const uint16_t* key, const float* query_norm,
+                                           const float* key_norm, uint32_t tokens, uint32_t start, int fmt,
+                                           uint16_t* query_out, uint16_t* key_out) {
+    for (uint32_t t = 0; t < tokens; ++t)
+        qxo_qwen_qk_norm_rope(query + (size_t)t * Q_QH * Q_D, key + (size_t)t * Q_KVH * Q_D, query_norm, key_norm,
+                              start + t, fmt, query_out + (size_t)t * Q_QH * Q_D, key_out + (size_t)t * Q_KVH * Q_D);
 }
 
 /* Inverse frequencies exactly as the CPU oracle forms them (glibc powf), for

@@ -4,11 +4,12 @@
 // harnesses that forbid it).  For them the split-K decode partials live in
 // one file-scope device array per GPU instead of a caller workspace.  The
 // array's host-side name is only a registration handle, not a device address:
-// hipGetSymbolAddress, called once per device with that device current (from
-// qxh_context_create), yields each GPU's own copy, and every launch uses that
-// pointer.  Every call on one GPU shares its array and the array keeps the
-// last call's contents; the decode kernels overwrite every partial they read,
-// so nothing needs clearing, but calls that overlap on one GPU race.
+// hipGetSymbolAddress, called once per device with that device current (on
+// the first no-alloc call on that device), yields each GPU's own copy, and
+// every launch uses that pointer.  Every call on one GPU shares its array and
+// the array keeps the last call's contents; the decode kernels overwrite
+// every partial they read, so nothing needs clearing, but calls that overlap
+// on one GPU race.
 #include <hip/hip_runtime.h>
 
 #include <mutex>

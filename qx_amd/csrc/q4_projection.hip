@@ -190,8 +190,9 @@ __global__ __launch_bounds__(256) void granite_q4_out_residual_kernel(GraniteQ4A
 }
 
 // fp32 and mixed caches: merge the attention launch's split partials in
-// every workgroup (block_merge.h), then the Q4 o rows.  grid 64 workgroups x
-// 8 waves, two rows per wave (16 rows per workgroup).
+// every workgroup (block_merge.h), then the Q4 o rows.  Two rows per wave,
+// 2 WAVES rows per workgroup: launched with WAVES = 4 as 128 workgroups of
+// 4 waves (8 rows each).
 template <int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void granite_q4_out_merge_residual_kernel(GraniteQ4Args a) {
     __shared__ float s_in[kHidden];

@@ -131,6 +131,220 @@ __global__ __launch_bounds__(256) void qwen_norm_rope_append_kernel(KvLayer kv, 
 }
 
 // ---------------------------------------------------------------------------
+// Prompt front ends: one wave per token row, every head of the row.
+//
+// The kernels above give each head its own threads and evaluate sin/cos per
+// head, so a prompt row repeats the same 32 (Granite) or 64 (Qwen) angles
+// once per head, and their loads are one element per lane.  Here a wave owns
+// a whole token row: each lane evaluates one angle, the lanes fetch the
+// values they need from each other (ds_bpermute), and a lane then works on
+// 8-element slices of both halves of a head (elements 8j..8j+7 and the
+// rotation partners half a head further on), so every load and store is
+// 16 bytes (two for fp32) and the rotation needs no exchange.  Same
+// arithmetic, element for element and in the same order, as the per-head
+// kernels: the results are identical bit for bit.
+// ---------------------------------------------------------------------------
+
+// 8 consecutive elements of a row in the template dtype.
+template <int DT>
+__device__ __forceinline__ void load_row8(const void* base, size_t idx, float (&v)[8]) {
+    if constexpr (DT == F32) {
+        const float* p = reinterpret_cast<const float*>(base) + idx;
+        const u32x4 a = load16<false>(p), b = load16<false>(p + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = __uint_as_float(a[i]);
+            v[4 + i] = __uint_as_float(b[i]);
+        }
+    } else {
+        const u32x4 a = load16<false>(reinterpret_cast<const uint16_t*>(base) + idx);
+        Unpack<DT>::run(a, v);
+    }
+}
+
+// 8 consecutive elements stored in a runtime dtype (wave-uniform), rounded as
+// store_any rounds them.
+__device__ __forceinline__ void store_row8(void* base, size_t idx, const float (&v)[8], int dt) {
+    if (dt == F32) {
+        float* p = reinterpret_cast<float*>(base) + idx;
+        *reinterpret_cast<u32x4*>(p) = u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                             __float_as_uint(v[3])};
+        *reinterpret_cast<u32x4*>(p + 4) = u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]),
+                                                 __float_as_uint(v[6]), __float_as_uint(v[7])};
+        return;
+    }
+    uint32_t w[4];
+    if (dt == F16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = (uint32_t)__builtin_bit_cast(uint16_t, (half_t)v[2 * i]) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, (half_t)v[2 * i + 1]) << 16);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = (uint32_t)f32_to_bf16_bits(v[2 * i]) | ((uint32_t)f32_to_bf16_bits(v[2 * i + 1]) << 16);
+    }
+    *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(base) + idx) = u32x4{w[0], w[1], w[2], w[3]};
+}
+
+__device__ __forceinline__ float lane_read(float v, int src_lane) {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(v)));
+}
+
+// Granite (16 q + 8 k + 8 v heads of 64): lane = 4 hs + j, slice j of
+// head hs (task 0, a query head) and of head 16 + hs (task 1: key head hs,
+// or value head hs - 8).  Lanes 0..31 evaluate the consensus sin/cos of
+// pair `lane`.  grid ceil(rows / 4) x 256, rows = tokens x sequences.
+template <int IDT>
+__global__ __launch_bounds__(256) void granite_rope_append_rows_kernel(KvLayer kv, RopeAppendArgs a) {
+    constexpr int D = 64, P = 32, QH = 16, KVH = 8;
+    const int lane = threadIdx.x & 63;
+    const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= a.tokens * a.sequences) return;
+    const uint32_t s = r / a.tokens, t = r - s * a.tokens;
+    const uint32_t pos = a.start_position + t;
+    const int j = lane & 3, hs = lane >> 2;
+    const bool has_q = a.query_out != nullptr;
+    const bool is_k = hs < KVH;
+    const int kvh = is_k ? hs : hs - KVH;
+    const void* src1 = is_k ? a.key : a.value;
+    const bool do_v = !is_k && kv.values;  // null values: a tiered cache (tiered_v.hip)
+    const size_t qbase = ((size_t)r * QH + hs) * D, kvbase = ((size_t)r * KVH + kvh) * D;
+    float qx[8], qy[8], x1[8], y1[8];
+    if (has_q) {
+        load_row8<IDT>(a.query, qbase + 8 * j, qx);
+        load_row8<IDT>(a.query, qbase + P + 8 * j, qy);
+    }
+    if (is_k || do_v) {
+        load_row8<IDT>(src1, kvbase + 8 * j, x1);
+        load_row8<IDT>(src1, kvbase + P + 8 * j, y1);
+    }
+    float sn0 = 0.0f, cs0 = 0.0f;
+    if (lane < P) granite_rope_sin_cos(pos, (uint32_t)lane, sn0, cs0);  // positions <= 4096: always defined
+    float sn[8], cs[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        sn[i] = lane_read(sn0, 8 * j + i);
+        cs[i] = lane_read(cs0, 8 * j + i);
+    }
+    if (has_q) {
+        float o0[8], o1[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            o0[i] = __builtin_fmaf(-qy[i], sn[i], qx[i] * cs[i]);
+            o1[i] = __builtin_fmaf(qy[i], cs[i], qx[i] * sn[i]);
+        }
+        store_row8(a.query_out, qbase + 8 * j, o0, a.output_dtype);
+        store_row8(a.query_out, qbase + P + 8 * j, o1, a.output_dtype);
+    }
+    const size_t dst = (size_t)s * kv.sequence_stride + (size_t)kvh * kv.head_stride + (size_t)pos * D;
+    if (is_k) {
+        float o0[8], o1[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            o0[i] = __builtin_fmaf(-y1[i], sn[i], x1[i] * cs[i]);
+            o1[i] = __builtin_fmaf(y1[i], cs[i], x1[i] * sn[i]);
+        }
+        store_row8(kv.keys, dst + 8 * j, o0, kv.key_dtype);
+        store_row8(kv.keys, dst + P + 8 * j, o1, kv.key_dtype);
+    } else if (do_v) {
+        store_row8(kv.values, dst + 8 * j, x1, kv.value_dtype);
+        store_row8(kv.values, dst + P + 8 * j, y1, kv.value_dtype);
+    }
+}
+
+// Qwen (32 q + 4 k + 4 v heads of 128): lane = 8 hs + j; task i < 4 is
+// slice j of query head 8 i + hs, task 4 of key head hs (hs < 4) or value
+// head hs - 4.  Lane l evaluates the angle of frequency l.
+template <int IDT>
+__global__ __launch_bounds__(256) void qwen_norm_rope_append_rows_kernel(KvLayer kv, RopeAppendArgs a) {
+    constexpr int D = 128, P = 64, QH = 32, KVH = 4;
+    const int lane = threadIdx.x & 63;
+    const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= a.tokens * a.sequences) return;
+    const uint32_t s = r / a.tokens, t = r - s * a.tokens;
+    const uint32_t pos = a.start_position + t;
+    const int j = lane & 7, hs = lane >> 3;
+    const bool has_q = a.query_out != nullptr;
+    const bool is_k = hs < KVH;
+    const int kvh = is_k ? hs : hs - KVH;
+    const void* src4 = is_k ? a.key : a.value;
+    const bool do_v = !is_k && kv.values;  // null values: a tiered cache (tiered_v.hip)
+    const size_t kvbase = ((size_t)r * KVH + kvh) * D;
+    // every load is requested before the first use
+    float qx[4][8], qy[4][8], x4[8], y4[8];
+    if (has_q) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const size_t qb = ((size_t)r * QH + 8 * i + hs) * D;
+            load_row8<IDT>(a.query, qb + 8 * j, qx[i]);
+            load_row8<IDT>(a.query, qb + P + 8 * j, qy[i]);
+        }
+    }
+    if (is_k || do_v) {
+        load_row8<IDT>(src4, kvbase + 8 * j, x4);
+        load_row8<IDT>(src4, kvbase + P + 8 * j, y4);
+    }
+    float qnl[8], qnr[8], knl[8], knr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        qnl[i] = a.query_norm ? a.query_norm[8 * j + i] : 1.0f;
+        qnr[i] = a.query_norm ? a.query_norm[P + 8 * j + i] : 1.0f;
+        knl[i] = a.key_norm ? a.key_norm[8 * j + i] : 1.0f;
+        knr[i] = a.key_norm ? a.key_norm[P + 8 * j + i] : 1.0f;
+    }
+    float sn0, cs0;
+    sincosf((float)pos * a.qwen_inv_freq[lane], &sn0, &cs0);
+    float sn[8], cs[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        sn[i] = lane_read(sn0, 8 * j + i);
+        cs[i] = lane_read(cs0, 8 * j + i);
+    }
+    // per-head RMSNorm over the 8 lanes of a head, then rotate-half RoPE
+    auto norm_rope = [&](const float (&x)[8], const float (&y)[8], const float (&nl)[8], const float (&nr)[8],
+                         float (&o0)[8], float (&o1)[8]) {
+        // the per-head kernel's sum, bit for bit: there lane l adds x_l^2 +
+        // x_{l+64}^2 and the 64 lanes combine as a balanced tree in lane
+        // order; here the tree's first three levels run inside the lane (its
+        // 8 consecutive l) and the last three across the head's 8 lanes
+        float t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t[i] = x[i] * x[i] + y[i] * y[i];
+        float ss = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+        ss = group_sum<8>(ss);
+        const float inv_rms = 1.0f / __builtin_sqrtf(ss / 128.0f + 1.0e-6f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float left = x[i] * inv_rms * nl[i];
+            const float right = y[i] * inv_rms * nr[i];
+            o0[i] = left * cs[i] - right * sn[i];
+            o1[i] = right * cs[i] + left * sn[i];
+        }
+    };
+    if (has_q) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const size_t qb = ((size_t)r * QH + 8 * i + hs) * D;
+            float o0[8], o1[8];
+            norm_rope(qx[i], qy[i], qnl, qnr, o0, o1);
+            store_row8(a.query_out, qb + 8 * j, o0, a.output_dtype);
+            store_row8(a.query_out, qb + P + 8 * j, o1, a.output_dtype);
+        }
+    }
+    const size_t dst = (size_t)s * kv.sequence_stride + (size_t)kvh * kv.head_stride + (size_t)pos * D;
+    if (is_k) {
+        float o0[8], o1[8];
+        norm_rope(x4, y4, knl, knr, o0, o1);
+        store_row8(kv.keys, dst + 8 * j, o0, kv.key_dtype);
+        store_row8(kv.keys, dst + P + 8 * j, o1, kv.key_dtype);
+    } else if (do_v) {
+        store_row8(kv.values, dst + 8 * j, x4, kv.value_dtype);
+        store_row8(kv.values, dst + P + 8 * j, y4, kv.value_dtype);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Store-only append (encode_qwen_store_kv counterpart).  grid (tokens, sequences).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void store_kv_kernel(KvLayer kv, RopeAppendArgs a, int kv_heads, int head_dim) {
@@ -282,7 +496,38 @@ __global__ void conformance_kernel(const float* in, const uint32_t* coords, uint
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
+// Rows (tokens x sequences) from which a call takes the row kernels: below
+// it the per-head kernels spread a row over more waves (decode latency).
+constexpr uint32_t kRowKernelMinRows = 16;
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
 hipError_t launch_rope_append(const ShapeDims& s, const KvLayer& kv, const RopeAppendArgs& a, hipStream_t st) {
+    const uint64_t rows = (uint64_t)a.tokens * a.sequences;
+    // the row kernels move 16-byte slices: every row and cache slot starts on
+    // a 16-byte boundary when the base pointers do (row lengths and cache
+    // strides are multiples of 8 elements)
+    const bool rows_ok = rows >= kRowKernelMinRows && a.mode != 2 && aligned16(a.query) && aligned16(a.key) &&
+                         aligned16(a.value) && aligned16(a.query_out) && aligned16(kv.keys) && aligned16(kv.values);
+    if (rows_ok) {
+        const dim3 grid((unsigned)((rows + 3) / 4));
+        if (a.mode == 0) {
+            if (a.input_dtype == F32)
+                hipLaunchKernelGGL(granite_rope_append_rows_kernel<F32>, grid, dim3(256), 0, st, kv, a);
+            else if (a.input_dtype == F16)
+                hipLaunchKernelGGL(granite_rope_append_rows_kernel<F16>, grid, dim3(256), 0, st, kv, a);
+            else
+                hipLaunchKernelGGL(granite_rope_append_rows_kernel<BF16>, grid, dim3(256), 0, st, kv, a);
+        } else {
+            if (a.input_dtype == F32)
+                hipLaunchKernelGGL(qwen_norm_rope_append_rows_kernel<F32>, grid, dim3(256), 0, st, kv, a);
+            else if (a.input_dtype == F16)
+                hipLaunchKernelGGL(qwen_norm_rope_append_rows_kernel<F16>, grid, dim3(256), 0, st, kv, a);
+            else
+                hipLaunchKernelGGL(qwen_norm_rope_append_rows_kernel<BF16>, grid, dim3(256), 0, st, kv, a);
+        }
+        return hipGetLastError();
+    }
     if (a.mode == 0) {
         dim3 grid(a.tokens, a.sequences);
         hipLaunchKernelGGL(granite_rope_append_kernel, grid, dim3(256), 0, st, kv, a, s.q_heads, s.kv_heads);

@@ -154,8 +154,6 @@ extern "C" int32_t qxh_context_create(int32_t device, qxh_context** out) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(QXH_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
     if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
-    // this device's copy of the no-alloc scratch, resolved once with the device current
-    if ((e = noalloc_scratch_init(device)) != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(no-alloc scratch)");
     qxh_context* c = new qxh_context();
     c->device = device;
     c->metrics = qxh_metrics{0, 0, 0.0};
@@ -382,7 +380,10 @@ extern "C" int32_t qxh_buffer_write(qxh_buffer_view v, const void* data, uint64_
     QXH_REQUIRE(bytes <= v.length, QXH_ERR_INVALID_ARGUMENT, "initialization data (%llu bytes) exceeds runtime buffer (%llu)",
                 (unsigned long long)bytes, (unsigned long long)v.length);
     if (!bytes) return QXH_OK;
+    // graphs may run on any stream of the device (the context's is non-blocking):
+    // the copy waits for all of them, so it never lands under a kernel that reads it
     hipError_t e = hipSetDevice(v.buffer->device);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e == hipSuccess) e = hipMemcpy(v.buffer->base + v.offset, data, bytes, hipMemcpyHostToDevice);
     if (e != hipSuccess) return hip_fail(e, "runtime buffer write");
     return QXH_OK;
@@ -395,7 +396,9 @@ extern "C" int32_t qxh_buffer_read(qxh_buffer_view v, void* data, uint64_t bytes
     QXH_REQUIRE(bytes <= v.length, QXH_ERR_INVALID_ARGUMENT, "read of %llu bytes exceeds runtime buffer (%llu)",
                 (unsigned long long)bytes, (unsigned long long)v.length);
     if (!bytes) return QXH_OK;
+    // reads what every submitted graph on the device has written
     hipError_t e = hipSetDevice(v.buffer->device);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e == hipSuccess) e = hipMemcpy(data, v.buffer->base + v.offset, bytes, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(e, "runtime buffer read");
     return QXH_OK;
@@ -918,8 +921,14 @@ extern "C" int32_t qxh_encode_attention_for_layer_no_alloc(qxh_graph* g, qxh_kv_
                                                            int32_t output_dtype) {
     int32_t r = check_graph(g);
     if (r) return r;
-    void* ws = noalloc_scratch(g->ctx->device);
-    QXH_REQUIRE(ws, QXH_ERR_HIP, "attention_no_alloc: device %d has no resolved scratch", g->ctx->device);
+    // this device's copy of the scratch, resolved on the first call with the
+    // device current (hipGetSymbolAddress allocates nothing; later calls reuse it)
+    const int device = g->ctx->device;
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess) e = noalloc_scratch_init(device);
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(no-alloc scratch)");
+    void* ws = noalloc_scratch(device);
+    QXH_REQUIRE(ws, QXH_ERR_HIP, "attention_no_alloc: device %d has no resolved scratch", device);
     return encode_attention(g, c, layer, first, count, length, query, query_dtype, output, output_dtype, ws,
                             kNoAllocScratchBytes, true);
 }
@@ -1461,6 +1470,9 @@ extern "C" int32_t qxh_run_qwen_gqa_attention(qxh_context* ctx, const uint16_t* 
     QXH_REQUIRE(dtype == QXH_F16 || dtype == QXH_BF16, QXH_ERR_INVALID_ARGUMENT,
                 "run_qwen_gqa_attention: dtype %d is not a 16-bit format", dtype);
     const uint32_t context = (uint32_t)(key_len / 512);
+    // the rows go through a head-major cache, whose capacity is capped
+    QXH_REQUIRE(context <= kMaxCapacity, QXH_ERR_INVALID_ARGUMENT,
+                "Qwen GQA context %u exceeds this backend's %u-position limit", context, kMaxCapacity);
     hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
     CacheGuard cache;

@@ -8,7 +8,7 @@ import torch
 from oracle import oracle as O
 from qx_amd import abi
 from qx_amd import runtime as rt
-from tests.helpers import TOL_F32, log, rel_err
+from tests.helpers import TOL_F32, attend64, check_fp32_bar, log, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -85,6 +85,58 @@ def test_block_at_position_4095_with_prefilled_cache(ctx):
     e = rel_err(out.cpu().numpy(), r)
     log(f"block@4095 max-abs/rms {e:.3e}")
     assert e <= TOL_F32
+
+
+@pytest.mark.parametrize("position", [999, 4095])
+def test_block_attention_matches_oracle_at_attention_level(ctx, position):
+    """The block's attention itself, not diluted by the residual: the merged
+    attention that o-projection workgroup 0 writes back to the workspace
+    (after the split-K launch of 16 splits and the partial merge inside the
+    o kernel) against granite_attend over the same rotated query and the
+    cache rows the block appended (crates/qx-runtime/src/lib.rs:847-929).
+    The fp32 bar: within 1e-5 of the oracle up to 1024 positions, within
+    5e-6 of float64 at any length (the reference's own sequential folds
+    drift past 1e-5 of exact at 4096).  A second call with the hidden state
+    scaled by 1e-4 makes the attention term dominate the block output."""
+    log(f"granite block attention-level @{position}")
+    rng = np.random.default_rng(34 + position)
+    w_np = weights(rng)
+    layer = rt.GraniteLayer(*[dev(w) for w in w_np])
+    L = position + 1
+    for scale in (1.0, 1e-4):
+        arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, 4096, abi.F32)
+        with rt.Graph(ctx) as g:
+            arena.fill_normal(g, seed=7, length=position)
+        h = (scale * rng.standard_normal(1024)).astype(np.float32)
+        out = torch.empty(1024, device="cuda:0")
+        ws = torch.zeros(rt.granite_block_workspace_bytes(arena, L), dtype=torch.uint8, device="cuda:0")
+        with rt.Graph(ctx) as g:
+            rt.granite_attention_block(g, arena, 0, position, layer, dev(h), out, ws)
+            kk, vv = arena.gather(g, 0, 0, 0, L)
+        kk, vv = kk.cpu().numpy(), vv.cpu().numpy()
+        w = ws[:2 * 1024 * 4].view(torch.float32).cpu().numpy()
+        q_rot, att = w[:1024], w[1024:]
+        ref = O.KvCache(4096)
+        ref.extend(kk[:position], vv[:position])
+        r_block = O.granite_attention_block(h, *w_np, position, ref)
+        # the appended row is the block's own projection (its dot products sum
+        # in another order than the oracle's): close to the oracle's row
+        assert rel_err(kk[position], ref.keys()[position]) <= TOL_F32
+        assert rel_err(vv[position], ref.values()[position]) <= TOL_F32
+        # the attention over exactly the rows the GPU holds, with its query
+        held = O.KvCache(4096)
+        held.extend(kk, vv)
+        r_att = O.granite_attend(q_rot, held, L)
+        exact = attend64(q_rot.reshape(16, 64), kk.reshape(L, 8, 64), vv.reshape(L, 8, 64), 0.015625).ravel()
+        e, e_gpu, e_ora = check_fp32_bar(att, r_att, exact, L)
+        e_block = rel_err(out.cpu().numpy(), r_block)
+        att_share = float(np.sqrt(np.mean((out.cpu().numpy() - h) ** 2) / np.mean(out.cpu().numpy() ** 2)))
+        log(f"block attention @{position} scale {scale:g}: vs oracle {e:.3e}, vs float64 {e_gpu:.3e} "
+            f"(oracle vs float64 {e_ora:.3e}); block output {e_block:.3e}, attention share of output RMS "
+            f"{att_share:.3f}")
+        assert e_block <= TOL_F32
+        if scale < 1.0:
+            assert att_share > 0.9
 
 
 def test_captured_block_replays_match_eager(ctx):

@@ -177,3 +177,16 @@ def test_shim_calls_only_declared_functions():
     declared = set(ffi_functions())
     called = set(re.findall(r"ffi::(qxh_\w+)\(", rust_source("lib.rs")))
     assert called and called <= declared, called - declared
+
+
+def test_only_the_context_owner_holds_the_raw_context():
+    """Arenas, graphs and submitted graphs keep the context alive through the
+    Rc of its owner, so safe code cannot destroy a context that a cache or a
+    graph still reads (qxh_kv_cache_destroy and qxh_graph_wait use it)."""
+    src = rust_source("lib.rs")
+    structs = dict(re.findall(r"pub struct (\w+)\s*\{(.*?)\n\}", src, flags=re.S))
+    raw_holders = [name for name, body in structs.items() if "*mut ffi::QxhContext" in body]
+    assert raw_holders == ["ContextInner"], raw_holders
+    for name in ("HipContext", "ArenaInner", "DecodeGraph", "SubmittedDecode"):
+        assert "Rc<ContextInner>" in structs[name], name
+    assert "qxh_context_destroy" in src.split("impl Drop for ContextInner")[1].split("\n}\n")[0]
