@@ -375,6 +375,10 @@ struct DecodeStepArgs {
     uint32_t position;
     int out_dtype;
     float qscale;          // softmax scale * log2(e)
+    // attention only (no RoPE, no append): the query in query_dtype attends
+    // cached positions [0, length)
+    int query_dtype;
+    uint32_t length;
 };
 
 template <int KDT> __device__ __forceinline__ float round_to(float v) {
@@ -383,7 +387,11 @@ template <int KDT> __device__ __forceinline__ float round_to(float v) {
     else return v;
 }
 
-template <int D, int G, int KDT, int VDT, int WAVES>
+// APPEND = false: the same kernel as attention only, one dispatch for a
+// short single-sequence context (the reference's encode_attention of one
+// layer): the query rows of the group are read into LDS as they are, no row
+// is appended, and the waves stream [0, length).
+template <int D, int G, int KDT, int VDT, int WAVES, bool APPEND = true>
 __global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs a) {
     constexpr int EB = Elem<KDT>::bytes;
     constexpr int VEB = Elem<VDT>::bytes;
@@ -414,31 +422,36 @@ __global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs 
     __shared__ float sm_sin[P], sm_cos[P];
     __shared__ float sm_q[G][D], sm_k[D], sm_v[D];
     const int tid = threadIdx.x;
-    if (tid < P) granite_rope_sin_cos(pos, (uint32_t)tid, sm_sin[tid], sm_cos[tid]);
-    __syncthreads();
     const size_t head_off = (size_t)kvh * a.head_stride;
-    if (tid < (G + 2) * D) {
-        const int row = tid / D, d = tid % D, i = d % P;
-        const float sn = sm_sin[i], cs = sm_cos[i];
-        if (row < G + 1) {
-            const float* v = row < G ? a.query + ((size_t)kvh * G + row) * D : a.key + (size_t)kvh * D;
-            const float x = v[i], y = v[i + P];
-            const float r = d < P ? __builtin_fmaf(-y, sn, x * cs) : __builtin_fmaf(y, cs, x * sn);
-            if (row < G) sm_q[row][d] = r;
-            else sm_k[d] = round_to<KDT>(r);
-        } else {
-            sm_v[d] = round_to<VDT>(a.value[(size_t)kvh * D + d]);
+    if constexpr (!APPEND) {
+        if (tid < G * D) sm_q[tid / D][tid % D] = load_any(a.query, (size_t)kvh * G * D + tid, a.query_dtype);
+        __syncthreads();
+    } else {
+        if (tid < P) granite_rope_sin_cos(pos, (uint32_t)tid, sm_sin[tid], sm_cos[tid]);
+        __syncthreads();
+        if (tid < (G + 2) * D) {
+            const int row = tid / D, d = tid % D, i = d % P;
+            const float sn = sm_sin[i], cs = sm_cos[i];
+            if (row < G + 1) {
+                const float* v = row < G ? a.query + ((size_t)kvh * G + row) * D : a.key + (size_t)kvh * D;
+                const float x = v[i], y = v[i + P];
+                const float r = d < P ? __builtin_fmaf(-y, sn, x * cs) : __builtin_fmaf(y, cs, x * sn);
+                if (row < G) sm_q[row][d] = r;
+                else sm_k[d] = round_to<KDT>(r);
+            } else {
+                sm_v[d] = round_to<VDT>(a.value[(size_t)kvh * D + d]);
+            }
         }
-    }
-    __syncthreads();  // every raw q/k/v read is done before query_out (may alias query) is written
-    if (tid < (G + 2) * D) {
-        const int row = tid / D, d = tid % D;
-        if (row < G) {
-            if (a.query_out) a.query_out[((size_t)kvh * G + row) * D + d] = sm_q[row][d];
-        } else if (row == G) {
-            store_any(reinterpret_cast<char*>(a.keys) + (head_off + (size_t)pos * D) * EB, d, sm_k[d], KDT);
-        } else {
-            store_any(reinterpret_cast<char*>(a.values) + (head_off + (size_t)pos * D) * VEB, d, sm_v[d], VDT);
+        __syncthreads();  // every raw q/k/v read is done before query_out (may alias query) is written
+        if (tid < (G + 2) * D) {
+            const int row = tid / D, d = tid % D;
+            if (row < G) {
+                if (a.query_out) a.query_out[((size_t)kvh * G + row) * D + d] = sm_q[row][d];
+            } else if (row == G) {
+                store_any(reinterpret_cast<char*>(a.keys) + (head_off + (size_t)pos * D) * EB, d, sm_k[d], KDT);
+            } else {
+                store_any(reinterpret_cast<char*>(a.values) + (head_off + (size_t)pos * D) * VEB, d, sm_v[d], VDT);
+            }
         }
     }
     float q[G][EPL], kp[EPL], vp[EPL];
@@ -446,14 +459,15 @@ __global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs 
     for (int e = 0; e < EPL; ++e) {
 #pragma unroll
         for (int g = 0; g < G; ++g) q[g][e] = sm_q[g][lcol + e] * a.qscale;
-        kp[e] = sm_k[lcol + e];
-        vp[e] = sm_v[lcol + e];
+        kp[e] = APPEND ? sm_k[lcol + e] : 0.0f;
+        vp[e] = APPEND ? sm_v[lcol + e] : 0.0f;
     }
 
-    // rows [0, pos) from the cache, split evenly over the waves
-    const uint32_t wspan = ((pos + WAVES - 1) / WAVES + RPW - 1) / RPW * RPW;
+    // cached rows [0, pos) (attention only: [0, length)), split evenly over the waves
+    const uint32_t span = APPEND ? pos : a.length;
+    const uint32_t wspan = ((span + WAVES - 1) / WAVES + RPW - 1) / RPW * RPW;
     const uint32_t w0 = wave * wspan;
-    const uint32_t w1 = min(pos, w0 + wspan);
+    const uint32_t w1 = min(span, w0 + wspan);
     const char* kb = reinterpret_cast<const char*>(a.keys) + head_off * EB;
     const char* vb = reinterpret_cast<const char*>(a.values) + head_off * VEB;
 
@@ -516,7 +530,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs 
         }
     }
     // the appended row, on wave 0's first row group (uniform per wave)
-    if (wave == 0) {
+    if (APPEND && wave == 0) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float d = 0.0f;
@@ -1151,9 +1165,55 @@ static DecodeArgs decode_args(const ShapeDims& s, const KvLayer& kv, const Decod
     return a;
 }
 
+// One sequence of a Granite fp32 or mixed cache at a short context: the
+// attention-only form of the step kernel, one workgroup per kv head, in one
+// dispatch (the split path needs a combine dispatch from 128 positions on).
+constexpr uint32_t kShortAttentionMax = 1024;
+
+static bool short_attention(const ShapeDims& s, const KvLayer& kv, uint32_t sequences, uint32_t length) {
+    return sequences == 1 && length <= kShortAttentionMax && s.head_dim == 64 && s.group == 2 &&
+           kv.value_dtype != I8T && valu_path(kv.key_dtype, kv.value_dtype);
+}
+
+template <int KDT, int VDT>
+static void launch_short(const DecodeStepArgs& a, dim3 grid, int waves, hipStream_t st) {
+    if (waves == 4) hipLaunchKernelGGL((decode_step_kernel<64, 2, KDT, VDT, 4, false>), grid, dim3(256), 0, st, a);
+    else if (waves == 8) hipLaunchKernelGGL((decode_step_kernel<64, 2, KDT, VDT, 8, false>), grid, dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((decode_step_kernel<64, 2, KDT, VDT, 16, false>), grid, dim3(1024), 0, st, a);
+}
+
+static hipError_t launch_short_attention(const ShapeDims& s, const KvLayer& kv, uint32_t length, const void* query,
+                                         int query_dtype, void* out, int out_dtype, hipStream_t st) {
+    DecodeStepArgs a{};
+    a.query_dtype = query_dtype;
+    a.length = length;
+    a.keys = kv.keys;
+    a.values = kv.values;
+    a.head_stride = kv.head_stride;
+    a.out = out;
+    a.out_dtype = out_dtype;
+    a.qscale = s.scale * kLog2e;
+    // the kernel reads the query through a.query's pointer with query_dtype
+    a.query = reinterpret_cast<const float*>(query);
+    const dim3 grid(s.kv_heads);
+    const int w = step_waves(length);
+    const int kd = kv.key_dtype, vd = kv.value_dtype;
+    if (kd == F32 && vd == F32) launch_short<F32, F32>(a, grid, w, st);
+    else if (kd == F32 && vd == F16) launch_short<F32, F16>(a, grid, w, st);
+    else if (kd == F32 && vd == BF16) launch_short<F32, BF16>(a, grid, w, st);
+    else if (kd == F16 && vd == F32) launch_short<F16, F32>(a, grid, w, st);
+    else if (kd == BF16 && vd == F32) launch_short<BF16, F32>(a, grid, w, st);
+    else return hipErrorNotSupported;
+    return hipGetLastError();
+}
+
 hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t sequences,
                                    uint32_t length, const void* query, int query_dtype, void* out, int out_dtype,
                                    void* workspace, hipStream_t st, int* dispatches) {
+    if (short_attention(s, kv, sequences, length)) {
+        *dispatches = 1;
+        return launch_short_attention(s, kv, length, query, query_dtype, out, out_dtype, st);
+    }
     DecodeArgs a = decode_args(s, kv, p, length, query, query_dtype, out, out_dtype);
     return launch_decode_impl(s, kv, p, a, sequences, workspace, st, dispatches);
 }

@@ -138,6 +138,12 @@ uint32_t prefill_pipe_vt_tiles(uint32_t capacity);
 uint64_t prefill_pipe_workspace_bytes(const ShapeDims& s, uint32_t capacity, uint32_t tokens);
 hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t start, uint32_t tokens, const void* query,
                              int dtype, void* out, int out_dtype, void* workspace, hipStream_t st, int* dispatches);
+// fp32 matrix-core path (prefill_f32.hip): Granite shape, fp32 or mixed K/V
+bool prefill_f32_supported(const ShapeDims& s, int key_dtype, int value_dtype);
+uint64_t prefill_f32_workspace_bytes(const ShapeDims& s, uint32_t tokens);
+hipError_t launch_prefill_f32(const ShapeDims& s, const KvLayer& kv, uint32_t start, uint32_t tokens, const void* query,
+                              int query_dtype, void* out, int out_dtype, void* workspace, hipStream_t st,
+                              int* dispatches);
 hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint32_t start_position, uint32_t tokens,
                                     const void* query, int query_dtype, void* out, int out_dtype, void* workspace,
                                     hipStream_t st, int* dispatches);

@@ -26,8 +26,8 @@ __global__ __launch_bounds__(512, 1) void prefill_exact_pass_kernel(PrefillArgs 
 // workgroups of the exact pass after the pipelined kernel: one per CU at most
 constexpr uint32_t kExactPassWgs = 256;
 
-// Causal rows on the split-K decode kernels, for fp32 and mixed K/V caches
-// and for short prompts on any cache: every query row streams its own
+// Causal rows on the split-K decode kernels, for short prompts on any cache
+// (and longer ones on Qwen-shape fp32 caches): every query row streams its own
 // prefix, split over the CUs like a decode.  That is quadratic in bytes for
 // long prompts but has no fixed cost beyond a decode's, while the pipelined
 // MFMA prefill (equal 16-bit K/V) first rewrites the layer's whole V prefix
@@ -52,6 +52,13 @@ static bool prefill_on_decode(const ShapeDims& s, int key_dtype, int value_dtype
     return key_dtype == F32 || key_dtype != value_dtype || !prefill_pipe_supported(s) || rows_on_decode(s, start, tokens);
 }
 
+// fp32 and mixed K/V caches at the Granite shape beyond a few rows take the
+// fp32 matrix-core kernel (prefill_f32.hip); Qwen-shape fp32 caches and
+// tiered values stay on causal decode rows.
+static bool prefill_on_f32(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t start, uint32_t tokens) {
+    return prefill_f32_supported(s, key_dtype, value_dtype) && !rows_on_decode(s, start, tokens);
+}
+
 // Tiered values with 16-bit keys take the pipelined MFMA prefill when the
 // rows would (its V^T pre-pass reading the tiers); the others stay on the
 // decode kernels.
@@ -65,6 +72,10 @@ uint64_t prefill_workspace_bytes(const ShapeDims& s, int key_dtype, int value_dt
     const bool pipe_dtypes = key_dtype != F32 && (key_dtype == value_dtype || value_dtype == I8T) &&
                              prefill_pipe_supported(s);
     const uint64_t rows = decode_causal_workspace_bound(s, key_dtype, value_dtype, capacity, tokens);
+    if (prefill_f32_supported(s, key_dtype, value_dtype) && tokens > kDecodeRowsAlways) {
+        const uint64_t f32 = prefill_f32_workspace_bytes(s, tokens);
+        return rows > f32 ? rows : f32;
+    }
     if (!pipe_dtypes || tokens <= kDecodeRowsAlways) return rows;
     const uint64_t pipe = prefill_pipe_workspace_bytes(s, capacity, tokens);
     return tokens < 64 && rows > pipe ? rows : pipe;
@@ -79,6 +90,9 @@ hipError_t launch_prefill_attention(const ShapeDims& s, const KvLayer& kv, uint3
         return launch_prefill_pipe(s, kv, start_position, tokens, query, query_dtype, out, out_dtype, workspace, st,
                                    dispatches);
     }
+    if (prefill_on_f32(s, kv.key_dtype, kv.value_dtype, start_position, tokens))
+        return launch_prefill_f32(s, kv, start_position, tokens, query, query_dtype, out, out_dtype, workspace, st,
+                                  dispatches);
     if (prefill_on_decode(s, kv.key_dtype, kv.value_dtype, start_position, tokens)) {
         const DecodePlan p = plan_decode_causal(s, kv.key_dtype, kv.value_dtype, start_position, tokens);
         return launch_decode_causal_rows(s, kv, p, start_position, tokens, query, query_dtype, out, out_dtype, workspace,

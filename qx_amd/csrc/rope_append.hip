@@ -173,16 +173,17 @@ __device__ __forceinline__ void store_row8(void* base, size_t idx, const float (
                                                  __float_as_uint(v[6]), __float_as_uint(v[7])};
         return;
     }
+    // gfx950 converts two floats per instruction, rounding to nearest even
+    // (v_cvt_pk_f16_f32, v_cvt_pk_bf16_f32), as store_any's conversions round
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
     uint32_t w[4];
-    if (dt == F16) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            w[i] = (uint32_t)__builtin_bit_cast(uint16_t, (half_t)v[2 * i]) |
-                   ((uint32_t)__builtin_bit_cast(uint16_t, (half_t)v[2 * i + 1]) << 16);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            w[i] = (uint32_t)f32_to_bf16_bits(v[2 * i]) | ((uint32_t)f32_to_bf16_bits(v[2 * i + 1]) << 16);
+    for (int i = 0; i < 4; ++i) {
+        const f32x2 p = {v[2 * i], v[2 * i + 1]};
+        w[i] = dt == F16 ? __builtin_bit_cast(uint32_t, __builtin_convertvector(p, f16x2))
+                         : __builtin_bit_cast(uint32_t, __builtin_convertvector(p, bf16x2));
     }
     *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(base) + idx) = u32x4{w[0], w[1], w[2], w[3]};
 }
@@ -253,45 +254,42 @@ __global__ __launch_bounds__(256) void granite_rope_append_rows_kernel(KvLayer k
     }
 }
 
-// Qwen (32 q + 4 k + 4 v heads of 128): lane = 8 hs + j; task i < 4 is
-// slice j of query head 8 i + hs, task 4 of key head hs (hs < 4) or value
-// head hs - 4.  Lane l evaluates the angle of frequency l.
+// Qwen (32 q + 4 k + 4 v heads of 128): five waves per token row, wave
+// task 0..3 the query heads 8 task + hs, task 4 the key heads (hs < 4) and
+// value heads (hs - 4); lane = 8 hs + j works on slice j of head hs.  Each
+// wave evaluates the row's 64 angles itself, one per lane (one task per wave
+// measured 30.4 against 36.0 us for all five tasks in one wave, cfg 5b's
+// 8192-row prompt: the smaller waves keep more of the row in flight).
 template <int IDT>
 __global__ __launch_bounds__(256) void qwen_norm_rope_append_rows_kernel(KvLayer kv, RopeAppendArgs a) {
     constexpr int D = 128, P = 64, QH = 32, KVH = 4;
     const int lane = threadIdx.x & 63;
-    const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // readfirstlane: the task (and every pointer chosen by it) is wave-uniform
+    const uint32_t v = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t r = v / 5, task = v % 5;
     if (r >= a.tokens * a.sequences) return;
     const uint32_t s = r / a.tokens, t = r - s * a.tokens;
     const uint32_t pos = a.start_position + t;
     const int j = lane & 7, hs = lane >> 3;
     const bool has_q = a.query_out != nullptr;
-    const bool is_k = hs < KVH;
+    if (task < 4 && !has_q) return;
+    const bool is_q = task < 4;
+    const bool is_k = !is_q && hs < KVH;
     const int kvh = is_k ? hs : hs - KVH;
-    const void* src4 = is_k ? a.key : a.value;
-    const bool do_v = !is_k && kv.values;  // null values: a tiered cache (tiered_v.hip)
-    const size_t kvbase = ((size_t)r * KVH + kvh) * D;
-    // every load is requested before the first use
-    float qx[4][8], qy[4][8], x4[8], y4[8];
-    if (has_q) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const size_t qb = ((size_t)r * QH + 8 * i + hs) * D;
-            load_row8<IDT>(a.query, qb + 8 * j, qx[i]);
-            load_row8<IDT>(a.query, qb + P + 8 * j, qy[i]);
-        }
+    const bool do_v = !is_q && !is_k && kv.values;
+    const void* src = is_q ? a.query : (is_k ? a.key : a.value);
+    const size_t base = is_q ? ((size_t)r * QH + 8 * task + hs) * D : ((size_t)r * KVH + kvh) * D;
+    float x[8], y[8];
+    if (is_q || is_k || do_v) {
+        load_row8<IDT>(src, base + 8 * j, x);
+        load_row8<IDT>(src, base + P + 8 * j, y);
     }
-    if (is_k || do_v) {
-        load_row8<IDT>(src4, kvbase + 8 * j, x4);
-        load_row8<IDT>(src4, kvbase + P + 8 * j, y4);
-    }
-    float qnl[8], qnr[8], knl[8], knr[8];
+    const float* norm = is_q ? a.query_norm : a.key_norm;
+    float nl[8], nr[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        qnl[i] = a.query_norm ? a.query_norm[8 * j + i] : 1.0f;
-        qnr[i] = a.query_norm ? a.query_norm[P + 8 * j + i] : 1.0f;
-        knl[i] = a.key_norm ? a.key_norm[8 * j + i] : 1.0f;
-        knr[i] = a.key_norm ? a.key_norm[P + 8 * j + i] : 1.0f;
+        nl[i] = norm ? norm[8 * j + i] : 1.0f;
+        nr[i] = norm ? norm[P + 8 * j + i] : 1.0f;
     }
     float sn0, cs0;
     sincosf((float)pos * a.qwen_inv_freq[lane], &sn0, &cs0);
@@ -301,46 +299,37 @@ __global__ __launch_bounds__(256) void qwen_norm_rope_append_rows_kernel(KvLayer
         sn[i] = lane_read(sn0, 8 * j + i);
         cs[i] = lane_read(cs0, 8 * j + i);
     }
-    // per-head RMSNorm over the 8 lanes of a head, then rotate-half RoPE
-    auto norm_rope = [&](const float (&x)[8], const float (&y)[8], const float (&nl)[8], const float (&nr)[8],
-                         float (&o0)[8], float (&o1)[8]) {
-        // the per-head kernel's sum, bit for bit: there lane l adds x_l^2 +
-        // x_{l+64}^2 and the 64 lanes combine as a balanced tree in lane
-        // order; here the tree's first three levels run inside the lane (its
-        // 8 consecutive l) and the last three across the head's 8 lanes
-        float t[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) t[i] = x[i] * x[i] + y[i] * y[i];
-        float ss = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
-        ss = group_sum<8>(ss);
-        const float inv_rms = 1.0f / __builtin_sqrtf(ss / 128.0f + 1.0e-6f);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float left = x[i] * inv_rms * nl[i];
-            const float right = y[i] * inv_rms * nr[i];
-            o0[i] = left * cs[i] - right * sn[i];
-            o1[i] = right * cs[i] + left * sn[i];
-        }
-    };
-    if (has_q) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const size_t qb = ((size_t)r * QH + 8 * i + hs) * D;
-            float o0[8], o1[8];
-            norm_rope(qx[i], qy[i], qnl, qnr, o0, o1);
-            store_row8(a.query_out, qb + 8 * j, o0, a.output_dtype);
-            store_row8(a.query_out, qb + P + 8 * j, o1, a.output_dtype);
-        }
-    }
     const size_t dst = (size_t)s * kv.sequence_stride + (size_t)kvh * kv.head_stride + (size_t)pos * D;
-    if (is_k) {
-        float o0[8], o1[8];
-        norm_rope(x4, y4, knl, knr, o0, o1);
+    if (do_v) {
+        store_row8(kv.values, dst + 8 * j, x, kv.value_dtype);
+        store_row8(kv.values, dst + P + 8 * j, y, kv.value_dtype);
+        return;
+    }
+    if (!is_q && !is_k) return;
+    // per-head RMSNorm, the per-head kernel's sum bit for bit: there lane l
+    // adds x_l^2 + x_{l+64}^2 and the 64 lanes combine as a balanced tree in
+    // lane order; here the tree's first three levels run inside the lane (its
+    // 8 consecutive l) and the last three across the head's 8 lanes
+    float tt[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) tt[i] = x[i] * x[i] + y[i] * y[i];
+    float ss = ((tt[0] + tt[1]) + (tt[2] + tt[3])) + ((tt[4] + tt[5]) + (tt[6] + tt[7]));
+    ss = group_sum<8>(ss);
+    const float inv_rms = 1.0f / __builtin_sqrtf(ss / 128.0f + 1.0e-6f);
+    float o0[8], o1[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float left = x[i] * inv_rms * nl[i];
+        const float right = y[i] * inv_rms * nr[i];
+        o0[i] = left * cs[i] - right * sn[i];
+        o1[i] = right * cs[i] + left * sn[i];
+    }
+    if (is_q) {
+        store_row8(a.query_out, base + 8 * j, o0, a.output_dtype);
+        store_row8(a.query_out, base + P + 8 * j, o1, a.output_dtype);
+    } else {
         store_row8(kv.keys, dst + 8 * j, o0, kv.key_dtype);
         store_row8(kv.keys, dst + P + 8 * j, o1, kv.key_dtype);
-    } else if (do_v) {
-        store_row8(kv.values, dst + 8 * j, x4, kv.value_dtype);
-        store_row8(kv.values, dst + P + 8 * j, y4, kv.value_dtype);
     }
 }
 
@@ -507,10 +496,12 @@ hipError_t launch_rope_append(const ShapeDims& s, const KvLayer& kv, const RopeA
     // the row kernels move 16-byte slices: every row and cache slot starts on
     // a 16-byte boundary when the base pointers do (row lengths and cache
     // strides are multiples of 8 elements)
-    const bool rows_ok = rows >= kRowKernelMinRows && a.mode != 2 && aligned16(a.query) && aligned16(a.key) &&
-                         aligned16(a.value) && aligned16(a.query_out) && aligned16(kv.keys) && aligned16(kv.values);
+    const bool rows_ok = rows >= kRowKernelMinRows && rows * 5 < (1ull << 31) && a.mode != 2 && aligned16(a.query) &&
+                         aligned16(a.key) && aligned16(a.value) && aligned16(a.query_out) && aligned16(kv.keys) &&
+                         aligned16(kv.values);
     if (rows_ok) {
-        const dim3 grid((unsigned)((rows + 3) / 4));
+        const dim3 grid((unsigned)((rows + 3) / 4));       // Granite: a wave per row
+        const dim3 qgrid((unsigned)((rows * 5 + 3) / 4));  // Qwen: five waves per row
         if (a.mode == 0) {
             if (a.input_dtype == F32)
                 hipLaunchKernelGGL(granite_rope_append_rows_kernel<F32>, grid, dim3(256), 0, st, kv, a);
@@ -520,11 +511,11 @@ hipError_t launch_rope_append(const ShapeDims& s, const KvLayer& kv, const RopeA
                 hipLaunchKernelGGL(granite_rope_append_rows_kernel<BF16>, grid, dim3(256), 0, st, kv, a);
         } else {
             if (a.input_dtype == F32)
-                hipLaunchKernelGGL(qwen_norm_rope_append_rows_kernel<F32>, grid, dim3(256), 0, st, kv, a);
+                hipLaunchKernelGGL(qwen_norm_rope_append_rows_kernel<F32>, qgrid, dim3(256), 0, st, kv, a);
             else if (a.input_dtype == F16)
-                hipLaunchKernelGGL(qwen_norm_rope_append_rows_kernel<F16>, grid, dim3(256), 0, st, kv, a);
+                hipLaunchKernelGGL(qwen_norm_rope_append_rows_kernel<F16>, qgrid, dim3(256), 0, st, kv, a);
             else
-                hipLaunchKernelGGL(qwen_norm_rope_append_rows_kernel<BF16>, grid, dim3(256), 0, st, kv, a);
+                hipLaunchKernelGGL(qwen_norm_rope_append_rows_kernel<BF16>, qgrid, dim3(256), 0, st, kv, a);
         }
         return hipGetLastError();
     }

@@ -212,3 +212,44 @@ def test_mixed_kv_leaf_and_verification_hashes(ctx, shape, kdt, vdt):
     ref = O.verification_hashes(res.cpu().numpy().tobytes(), stride, [row_bytes(k[0]) for k, _ in vrows],
                                 [row_bytes(v[0]) for _, v in vrows], token, layers, 2)
     assert dig.cpu().numpy().tobytes() == ref
+
+
+@pytest.mark.parametrize("kdt,vdt", [(abi.F32, abi.F32)] + MIXED)
+def test_short_single_sequence_attention(ctx, kdt, vdt):
+    """One sequence at contexts up to 1024 positions takes the one-dispatch
+    attention (one workgroup per kv head, 4, 8 or 16 waves by length): every
+    length class against the oracle at the fp32 bar, a 16-bit query and a
+    bf16 output once each, and the split path (the same sequence inside a
+    two-sequence call) within the bar of it."""
+    rng = np.random.default_rng(100 + 5 * kdt + vdt)
+    for length in (1, 37, 128, 129, 500, 768, 769, 1024):
+        arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 2, 1024, kdt, vdt)
+        with rt.Graph(ctx) as g:
+            arena.fill_normal(g, seed=length, length=length)
+            kk, vv = arena.gather(g, 0, 0, 0, length)
+        kf, vf = kk.float().cpu().numpy(), vv.float().cpu().numpy()
+        ref_cache = O.KvCache(1024)
+        ref_cache.extend(kf, vf)
+        qn = rng.standard_normal((16, 64), dtype=np.float32)
+        q16 = length == 129
+        qt = dev(qn).half() if q16 else dev(qn)
+        qf = qt.float().cpu().numpy()
+        out_dt = torch.bfloat16 if length == 500 else torch.float32
+        out = torch.empty((1, 16, 64), dtype=out_dt, device="cuda:0")
+        with rt.Graph(ctx) as g:
+            rt.attention(g, arena, 0, qt[None], length, out=out)
+        ref = O.granite_attend(qf.ravel(), ref_cache, length)
+        got = out.float().cpu().numpy().ravel()
+        if out_dt == torch.bfloat16:
+            want = torch.from_numpy(ref).to(torch.bfloat16).float().numpy()
+            assert np.max(np.abs(got - want)) <= 2.0 ** -8 * np.max(np.abs(want)) + 1e-6, length
+        else:
+            e, _, _ = check_fp32_bar(got, ref, attend64(qf, kf, vf, 0.015625).ravel(), length)
+            log(f"short attention {kdt}/{vdt} L={length}: {e:.2e}")
+        # sequence 0 again inside a two-sequence call, which takes the split path
+        two = torch.empty((2, 16, 64), device="cuda:0")
+        q2 = torch.stack([qt.float(), qt.float()])
+        with rt.Graph(ctx) as g:
+            rt.attention(g, arena, 0, q2, length, out=two)
+        if out_dt == torch.float32:
+            assert rel_err(two[0].cpu().numpy().ravel(), got) <= TOL_F32
