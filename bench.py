@@ -50,6 +50,26 @@ def timed(fn, steps, warmup, stream):
     return start.elapsed_time(end) / steps  # ms per step
 
 
+_SLEEP_CYCLES_PER_US = None
+
+
+def gpu_hold(stream, us):
+    """Keep the GPU busy for about `us` microseconds (torch's bounded
+    cycle-count spin kernel) so that work the host enqueues behind it is
+    timed by its events without the host's launch cost in between."""
+    import torch
+    global _SLEEP_CYCLES_PER_US
+    if _SLEEP_CYCLES_PER_US is None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1000)
+        e0.record(stream)
+        torch.cuda._sleep(2_000_000)
+        e1.record(stream)
+        e1.synchronize()
+        _SLEEP_CYCLES_PER_US = 2_000_000 / max(e0.elapsed_time(e1) * 1000.0, 1.0)
+    torch.cuda._sleep(int(us * _SLEEP_CYCLES_PER_US))
+
+
 def source_digest(paths):
     """sha256 over the named repository files (the sources a kernel is built from)."""
     import hashlib
@@ -518,17 +538,35 @@ def bench_prefill(ctx, steps, warmup, shape_name):
     tflops = flops / (ms * 1e-3) / 1e12
     peak = MFMA_PEAK_TFLOPS["f16" if dtype == abi.F16 else "bf16"]
 
-    # the prompt's front end: RoPE of q and k (Qwen: per-head RMSNorm first)
-    # and the K/V append of all T rows, one launch (the cursor rewinds on the
-    # host between steps)
-    def front():
-        arena.set_len(0)
-        rt.rope_kv_batch(g, arena, 0, 0, q, k, v, query_out=qo)
-
-    ms_fe = timed(front, steps, warmup, stream)
     g.finish()
+
+    # the prompt's front end: RoPE of q and k (Qwen: per-head RMSNorm first)
+    # and the K/V append of all T rows, one launch per prompt.  Input sets
+    # are rotated so they total more than the 256 MB memory-side cache (every
+    # call reads its q/k/v from HBM), and all sets' calls are captured in one
+    # HIP graph (the cursor rewinds on the host between captured calls), so
+    # the replay time is GPU time with no host launch cost per call.
     eb = 2
-    fe_bytes = 2 * T * (info.q_heads + 2 * info.kv_heads) * info.head_dim * eb
+    fe_in = T * (info.q_heads + 2 * info.kv_heads) * info.head_dim * eb
+    fe_bytes = 2 * fe_in
+    nsets = max(2, -(-(320 << 20) // fe_in))
+    sets = []
+    with rt.Graph(ctx, stream) as g:
+        for i in range(nsets):
+            ts = [torch.empty_like(t) for t in (q, k, v)]
+            for j, t in enumerate(ts):
+                rt.fill_normal(g, t, seed=400 + 3 * i + j)
+            sets.append(ts)
+    qos = [torch.empty_like(qo) for _ in range(2)]
+    g = rt.Graph(ctx, stream)
+    g.capture_begin()
+    for i, (qi, ki, vi) in enumerate(sets):
+        arena.set_len(0)
+        rt.rope_kv_batch(g, arena, 0, 0, qi, ki, vi, query_out=qos[i & 1])
+    replay = g.capture_end()
+    g.discard()
+    ms_fe = timed(lambda: replay.launch(stream), max(3, steps // 2), 2, stream) / nsets
+    del replay, sets, qos
     return {"us_per_prefill": ms * 1000.0, "tokens": T, "flop": flops,
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
                          "frac": round(tflops / peak, 4), "traffic": None},
@@ -536,7 +574,8 @@ def bench_prefill(ctx, steps, warmup, shape_name):
                          "roofline": roofline_hbm(fe_bytes, ms_fe, None),
                          "note": "RoPE of q and k" + (" after per-head RMSNorm" if shape != abi.SHAPE_GRANITE else "") +
                                  ", K/V append of every prompt row, one launch (qxh_encode_rope_kv_batch); bytes = "
-                                 "q, k, v read + rotated q, cache K, cache V written"},
+                                 f"q, k, v read + rotated q, cache K, cache V written; {nsets} input sets rotated "
+                                 "(more than the 256 MB memory-side cache), their calls replayed as one HIP graph"},
             "prompt_total_us": round((ms + ms_fe) * 1000.0, 2),
             "note": "us_per_prefill/roofline: causal attention only, eager stream launches; flop = 4*D*Hq*T(T+1)/2; "
                     "prompt_total_us = front end + attention"}
@@ -585,10 +624,11 @@ def bench_prefill_fp32(ctx, steps, warmup):
 # ---------------------------------------------------------------------------
 # The reference's isolated decode-attention sweep (--v2-attention-sweep:
 # Granite, one layer, batch 1, fp32 K/V at ctx 32..512, one attention per
-# command buffer, median of the GPU times) and its K/V-precision table at ctx
-# 512 (fp32 K/V, fp16 K, fp16 V): here one attention launch per graph, timed
-# per launch with HIP events on the stream it runs on (median of >= 50), and
-# the host wall time of begin -> finish of that graph.
+# command buffer, median of the command buffers' GPU times) and its
+# K/V-precision table at ctx 512 (fp32 K/V, fp16 K, fp16 V): here each
+# attention call is bracketed by HIP events on its stream, all of them queued
+# behind a spin kernel so the events time the GPU alone (median of >= 50),
+# and separately the host wall time of graph begin -> finish per call.
 # ---------------------------------------------------------------------------
 def bench_attention_sweep(ctx, steps, warmup):
     import statistics
@@ -616,25 +656,40 @@ def bench_attention_sweep(ctx, steps, warmup):
                 rt.attention(g, arena, 0, q, L, out=out, workspace=ws)
         torch.cuda.synchronize()
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        walls = []
+        gpu_hold(stream, 100.0 * reps)
+        g = rt.Graph(ctx, stream)
         for e0, e1 in ev:
-            t0 = time.perf_counter()
-            g = rt.Graph(ctx, stream)
             e0.record(stream)
             rt.attention(g, arena, 0, q, L, out=out, workspace=ws)
             e1.record(stream)
-            g.finish()
-            walls.append((time.perf_counter() - t0) * 1e6)
+        g.finish()
         torch.cuda.synchronize()
         gpu = statistics.median(e0.elapsed_time(e1) * 1000.0 for e0, e1 in ev)
+        walls = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            with rt.Graph(ctx, stream) as g:
+                rt.attention(g, arena, 0, q, L, out=out, workspace=ws)
+            walls.append((time.perf_counter() - t0) * 1e6)
+        # back to back in a decode loop: 32 calls captured in one HIP graph
+        g = rt.Graph(ctx, stream)
+        g.capture_begin()
+        for _ in range(32):
+            rt.attention(g, arena, 0, q, L, out=out, workspace=ws)
+        replay = g.capture_end()
+        g.discard()
+        loop_us = timed(lambda: replay.launch(stream), 5, 2, stream) * 1000.0 / 32
+        del replay
         nbytes = L * 8 * 64 * (eb[kdt] + eb[vdt]) + 2 * 16 * 64 * 4
         res[name] = {"context": L, "gpu_median_us": round(gpu, 2), "wall_median_us": round(statistics.median(walls), 2),
-                     "bytes": nbytes, "roofline": roofline_hbm(nbytes, gpu / 1000.0, None)}
+                     "graph_loop_us": round(loop_us, 2), "bytes": nbytes,
+                     "roofline": roofline_hbm(nbytes, gpu / 1000.0, None)}
         del arena, ws
     res["note"] = (f"Granite, 1 layer, batch 1, attention only (qxh_encode_attention_for_layer), {reps} samples "
-                   "per case; gpu = HIP events around the launch on its stream, wall = host time of graph "
-                   "begin -> finish; the reference publishes 54.63-67.75 us GPU medians for the same cases on "
-                   "an Apple M5 Pro")
+                   "per case; gpu = HIP events around each launch on its stream, every launch queued behind a "
+                   "spin kernel so no host time falls between the events; wall = host time of graph begin -> "
+                   "finish (synchronous) per call; graph_loop = per call in a HIP graph of 32 back-to-back calls; "
+                   "the reference publishes 54.63-67.75 us GPU medians for the same cases on an Apple M5 Pro")
     return res
 
 
