@@ -145,19 +145,20 @@ __global__ __launch_bounds__(256) void qwen_norm_rope_append_kernel(KvLayer kv, 
 // kernels: the results are identical bit for bit.
 // ---------------------------------------------------------------------------
 
-// 8 consecutive elements of a row in the template dtype.
+// 8 consecutive elements of a row in the template dtype (nontemporal: each
+// prompt row is read once).
 template <int DT>
 __device__ __forceinline__ void load_row8(const void* base, size_t idx, float (&v)[8]) {
     if constexpr (DT == F32) {
         const float* p = reinterpret_cast<const float*>(base) + idx;
-        const u32x4 a = load16<false>(p), b = load16<false>(p + 4);
+        const u32x4 a = load16<true>(p), b = load16<true>(p + 4);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             v[i] = __uint_as_float(a[i]);
             v[4 + i] = __uint_as_float(b[i]);
         }
     } else {
-        const u32x4 a = load16<false>(reinterpret_cast<const uint16_t*>(base) + idx);
+        const u32x4 a = load16<true>(reinterpret_cast<const uint16_t*>(base) + idx);
         Unpack<DT>::run(a, v);
     }
 }
@@ -167,10 +168,12 @@ __device__ __forceinline__ void load_row8(const void* base, size_t idx, float (&
 __device__ __forceinline__ void store_row8(void* base, size_t idx, const float (&v)[8], int dt) {
     if (dt == F32) {
         float* p = reinterpret_cast<float*>(base) + idx;
-        *reinterpret_cast<u32x4*>(p) = u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
-                                             __float_as_uint(v[3])};
-        *reinterpret_cast<u32x4*>(p + 4) = u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]),
-                                                 __float_as_uint(v[6]), __float_as_uint(v[7])};
+        __builtin_nontemporal_store(
+            u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])},
+            reinterpret_cast<u32x4*>(p));
+        __builtin_nontemporal_store(
+            u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])},
+            reinterpret_cast<u32x4*>(p + 4));
         return;
     }
     // gfx950 converts two floats per instruction, rounding to nearest even
@@ -185,7 +188,10 @@ __device__ __forceinline__ void store_row8(void* base, size_t idx, const float (
         w[i] = dt == F16 ? __builtin_bit_cast(uint32_t, __builtin_convertvector(p, f16x2))
                          : __builtin_bit_cast(uint32_t, __builtin_convertvector(p, bf16x2));
     }
-    *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(base) + idx) = u32x4{w[0], w[1], w[2], w[3]};
+    // nontemporal: the rows stream through once (cfg 5b's 8192-row front end
+    // 37.0 -> 33.8 us, cfg 3's 6.15 -> 5.27 us against ordinary stores)
+    __builtin_nontemporal_store(u32x4{w[0], w[1], w[2], w[3]},
+                                reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(base) + idx));
 }
 
 __device__ __forceinline__ float lane_read(float v, int src_lane) {
