@@ -594,8 +594,9 @@ def bench_prefill_fp32(ctx, steps, warmup):
     T = 2048
     stream = torch.cuda.current_stream()
     res = {}
-    for name, kdt, vdt in (("fp32k_f16v", abi.F32, abi.F16), ("fp32", abi.F32, abi.F32)):
-        arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, T, kdt, vdt)
+    for name, kdt, vdt in (("fp32k_f16v", abi.F32, abi.F16), ("fp32", abi.F32, abi.F32),
+                           ("fp32k_tiered", abi.F32, abi.I8_TIERED)):
+        arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, T, kdt, vdt, value_window=256 if vdt == abi.I8_TIERED else 0)
         q = torch.empty((1, T, 16, 64), device="cuda:0")
         k = torch.empty((1, T, 8, 64), device="cuda:0")
         v = torch.empty_like(k)
@@ -616,7 +617,8 @@ def bench_prefill_fp32(ctx, steps, warmup):
                                   "frac": round(tflops / 157.3, 4), "traffic": None}}
         del arena, ws
         torch.cuda.empty_cache()
-    res["note"] = ("Granite causal prefill of 2048 tokens, fp32 queries and outputs; peak = dense fp32 MFMA "
+    res["note"] = ("Granite causal prefill of 2048 tokens, fp32 queries and outputs; fp32k_tiered: fp32 K with "
+                   "tiered values (f16 window of 256 rows, block INT8 below); peak = dense fp32 MFMA "
                    "(157.3 TFLOP/s); flop = 4*D*Hq*T(T+1)/2")
     return res
 

@@ -30,6 +30,8 @@
 // are in flight while the current one is computed.  Scores are scaled by
 // softmax scale x log2(e) in fp32 after the dot product and exponentiated
 // with v_exp_f32; the online softmax keeps per-column (m, l) in every lane.
+#include <type_traits>
+
 #include "common.h"
 #include "internal.h"
 #include "mfma.h"
@@ -43,6 +45,7 @@ constexpr int kD = 64;
 constexpr int kRowF = kD + 4;                  // padded fp32 row of a staged tile (floats)
 constexpr int kTileF = kPrefillTile * kRowF;   // floats per staged tile
 constexpr float kNegBigF = -1.0e30f;
+constexpr int kTierBlockF32 = 32;  // elements per INT8 scale block of a tiered value cache
 
 __device__ __forceinline__ f32x4 mma4(float a, float b, const f32x4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -83,6 +86,55 @@ template <int DT> struct TileIo {
     }
 };
 
+// The V tile of a tiered value cache: thread t widens elements 16 (t % 4)
+// .. + 15 of row t / 4 (half of one 32-element block).  A row below the
+// boundary is 16 INT8 codes times the block's f16 scale (exact in fp32), a
+// row at or above it 16 f16 values from its window slot.
+struct TieredTileIo {
+    static constexpr int EB = 1;  // bytes per element of `values` (the INT8 codes)
+    static constexpr int CH = 2;
+    __device__ __forceinline__ static uint32_t row_of(uint32_t tile, uint32_t kv_len, int tid) {
+        return min(tile * kPrefillTile + (uint32_t)(tid >> 2), kv_len - 1);
+    }
+    __device__ __forceinline__ static void load(u32x4 (&raw)[CH], const PrefillPipeArgs& a, uint32_t kvh,
+                                                uint32_t tile, uint32_t kv_len, int tid) {
+        const uint32_t row = row_of(tile, kv_len, tid);
+        const int col = 16 * (tid & 3);
+        if (row < a.tier) {
+            const size_t e = (size_t)kvh * a.head_stride + (size_t)row * kD + col;
+            raw[0] = load16<false>(reinterpret_cast<const int8_t*>(a.values) + e);
+            raw[1] = u32x4{(uint32_t)a.value_scales[e / kTierBlockF32], 0u, 0u, 0u};
+        } else {
+            const uint16_t* w =
+                a.value_ring + (size_t)kvh * a.ring_head_stride + (size_t)(row & a.window_mask) * kD + col;
+            raw[0] = load16<false>(w);
+            raw[1] = load16<false>(w + 8);
+        }
+    }
+    __device__ __forceinline__ static void store(const u32x4 (&raw)[CH], float* lds, const PrefillPipeArgs& a,
+                                                 uint32_t tile, uint32_t kv_len, int tid) {
+        float f[16];
+        if (row_of(tile, kv_len, tid) < a.tier) {
+            const float sc = (float)__builtin_bit_cast(half_t, (uint16_t)raw[1][0]);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int32_t code = (int32_t)(raw[0][i >> 2] << (24 - 8 * (i & 3))) >> 24;
+                f[i] = (float)code * sc;
+            }
+        } else {
+            Unpack<F16>::run(raw[0], f);
+            float g[8];
+            Unpack<F16>::run(raw[1], g);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) f[8 + i] = g[i];
+        }
+        float* dst = lds + (tid >> 2) * kRowF + 16 * (tid & 3);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            *reinterpret_cast<f32x4*>(dst + 4 * r) = f32x4{f[4 * r], f[4 * r + 1], f[4 * r + 2], f[4 * r + 3]};
+    }
+};
+
 // 16 consecutive elements of a query row in its dtype, widened.
 __device__ __forceinline__ void load_q16(const void* base, size_t idx, int dt, float (&q)[16]) {
     if (dt == F32) {
@@ -118,7 +170,7 @@ __device__ __forceinline__ void load_q16(const void* base, size_t idx, int dt, f
 template <int KDT, int VDT>
 __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillPipeArgs a) {
     using KIo = TileIo<KDT>;
-    using VIo = TileIo<VDT>;
+    using VIo = std::conditional_t<VDT == I8T, TieredTileIo, TileIo<VDT == I8T ? F16 : VDT>>;
     __shared__ __attribute__((aligned(16))) float lds[2][2][kTileF];  // [stage][K, V]
 
     const int tid = threadIdx.x;
@@ -163,10 +215,19 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillPipeArgs a) 
     const char* kbase = reinterpret_cast<const char*>(a.keys) + (size_t)kvh * a.head_stride * KIo::EB;
     const char* vbase = reinterpret_cast<const char*>(a.values) + (size_t)kvh * a.head_stride * VIo::EB;
 
+    auto vload = [&](u32x4 (&raw)[VIo::CH], uint32_t tile) __attribute__((always_inline)) {
+        if constexpr (VDT == I8T) VIo::load(raw, a, kvh, tile, kv_len, tid);
+        else VIo::load(raw, vbase, tile, kv_len, tid);
+    };
+    auto vstore = [&](const u32x4 (&raw)[VIo::CH], float* dst, uint32_t tile) __attribute__((always_inline)) {
+        if constexpr (VDT == I8T) VIo::store(raw, dst, a, tile, kv_len, tid);
+        else VIo::store(raw, dst, tid);
+    };
+
     // tile 0 of the chunk into stage 0; the query loads go out behind it
     u32x4 kraw[KIo::CH], vraw[VIo::CH];
     KIo::load(kraw, kbase, t0, kv_len, tid);
-    VIo::load(vraw, vbase, t0, kv_len, tid);
+    vload(vraw, t0);
 
     // Q^T operands: lane (g, i) holds dims 16g .. 16g + 15 of column i
     float q[2][16];
@@ -177,7 +238,7 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillPipeArgs a) 
             load_q16(a.query, ((size_t)qr * a.q_heads + (size_t)kvh * 2 + nt) * kD + 16 * lg, a.query_dtype, q[nt]);
     }
     KIo::store(kraw, lds[0][0], tid);
-    VIo::store(vraw, lds[0][1], tid);
+    vstore(vraw, lds[0][1], t0);
     __syncthreads();
 
     f32x4 oacc[4][2];  // [output block db][head nt]
@@ -252,12 +313,12 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillPipeArgs a) 
         const bool more = r + 1 < m;
         if (more) {  // the next tile's loads are in flight during this tile's math
             KIo::load(kraw, kbase, t0 + r + 1, kv_len, tid);
-            VIo::load(vraw, vbase, t0 + r + 1, kv_len, tid);
+            vload(vraw, t0 + r + 1);
         }
         if (r < wave_m) compute(lds[st][0], lds[st][1], t0 + r);
         if (more) {  // the other stage was last read in round r - 1, before its barrier
             KIo::store(kraw, lds[st ^ 1][0], tid);
-            VIo::store(vraw, lds[st ^ 1][1], tid);
+            vstore(vraw, lds[st ^ 1][1], t0 + r + 1);
         }
         __syncthreads();
     }
@@ -311,7 +372,10 @@ constexpr uint32_t kF32MaxChunks = 32;
 constexpr uint32_t kF32Columns = 128;
 
 bool prefill_f32_supported(const ShapeDims& s, int key_dtype, int value_dtype) {
-    if (s.head_dim != kD || s.group != 2 || value_dtype == I8T) return false;
+    if (s.head_dim != kD || s.group != 2) return false;
+    // tiered values with fp32 keys: the reference's proposed plan (16-bit
+    // keys with tiered values take the pipelined kernel)
+    if (value_dtype == I8T) return key_dtype == F32;
     return key_dtype == F32 || value_dtype == F32;
 }
 
@@ -352,6 +416,11 @@ hipError_t launch_prefill_f32(const ShapeDims& s, const KvLayer& kv, uint32_t st
     a.query_dtype = query_dtype;
     a.keys = kv.keys;
     a.values = kv.values;
+    a.value_scales = reinterpret_cast<const uint16_t*>(kv.value_scales);
+    a.value_ring = reinterpret_cast<const uint16_t*>(kv.value_ring);
+    a.ring_head_stride = kv.ring_head_stride;
+    a.window_mask = kv.window ? kv.window - 1 : 0;
+    a.tier = kv.tier;
     a.out = out;
     a.head_stride = kv.head_stride;
     a.start = start;
@@ -375,6 +444,7 @@ hipError_t launch_prefill_f32(const ShapeDims& s, const KvLayer& kv, uint32_t st
     if (kd == F32 && vd == F32) hipLaunchKernelGGL((prefill_f32_kernel<F32, F32>), grid, dim3(256), 0, st, a);
     else if (kd == F32 && vd == F16) hipLaunchKernelGGL((prefill_f32_kernel<F32, F16>), grid, dim3(256), 0, st, a);
     else if (kd == F32 && vd == BF16) hipLaunchKernelGGL((prefill_f32_kernel<F32, BF16>), grid, dim3(256), 0, st, a);
+    else if (kd == F32 && vd == I8T) hipLaunchKernelGGL((prefill_f32_kernel<F32, I8T>), grid, dim3(256), 0, st, a);
     else if (kd == F16 && vd == F32) hipLaunchKernelGGL((prefill_f32_kernel<F16, F32>), grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL((prefill_f32_kernel<BF16, F32>), grid, dim3(256), 0, st, a);
     *dispatches = 1;

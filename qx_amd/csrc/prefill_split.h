@@ -41,6 +41,14 @@ struct PrefillPipeArgs {
     // queries in any dtype; the pipelined kernel uses neither field
     const void* values;    // [Hkv][cap][D] of this layer and sequence
     int query_dtype;
+    // tiered values (QXH_I8_TIERED) on the fp32 kernel: `values` holds the
+    // INT8 codes, one f16 scale per 32 elements, the f16 window of
+    // window_mask + 1 rows per kv head; positions below `tier` are INT8
+    const uint16_t* value_scales;
+    const uint16_t* value_ring;
+    uint64_t ring_head_stride;  // elements
+    uint32_t window_mask;
+    uint32_t tier;
 };
 
 // Column c (0 .. 32 NW - 1) of a workgroup: wave c / 32, block nt =

@@ -100,3 +100,27 @@ def test_f32_prefill_equals_decode_rows_of_the_same_cache(ctx):
     whole = whole.cpu().numpy()
     rms = np.sqrt(np.mean(parts.astype(np.float64) ** 2))
     assert np.max(np.abs(whole - parts)) / rms <= 1e-5
+
+
+@pytest.mark.parametrize("start,T,W", [(0, 300, 64), (500, 100, 256), (37, 129, 32)])
+def test_f32_prefill_on_tiered_values(ctx, start, T, W):
+    """fp32 keys with tiered values (recent rows f16, older rows block INT8:
+    the reference's proposed plan, docs/qx-structural-memory-2026-08-25.md:
+    69-74) on the fp32 kernel: each V tile row widened from its tier (INT8
+    code x block scale, exact in fp32, or the f16 window slot), against the
+    oracle over the values the cache holds (the dequantised gather)."""
+    cap = start + T
+    rng = np.random.default_rng(cap + W)
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, cap, abi.F32, abi.I8_TIERED, value_window=W)
+    q = torch.from_numpy(rng.standard_normal((T, 16, 64), dtype=np.float32)).cuda()
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=W, length=cap)
+        out = rt.prefill_attention(g, arena, 0, start, q)
+        kk, vv = arena.gather(g, 0, 0, 0, cap)
+    assert arena.value_tier() == max(0, cap - W)
+    kf, vf = kk.float().cpu().numpy(), vv.float().cpu().numpy()
+    ref = O.KvCache(cap)
+    ref.extend(kf, vf)
+    rows = rows_to_check(T, rng, first=8, last=8, rand=16)
+    e, e64 = check_rows(q.cpu().numpy(), out.cpu().numpy(), ref, kf, vf, start, rows)
+    log(f"f32 prefill tiered W={W} start {start} T {T}: vs oracle {e:.2e}, vs float64 {e64:.2e}")
