@@ -571,7 +571,7 @@ def bench_prefill(ctx, steps, warmup, shape_name):
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
                          "frac": round(tflops / peak, 4), "traffic": None},
             "frontend": {"us": round(ms_fe * 1000.0, 2), "bytes": fe_bytes,
-                         "roofline": roofline_hbm(fe_bytes, ms_fe, None),
+                         "roofline": roofline_hbm(fe_bytes, ms_fe, load_traffic(f"{shape_name}_frontend")),
                          "note": "RoPE of q and k" + (" after per-head RMSNorm" if shape != abi.SHAPE_GRANITE else "") +
                                  ", K/V append of every prompt row, one launch (qxh_encode_rope_kv_batch); bytes = "
                                  f"q, k, v read + rotated q, cache K, cache V written; {nsets} input sets rotated "
