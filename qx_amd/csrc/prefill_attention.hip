@@ -31,7 +31,9 @@ constexpr uint32_t kExactPassWgs = 256;
 // prefix, split over the CUs like a decode.  That is quadratic in bytes for
 // long prompts but has no fixed cost beyond a decode's, while the pipelined
 // MFMA prefill (equal 16-bit K/V) first rewrites the layer's whole V prefix
-// into the f16 V^T scratch.  Measured per call (us; causal rows / pipelined):
+// into the f16 V^T scratch (bf16 and Qwen-shape caches; Granite f16 caches
+// skip that pass).  Measured per call (us; causal rows / pipelined, the
+// Granite figure with the pre-pass):
 // Qwen bf16 at 1020 cached positions 14 / 31 for 1-8 rows, 31 / 32 for 63;
 // at 8188, 42 / 56 for 16 rows; at 32764, 19 / 71 for one row, 71 / 71 for 8,
 // 142 / 69 for 16.  Granite f16 at 3840: 18 / 17 for 16 rows, 48 / 20 for 63.

@@ -2,10 +2,13 @@
 //
 // Two kernels per call:
 //
-// 1. prefill_vt_kernel: the layer's V rows [0, kv_len) of each kv head are
-//    rewritten once into an f16 V^T scratch, [kv_head][tile][d][64], so that
-//    the P.V operand of a lane (16 contiguous bytes) is one ds_read_b128
-//    instead of two transposed 8-byte reads.  Within each 32-position half of
+// 1. prefill_vt_kernel (bf16 caches, tiered values and Qwen-shape f16 caches):
+//    the layer's V rows [0, kv_len) of each kv head are rewritten once into
+//    an f16 V^T scratch, [kv_head][tile][d][64], so that the P.V operand of a
+//    lane (16 contiguous bytes) is one ds_read_b128 instead of two transposed
+//    8-byte reads.  Granite-shape f16 caches skip it: their main kernel stages
+//    the cache's own V rows and reads the operand with two ds_read_b64_tr_b16
+//    (DIRECT_V below).  Within each 32-position half of
 //    a 64-position tile the slots are permuted the way the Q.K accumulator
 //    leaves probabilities in lanes: slot 8g+j (j < 4) holds position 4g+j and
 //    slot 8g+4+j holds position 16+4g+j.  bf16 values are rounded to f16
@@ -27,6 +30,13 @@
 //    independent workgroups per CU instead: Qwen runs two 4-wave workgroups
 //    per query block (heads 0-3 and 4-7 of the group, 64 KB of LDS each, so
 //    two share a CU and drift against each other), Granite three.
+//
+// DIRECT_V (Granite f16): a V tile is staged row-major like K, 16-byte
+// chunks XOR-swizzled by (row & 7), and each P.V operand is two transposed
+// 8-byte reads (rows 4g.. and 16+4g.. of a 32-position half): lane (g, i)
+// then holds the eight positions whose probabilities a 16x16 S^T block
+// leaves in lane (g, i), the slot order the V^T pre-pass writes.  For one
+// operand read the 16 rows of a half-wave fall on distinct banks.
 //
 // Stage r (K tile r, V^T tile r-1) is read only in the MFMA phase of round
 // r.  With three stages (Granite) its loads are issued at the start of
@@ -223,7 +233,7 @@ __global__ __launch_bounds__(D) void prefill_vt_tiered_kernel(TieredVtArgs a) {
 // NW = 4 waves): nt selects the head, wave w covers tokens 16w .. of the
 // workgroup's 64; three such workgroups share a CU (under 168 VGPRs, 48 KB
 // LDS) and overlap each other's phases.
-template <int D, int DT, int HEADS_PER_WAVE, int NW, int HALVES = 1>
+template <int D, int DT, int HEADS_PER_WAVE, int NW, int HALVES = 1, bool DIRECT_V = false>
 __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void prefill_pipe_kernel(PrefillPipeArgs a) {
     using M = MfmaT<DT>;
     using MH = MfmaT<F16>;
@@ -245,6 +255,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
     constexpr int STAGES = HALVES == 2 ? 2 : 3;             // LDS ring depth
     static_assert(LPW * NW == KI + VI, "stage loads must split evenly over the waves");
     static_assert(HALVES == 1 || (HEADS_PER_WAVE == 1 && NW == 4), "halves: Qwen, 4 waves");
+    static_assert(!DIRECT_V || (D == 64 && DT == F16), "row-major V tiles: Granite f16 caches");
 
     __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGEB];
 
@@ -314,7 +325,25 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
     }
 
     const char* kbase = reinterpret_cast<const char*>(a.keys) + (size_t)kvh * a.head_stride * 2;
-    const char* vtbase = reinterpret_cast<const char*>(a.vt) + (size_t)kvh * a.vt_tiles * VTILEB;
+    const char* vtbase = DIRECT_V ? reinterpret_cast<const char*>(a.values) + (size_t)kvh * a.head_stride * 2
+                                  : reinterpret_cast<const char*>(a.vt) + (size_t)kvh * a.vt_tiles * VTILEB;
+
+    // DIRECT_V: the last tile's rows at or past kv_len are not loaded.  Their
+    // probabilities are zero, and so is every probability of round 0's P.V
+    // (which reads slot 0), so when this workgroup reaches a partial last
+    // tile the V halves of all slots are cleared first: stale LDS bits can
+    // then never meet a zero probability as inf or NaN.
+    if constexpr (DIRECT_V) {
+        if (t1 == n && kv_len % kTile != 0) {
+#pragma unroll
+            for (int sl = 0; sl < STAGES; ++sl)
+#pragma unroll
+                for (int k = 0; k < VTILEB / (64 * NW * 16); ++k)
+                    *reinterpret_cast<u32x4*>(lds + sl * STAGEB + KTILEB + (k * 64 * NW + tid) * 16) =
+                        u32x4{0u, 0u, 0u, 0u};
+            __syncthreads();
+        }
+    }
 
     // Direct loads: stage load j (1 KB) is issued by wave j / LPW, so a wave
     // issues only K loads (j < KI: RPI rows of the K tile each) or only V^T
@@ -335,11 +364,29 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
             const int row = j * RPI + lane / KCH;
             const int swz = D == 128 ? (row & 15) : ((row >> 1) & 7);
             ld_off[k] = (uint32_t)(row * KROWB + ((lane % KCH) ^ swz) * 16);
+        } else if (DIRECT_V) {
+            const int row = (j - KI) * RPI + lane / KCH;
+            ld_off[k] = (uint32_t)(row * KROWB + ((lane % KCH) ^ (row & 7)) * 16);
         } else {
             const int d = (j - KI) * 8 + (lane >> 3);
             ld_off[k] = (uint32_t)(d * 128 + ((lane & 7) ^ ((d >> 1) & 7)) * 16);
         }
     }
+    // DIRECT_V: K and V tiles are staged by the same code, and the compiler
+    // would merge the two branches below into a per-lane select of the buffer
+    // resource (a waterfall loop around every load); reading the resource's
+    // base and size through readfirstlane keeps it in scalar registers
+    auto tile_rsrc = [](const char* base, uint32_t bytes) __attribute__((always_inline)) {
+        if constexpr (DIRECT_V) {
+            const uint64_t p = reinterpret_cast<uint64_t>(base);
+            const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+            const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+            return make_rsrc(reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo),
+                             __builtin_amdgcn_readfirstlane(bytes));
+        } else {
+            return make_rsrc(base, bytes);
+        }
+    };
     auto issue_stage = [&](uint32_t r) __attribute__((always_inline)) {
         // the slot offset passes through an empty asm so that the compiler
         // derives the eight LDS destinations in the round (scalar adds)
@@ -349,12 +396,14 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
         char* sb = lds + sb_off;
         if (k_wave) {
             const uint32_t kt = t0 + min(r, m - 1);
-            const __amdgpu_buffer_rsrc_t rs = make_rsrc(kbase + (size_t)kt * KTILEB, (kv_len - kt * kTile) * KROWB);
+            const __amdgpu_buffer_rsrc_t rs = tile_rsrc(kbase + (size_t)kt * KTILEB, (kv_len - kt * kTile) * KROWB);
 #pragma unroll
             for (int k = 0; k < LPW; ++k) lds_dma16(rs, ld_off[k], sb + (wave * LPW + k) * 1024);
         } else {
             const uint32_t vtile = t0 + (r == 0 ? 0u : min(r - 1, m - 1));
-            const __amdgpu_buffer_rsrc_t rs = make_rsrc(vtbase + (size_t)vtile * VTILEB, VTILEB);
+            const __amdgpu_buffer_rsrc_t rs =
+                DIRECT_V ? tile_rsrc(vtbase + (size_t)vtile * KTILEB, (kv_len - vtile * kTile) * KROWB)
+                         : tile_rsrc(vtbase + (size_t)vtile * VTILEB, VTILEB);
 #pragma unroll
             for (int k = 0; k < LPW; ++k) lds_dma16(rs, ld_off[k], sb + KTILEB + (wave * LPW + k - KI) * 1024);
         }
@@ -413,6 +462,19 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
         // operand i: PV (i < NPV): half = i / DTILES, dt = i % DTILES;
         //            QK: ks = (i - NPV) / 4, mt = (i - NPV) % 4
         auto read = [&](int i) -> u32x4 {
+            if (DIRECT_V && i < NPV) {
+                // rows 32*half + 4*lg + li/4 (and 16 on; same swizzle), dims
+                // 16*dt + 4*(li%4): bytes 32*dt + 8*(li%4) of the row
+                const int half = i / DTILES, dt = i % DTILES;
+                const int row = 32 * half + 4 * lg + (li >> 2);
+                const int col = 32 * dt + 8 * (li & 3);
+                const char* p0 = st + KTILEB + row * KROWB + ((((col >> 4) ^ (row & 7)) << 4) | (col & 15));
+                const lds_i16x4* q0 = (const lds_i16x4*)p0;
+                const lds_i16x4* q1 = (const lds_i16x4*)(p0 + 16 * KROWB);
+                const i16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(q0));
+                const i16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(q1));
+                return __builtin_bit_cast(u32x4, __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7));
+            }
             if (i < NPV) {
                 const int half = i / DTILES, dt = i % DTILES;
                 const int d = 16 * dt + li;
@@ -455,15 +517,23 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
         // then the tail.  Operand i feeds 2 MFMAs, or 4 for the last V^T
         // operand of each half (the row-sum MFMAs ride along).
         constexpr auto nmfma = [](int i) constexpr { return (i < NPV && i % DTILES == DTILES - 1) ? 4 : 2; };
+        // LDS reads per operand: a row-major V operand takes two
+        constexpr auto nds = [](int i) constexpr { return (DIRECT_V && i < NPV) ? 2 : 1; };
+        constexpr int HEAD = [&]() constexpr {
+            int t = 0;
+            for (int i = 0; i < PREF; ++i) t += nds(B0 + i);
+            return t;
+        }();
         constexpr int TAIL = [&]() constexpr {
             int t = 0;
             for (int i = N - PREF; i < N; ++i) t += nmfma(B0 + i);
             return t;
         }();
-        __builtin_amdgcn_sched_group_barrier(0x100, PREF, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, HEAD, 0);
 #pragma unroll
         for (int i = 0; i < N - PREF; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (nds(B0 + i + PREF) == 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             if (nmfma(B0 + i) == 4) __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
             else __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
         }
@@ -718,6 +788,9 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
     dim3 vgrid(tiles, s.kv_heads);
     const bool bf = dtype == BF16;
     const bool tiered = kv.value_dtype == I8T;
+    // Granite f16 caches take no pre-pass: the main kernel reads the cache's
+    // V rows itself
+    const bool direct_v = !tiered && !bf && s.head_dim == 64;
     if (tiered) {
         TieredVtArgs ta{reinterpret_cast<const int8_t*>(kv.values), reinterpret_cast<const uint16_t*>(kv.value_scales),
                         reinterpret_cast<const uint16_t*>(kv.value_ring), vt, kv.head_stride, kv.ring_head_stride,
@@ -728,15 +801,15 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
         VtArgs va{kv.values, vt, flags, kv.head_stride, vt_tiles, kv_len};
         if (bf) hipLaunchKernelGGL((prefill_vt_kernel<128, BF16>), vgrid, dim3(128), 0, st, va);
         else hipLaunchKernelGGL((prefill_vt_kernel<128, F16>), vgrid, dim3(128), 0, st, va);
-    } else {
+    } else if (!direct_v) {
         VtArgs va{kv.values, vt, flags, kv.head_stride, vt_tiles, kv_len};
-        if (bf) hipLaunchKernelGGL((prefill_vt_kernel<64, BF16>), vgrid, dim3(64), 0, st, va);
-        else hipLaunchKernelGGL((prefill_vt_kernel<64, F16>), vgrid, dim3(64), 0, st, va);
+        hipLaunchKernelGGL((prefill_vt_kernel<64, BF16>), vgrid, dim3(64), 0, st, va);
     }
 
     PrefillPipeArgs a{};
     a.query = query;
     a.keys = kv.keys;
+    a.values = kv.values;
     a.vt = vt;
     a.flags = bf && !tiered ? flags : nullptr;
     a.out = out;
@@ -766,15 +839,15 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
         else hipLaunchKernelGGL((prefill_pipe_kernel<128, F16, 1, 4, 2>), grid, dim3(256), 0, st, a);
     } else {
         if (bf) hipLaunchKernelGGL((prefill_pipe_kernel<64, BF16, 2, 4>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((prefill_pipe_kernel<64, F16, 2, 4>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((prefill_pipe_kernel<64, F16, 2, 4, 1, true>), grid, dim3(256), 0, st, a);
     }
-    *dispatches = 2;
+    *dispatches = direct_v ? 1 : 2;
     if (chunks > 1) {
         const uint32_t cpb = 256 / (s.head_dim / 4);
         dim3 cgrid(a.qblocks * s.kv_heads, pipe_columns(s) / cpb);
         if (s.head_dim == 128) hipLaunchKernelGGL((prefill_combine_kernel<128, 1, 8>), cgrid, dim3(256), 0, st, a);
         else hipLaunchKernelGGL((prefill_combine_kernel<64, 2, 4>), cgrid, dim3(256), 0, st, a);
-        *dispatches = 3;
+        *dispatches += 1;
     }
     return hipGetLastError();
 }
