@@ -245,3 +245,40 @@ def test_k_wide_verifier_with_rollback(ctx, shape, dtype):
     n = L0 + accepted
     assert np.array_equal(bits(kk2[:n]), bits(kk1[:n])) and np.array_equal(bits(vv2[:n]), bits(vv1[:n]))
     assert not np.array_equal(bits(kk2[n:n + K - accepted]), bits(kk1[n:]))
+
+
+TORCH = {abi.F32: torch.float32, abi.F16: torch.float16, abi.BF16: torch.bfloat16}
+
+
+# Every prefill path, with the prompt ending inside a 64-position tile:
+# Granite f16 (V tiles read straight from the cache; one chunk, then two),
+# Granite bf16 and Qwen bf16 (V^T pre-pass), Fp32KFp16V (fp32 matrix-core
+# kernel; one chunk, then several) and a few rows (causal decode rows).
+@pytest.mark.parametrize("shape,kdt,vdt,start,T", [
+    (abi.SHAPE_GRANITE, abi.F16, abi.F16, 0, 300), (abi.SHAPE_GRANITE, abi.F16, abi.F16, 1000, 100),
+    (abi.SHAPE_GRANITE, abi.BF16, abi.BF16, 0, 300), (abi.SHAPE_QWEN3, abi.BF16, abi.BF16, 0, 300),
+    (abi.SHAPE_GRANITE, abi.F32, abi.F16, 0, 300), (abi.SHAPE_GRANITE, abi.F32, abi.F16, 1000, 100),
+    (abi.SHAPE_GRANITE, abi.F16, abi.F16, 37, 6)])
+def test_prefill_ignores_cache_rows_past_the_prompt(ctx, shape, kdt, vdt, start, T):
+    """Rows at and past start + T are outside every prompt row's causal
+    range, whatever they hold: with NaN there (appended after the prompt's
+    rows, so the cache's length covers them) the output is finite and bit for
+    bit the output over finite rows there.  The last tile's tail is neither
+    read into a score nor multiplied by a zero probability."""
+    kv_len, extra = start + T, 40
+    log("prefill with NaN past the prompt", shape, kdt, vdt, start, T)
+    heads, kvh, d = (16, 8, 64) if shape == abi.SHAPE_GRANITE else (32, 4, 128)
+    rng = np.random.default_rng(kv_len + 7 * kdt)
+    q = torch.from_numpy(rng.standard_normal((T, heads, d), dtype=np.float32)).cuda().to(TORCH[kdt])
+    outs = []
+    for nan_tail in (False, True):
+        arena = rt.KvArena(ctx, shape, 1, 1, kv_len + extra, kdt, vdt)
+        with rt.Graph(ctx) as g:
+            arena.fill_normal(g, seed=9, length=kv_len if nan_tail else kv_len + extra)
+            if nan_tail:
+                nan = torch.full((1, extra, kvh, d), float("nan"), dtype=TORCH[kdt], device="cuda:0")
+                rt.rope_kv_batch(g, arena, 0, kv_len, None, nan, nan)
+            outs.append(rt.prefill_attention(g, arena, 0, start, q, out_dtype=torch.float32))
+        assert arena.len() == kv_len + extra
+    assert torch.isfinite(outs[1]).all()
+    assert torch.equal(outs[0], outs[1])
