@@ -507,8 +507,13 @@ def qwen_gqa_attention(query_bits, key_cache_bits, value_cache_bits, fmt: int = 
     return (out, of) if want_f32 else out
 
 
-def qwen_prefill_rows(query_bits, key_cache_bits, value_cache_bits, start: int, rows, fmt: int = F16):
-    """Repeated-decode causal prefill for Qwen; returns (bits, f32) for `rows`."""
+def qwen_prefill_rows(query_bits, key_cache_bits, value_cache_bits, start: int, rows, fmt: int = F16,
+                      workers: int = 1):
+    """Repeated-decode causal prefill for Qwen; returns (bits, f32) for `rows`.
+
+    workers > 1 splits the rows over that many threads (each row is an
+    independent C call that holds no state between calls; ctypes releases
+    the GIL while it runs), for samples of long prompts."""
     q = np.ascontiguousarray(query_bits, dtype=np.uint16)
     kc = np.ascontiguousarray(key_cache_bits, dtype=np.uint16)
     vc = np.ascontiguousarray(value_cache_bits, dtype=np.uint16)
@@ -516,8 +521,26 @@ def qwen_prefill_rows(query_bits, key_cache_bits, value_cache_bits, start: int, 
     n = QWEN_Q_HEADS * QWEN_HEAD_DIM
     out = np.zeros((rows.size, n), np.uint16)
     of = np.zeros((rows.size, n), np.float32)
-    _check(lib().qxo_qwen_prefill_rows(_p(q, _u16p), _p(kc, _u16p), _p(vc, _u16p), start, _p(rows, _u32p),
-                                       rows.size, fmt, _p(out, _u16p), _p(of)))
+
+    def run(idx):
+        r = np.ascontiguousarray(rows[idx])
+        o = np.zeros((r.size, n), np.uint16)
+        f = np.zeros((r.size, n), np.float32)
+        status = lib().qxo_qwen_prefill_rows(_p(q, _u16p), _p(kc, _u16p), _p(vc, _u16p), start, _p(r, _u32p),
+                                             r.size, fmt, _p(o, _u16p), _p(f))
+        out[idx], of[idx] = o, f
+        return status
+
+    w = max(1, min(workers, rows.size))
+    if w == 1:
+        _check(run(np.arange(rows.size)))
+        return out, of
+    import concurrent.futures as cf
+    # rows dealt round-robin, so long and short rows spread over the threads
+    with cf.ThreadPoolExecutor(w) as ex:
+        codes = list(ex.map(lambda i: run(np.arange(i, rows.size, w)), range(w)))
+    for c in codes:
+        _check(c)
     return out, of
 
 

@@ -25,6 +25,19 @@ def rel_err(got, ref) -> float:
     return float(np.max(np.abs(got - ref))) / max(rms, 1e-30)
 
 
+def row_rel_err(got, ref) -> float:
+    """The bar per attention output: max over rows of max |got - ref| / rms(ref
+    row), rows along the first axis.  A prefill row is the decode output at
+    its position (the reference runs a prompt as repeated decode), held to
+    the bar of its own RMS as every decode output is; one RMS over rows of
+    very different lengths would let the long rows' small outputs set the
+    scale for the short rows' large ones."""
+    got = np.asarray(got, dtype=np.float64).reshape(np.shape(got)[0], -1)
+    ref = np.asarray(ref, dtype=np.float64).reshape(got.shape)
+    rms = np.sqrt(np.mean(ref * ref, axis=1))
+    return float(np.max(np.max(np.abs(got - ref), axis=1) / np.maximum(rms, 1e-30)))
+
+
 def attend64(q, keys, values, scale):
     """float64 GQA attention: q [Hq][D], keys/values [L][Hkv][D]."""
     out = np.zeros(q.shape)

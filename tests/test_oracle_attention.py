@@ -266,6 +266,12 @@ def test_qwen_prefill_rows_equal_decode():
     bits, _ = O.qwen_prefill_rows(q, kc, vc, 0, rows)
     for i, t in enumerate(rows):
         assert np.array_equal(bits[i], O.qwen_gqa_attention(q[t], kc[:t + 1], vc[:t + 1]))
+    # rows dealt over threads come back in order, bit for bit
+    many = [8, 0, 5, 3, 3, 7, 1]
+    b1, f1 = O.qwen_prefill_rows(q, kc, vc, 0, many)
+    b4, f4 = O.qwen_prefill_rows(q, kc, vc, 0, many, workers=4)
+    assert np.array_equal(b1, b4) and np.array_equal(f1, f4)
+    assert np.array_equal(b1[1], bits[0]) and np.array_equal(b1[3], bits[1]) and np.array_equal(b1[0], bits[2])
 
 
 def test_oracle_rounding_against_exact_attention_grows_past_the_fp32_bar():
