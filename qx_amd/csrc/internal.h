@@ -132,15 +132,16 @@ bool block_decode_fused(int key_dtype, int value_dtype);
 DecodePlan plan_block_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t length);
 hipError_t launch_block_decode_attention(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t length,
                                          const float* query, float* out, void* workspace, hipStream_t st);
-// pipelined path (prefill_pipelined.hip): V^T pre-pass + pipelined MFMA kernel
+// pipelined path (prefill_pipelined.hip): V^T pre-pass (not for Granite f16
+// caches) + pipelined MFMA kernel
 bool prefill_pipe_supported(const ShapeDims& s);
 uint32_t prefill_pipe_vt_tiles(uint32_t capacity);
-uint64_t prefill_pipe_workspace_bytes(const ShapeDims& s, uint32_t capacity, uint32_t tokens);
+uint64_t prefill_pipe_workspace_bytes(const ShapeDims& s, int value_dtype, uint32_t capacity, uint32_t tokens);
 hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t start, uint32_t tokens, const void* query,
                              int dtype, void* out, int out_dtype, void* workspace, hipStream_t st, int* dispatches);
 // fp32 matrix-core path (prefill_f32.hip): Granite shape, fp32 or mixed K/V
 bool prefill_f32_supported(const ShapeDims& s, int key_dtype, int value_dtype);
-uint64_t prefill_f32_workspace_bytes(const ShapeDims& s, uint32_t tokens);
+uint64_t prefill_f32_workspace_bytes(const ShapeDims& s, uint32_t capacity, uint32_t tokens);
 hipError_t launch_prefill_f32(const ShapeDims& s, const KvLayer& kv, uint32_t start, uint32_t tokens, const void* query,
                               int query_dtype, void* out, int out_dtype, void* workspace, hipStream_t st,
                               int* dispatches);

@@ -75,11 +75,11 @@ uint64_t prefill_workspace_bytes(const ShapeDims& s, int key_dtype, int value_dt
                              prefill_pipe_supported(s);
     const uint64_t rows = decode_causal_workspace_bound(s, key_dtype, value_dtype, capacity, tokens);
     if (prefill_f32_supported(s, key_dtype, value_dtype) && tokens > kDecodeRowsAlways) {
-        const uint64_t f32 = prefill_f32_workspace_bytes(s, tokens);
+        const uint64_t f32 = prefill_f32_workspace_bytes(s, capacity, tokens);
         return rows > f32 ? rows : f32;
     }
     if (!pipe_dtypes || tokens <= kDecodeRowsAlways) return rows;
-    const uint64_t pipe = prefill_pipe_workspace_bytes(s, capacity, tokens);
+    const uint64_t pipe = prefill_pipe_workspace_bytes(s, value_dtype, capacity, tokens);
     return tokens < 64 && rows > pipe ? rows : pipe;
 }
 

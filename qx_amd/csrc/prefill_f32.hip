@@ -383,15 +383,19 @@ static uint32_t f32_blocks(const ShapeDims& s, uint32_t tokens) {
     return (tokens + kPrefillTile - 1) / kPrefillTile * s.kv_heads;
 }
 
-static uint32_t f32_max_chunks(const ShapeDims& s, uint32_t tokens) {
+// most chunks a block can take in a cache of `capacity` positions
+static uint32_t f32_max_chunks(const ShapeDims& s, uint32_t tokens, uint32_t capacity) {
     const uint32_t wgs = f32_blocks(s, tokens);
     if (wgs >= kF32TargetWgs) return 1;
-    const uint32_t want = (kF32TargetWgs + wgs - 1) / wgs;
-    return want < kF32MaxChunks ? want : kF32MaxChunks;
+    uint32_t want = (kF32TargetWgs + wgs - 1) / wgs;
+    if (want > kF32MaxChunks) want = kF32MaxChunks;
+    const uint32_t fit = (capacity + kPrefillTile - 1) / kPrefillTile / kF32MinChunkTiles;
+    if (want > fit) want = fit;
+    return want < 1 ? 1 : want;
 }
 
-static uint32_t f32_chunk_tiles(const ShapeDims& s, uint32_t start, uint32_t tokens) {
-    const uint32_t want = f32_max_chunks(s, tokens);
+static uint32_t f32_chunk_tiles(const ShapeDims& s, uint32_t start, uint32_t tokens, uint32_t capacity) {
+    const uint32_t want = f32_max_chunks(s, tokens, capacity);
     const uint32_t n_max = (start + tokens + kPrefillTile - 1) / kPrefillTile;
     const uint32_t fit = n_max / kF32MinChunkTiles;
     const uint32_t chunks = want < fit ? want : fit;
@@ -399,8 +403,8 @@ static uint32_t f32_chunk_tiles(const ShapeDims& s, uint32_t start, uint32_t tok
     return (n_max + chunks - 1) / chunks;
 }
 
-uint64_t prefill_f32_workspace_bytes(const ShapeDims& s, uint32_t tokens) {
-    const uint32_t mc = f32_max_chunks(s, tokens);
+uint64_t prefill_f32_workspace_bytes(const ShapeDims& s, uint32_t capacity, uint32_t tokens) {
+    const uint32_t mc = f32_max_chunks(s, tokens, capacity);
     if (mc <= 1) return 0;
     const uint64_t slots = (uint64_t)f32_blocks(s, tokens) * mc * kF32Columns;
     return slots * (2 + kD) * sizeof(float);
@@ -432,8 +436,8 @@ hipError_t launch_prefill_f32(const ShapeDims& s, const KvLayer& kv, uint32_t st
     a.kv_heads = s.kv_heads;
     a.qblocks = (tokens + kPrefillTile - 1) / kPrefillTile;
     a.xcd_map = (8 % s.kv_heads == 0) && ((uint64_t)a.qblocks * s.kv_heads) % 8 == 0;
-    a.chunk_tiles = f32_chunk_tiles(s, start, tokens);
-    a.max_chunks = f32_max_chunks(s, tokens);
+    a.chunk_tiles = f32_chunk_tiles(s, start, tokens, kv.capacity);
+    a.max_chunks = f32_max_chunks(s, tokens, kv.capacity);
     const uint64_t slots = (uint64_t)a.qblocks * s.kv_heads * a.max_chunks * kF32Columns;
     a.part_ml = reinterpret_cast<float*>(workspace);
     a.part_o = a.part_ml + 2 * slots;

@@ -735,16 +735,21 @@ static uint32_t pipe_blocks(const ShapeDims& s, uint32_t tokens) {
 }
 
 // most chunks a block of a `tokens`-row prompt can take, whatever its start
-static uint32_t pipe_max_chunks(const ShapeDims& s, uint32_t tokens) {
+// in a cache of `capacity` positions (whose tiles give at most capacity /
+// (64 min_chunk_tiles) chunks)
+static uint32_t pipe_max_chunks(const ShapeDims& s, uint32_t tokens, uint32_t capacity) {
     const uint64_t wgs = (uint64_t)pipe_blocks(s, tokens) * pipe_wgs_per_block(s);
     if (wgs >= kTargetWgs) return 1;
-    const uint32_t want = (uint32_t)((kTargetWgs + wgs - 1) / wgs);
-    return want < kMaxPipeChunks ? want : kMaxPipeChunks;
+    uint32_t want = (uint32_t)((kTargetWgs + wgs - 1) / wgs);
+    if (want > kMaxPipeChunks) want = kMaxPipeChunks;
+    const uint32_t fit = prefill_pipe_vt_tiles(capacity) / min_chunk_tiles(s);
+    if (want > fit) want = fit;
+    return want < 1 ? 1 : want;
 }
 
 // Chunk size in tiles for this call, 0 for no split.
-static uint32_t pipe_chunk_tiles(const ShapeDims& s, uint32_t start, uint32_t tokens) {
-    const uint32_t want = pipe_max_chunks(s, tokens);
+static uint32_t pipe_chunk_tiles(const ShapeDims& s, uint32_t start, uint32_t tokens, uint32_t capacity) {
+    const uint32_t want = pipe_max_chunks(s, tokens, capacity);
     const uint32_t n_max = (start + tokens + kTile - 1) / kTile;
     const uint32_t fit = n_max / min_chunk_tiles(s);
     const uint32_t chunks = want < fit ? want : fit;
@@ -752,8 +757,8 @@ static uint32_t pipe_chunk_tiles(const ShapeDims& s, uint32_t start, uint32_t to
     return (n_max + chunks - 1) / chunks;
 }
 
-static uint64_t pipe_part_bytes(const ShapeDims& s, uint32_t tokens) {
-    const uint32_t mc = pipe_max_chunks(s, tokens);
+static uint64_t pipe_part_bytes(const ShapeDims& s, uint32_t tokens, uint32_t capacity) {
+    const uint32_t mc = pipe_max_chunks(s, tokens, capacity);
     if (mc <= 1) return 0;
     const uint64_t slots = (uint64_t)pipe_blocks(s, tokens) * mc * pipe_columns(s);
     return slots * 2 * 4 + slots * s.head_dim * 4;
@@ -763,10 +768,17 @@ static uint64_t pipe_flag_bytes(const ShapeDims& s, uint32_t vt_tiles) {
     return ((uint64_t)s.kv_heads * vt_tiles * 4 + 255) / 256 * 256;
 }
 
-// workspace: [tile flags][V^T tiles][split partials: (m, l) then O]
-uint64_t prefill_pipe_workspace_bytes(const ShapeDims& s, uint32_t capacity, uint32_t tokens) {
+// Granite f16 caches take no pre-pass: the main kernel reads the cache's V
+// rows itself (DIRECT_V)
+static bool pipe_direct_v(const ShapeDims& s, int value_dtype) { return s.head_dim == 64 && value_dtype == F16; }
+
+// workspace: [tile flags][V^T tiles][split partials: (m, l) then O], the
+// first two only where the V^T pre-pass runs
+uint64_t prefill_pipe_workspace_bytes(const ShapeDims& s, int value_dtype, uint32_t capacity, uint32_t tokens) {
+    if (pipe_direct_v(s, value_dtype)) return pipe_part_bytes(s, tokens, capacity);
     const uint64_t tiles = prefill_pipe_vt_tiles(capacity);
-    return pipe_flag_bytes(s, tiles) + (uint64_t)s.kv_heads * tiles * s.head_dim * kTile * 2 + pipe_part_bytes(s, tokens);
+    return pipe_flag_bytes(s, tiles) + (uint64_t)s.kv_heads * tiles * s.head_dim * kTile * 2 +
+           pipe_part_bytes(s, tokens, capacity);
 }
 
 bool prefill_pipe_supported(const ShapeDims& s) {
@@ -783,14 +795,12 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
     uint32_t* flags = reinterpret_cast<uint32_t*>(ws);
     const uint64_t flag_bytes = pipe_flag_bytes(s, vt_tiles);
     uint16_t* vt = reinterpret_cast<uint16_t*>(ws + flag_bytes);
-    char* parts = ws + flag_bytes + (uint64_t)s.kv_heads * vt_tiles * s.head_dim * kTile * 2;
+    const bool direct_v = pipe_direct_v(s, kv.value_dtype);
+    char* parts = direct_v ? ws : ws + flag_bytes + (uint64_t)s.kv_heads * vt_tiles * s.head_dim * kTile * 2;
 
     dim3 vgrid(tiles, s.kv_heads);
     const bool bf = dtype == BF16;
     const bool tiered = kv.value_dtype == I8T;
-    // Granite f16 caches take no pre-pass: the main kernel reads the cache's
-    // V rows itself
-    const bool direct_v = !tiered && !bf && s.head_dim == 64;
     if (tiered) {
         TieredVtArgs ta{reinterpret_cast<const int8_t*>(kv.values), reinterpret_cast<const uint16_t*>(kv.value_scales),
                         reinterpret_cast<const uint16_t*>(kv.value_ring), vt, kv.head_stride, kv.ring_head_stride,
@@ -826,8 +836,8 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
     a.qblocks = (tokens + wgt - 1) / wgt;
     const uint32_t halves = pipe_wgs_per_block(s);  // Qwen: two 4-wave workgroups per query block
     a.xcd_map = (8 % s.kv_heads == 0) && ((uint64_t)a.qblocks * s.kv_heads * halves) % 8 == 0;
-    a.chunk_tiles = pipe_chunk_tiles(s, start, tokens);
-    a.max_chunks = pipe_max_chunks(s, tokens);
+    a.chunk_tiles = pipe_chunk_tiles(s, start, tokens, kv.capacity);
+    a.max_chunks = pipe_max_chunks(s, tokens, kv.capacity);
     const uint64_t slots = (uint64_t)a.qblocks * s.kv_heads * a.max_chunks * pipe_columns(s);
     a.part_ml = reinterpret_cast<float*>(parts);
     a.part_o = a.part_ml + 2 * slots;
