@@ -350,16 +350,19 @@ QXH_API int32_t qxh_encode_attention_for_layer_no_alloc(qxh_graph* graph, qxh_kv
  * fp16/bf16 caches run on MFMA with fp32 accumulation.  A call of a few rows
  * (up to 8, or while rows x context is small: the K-wide verifier) runs each
  * row as a causal decode, split over the context like qxh_encode_attention.
- * Longer calls first rewrite the layer's V rows [0, start_position + tokens)
- * into an f16 V^T scratch inside `workspace`, then run the pipelined MFMA
- * kernel (P.V in f16), splitting the KV range of each query block over the
- * CUs when there are few blocks.  For bf16 caches, rows that reach a V value
- * outside the f16 range are recomputed by an exact bf16 pass.  fp32 and mixed
- * caches always run causal decode rows.  `workspace` must hold
- * qxh_prefill_workspace_bytes, which covers every start_position: for the
- * pipelined kernel kv_heads x capacity (rounded up to 64) x head_dim x 2 bytes
- * plus per-tile flags and the split partials, for decode rows the split
- * partials of every row. */
+ * Longer calls run the pipelined MFMA kernel (P.V in f16), splitting the KV
+ * range of each query block over the CUs when there are few blocks; on bf16
+ * caches, tiered values and Qwen-shape f16 caches it first rewrites the
+ * layer's V rows [0, start_position + tokens) into an f16 V^T scratch inside
+ * `workspace` (Granite-shape f16 caches are read as they are).  For bf16
+ * caches, rows that reach a V value outside the f16 range are recomputed by
+ * an exact bf16 pass.  Granite-shape fp32 and mixed caches run an fp32
+ * matrix-core kernel (fp32 products and accumulation); Qwen-shape fp32
+ * caches run causal decode rows.  `workspace` must hold
+ * qxh_prefill_workspace_bytes, which covers every start_position: the V^T
+ * scratch where it is used (kv_heads x capacity rounded up to 64 x head_dim
+ * x 2 bytes plus per-tile flags) and the split partials, for decode rows the
+ * split partials of every row. */
 QXH_API int32_t qxh_prefill_workspace_bytes(const qxh_kv_cache* cache, uint32_t tokens, uint64_t* bytes);
 QXH_API int32_t qxh_encode_prefill_attention(qxh_graph* graph, qxh_kv_cache* cache, uint32_t layer, uint32_t sequence,
                                      uint32_t start_position, uint32_t tokens, const void* query,
