@@ -31,6 +31,11 @@
 //    per query block (heads 0-3 and 4-7 of the group, 64 KB of LDS each, so
 //    two share a CU and drift against each other), Granite three.
 //
+// KVG > 1 (Granite f16, grids of at most 256 blocks): a workgroup is KVG
+// groups of four waves, each over its share of the block's KV range with its
+// own LDS ring; the groups merge their (m, l, O) through LDS at the end, in
+// place of split partials and a merge dispatch.
+//
 // DIRECT_V (Granite f16): a V tile is staged row-major like K, 16-byte
 // chunks XOR-swizzled by (row & 7), and each P.V operand is two transposed
 // 8-byte reads (rows 4g.. and 16+4g.. of a 32-position half): lane (g, i)
@@ -233,8 +238,9 @@ __global__ __launch_bounds__(D) void prefill_vt_tiered_kernel(TieredVtArgs a) {
 // NW = 4 waves): nt selects the head, wave w covers tokens 16w .. of the
 // workgroup's 64; three such workgroups share a CU (under 168 VGPRs, 48 KB
 // LDS) and overlap each other's phases.
-template <int D, int DT, int HEADS_PER_WAVE, int NW, int HALVES = 1, bool DIRECT_V = false>
-__global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void prefill_pipe_kernel(PrefillPipeArgs a) {
+template <int D, int DT, int HEADS_PER_WAVE, int NW, int HALVES = 1, bool DIRECT_V = false, int KVG = 1>
+__global__ __launch_bounds__(64 * NW * KVG, NW == 8 || KVG > 1 ? 1 : (HALVES == 2 ? 2 : 3)) void prefill_pipe_kernel(
+    PrefillPipeArgs a) {
     using M = MfmaT<DT>;
     using MH = MfmaT<F16>;
     using vec = typename M::vec;
@@ -256,13 +262,21 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
     static_assert(LPW * NW == KI + VI, "stage loads must split evenly over the waves");
     static_assert(HALVES == 1 || (HEADS_PER_WAVE == 1 && NW == 4), "halves: Qwen, 4 waves");
     static_assert(!DIRECT_V || (D == 64 && DT == F16), "row-major V tiles: Granite f16 caches");
+    static_assert(KVG == 1 || (HALVES == 1 && NW == 4), "KV groups: one 4-wave group per part of the KV range");
+    constexpr int GRPB = STAGES * STAGEB;  // one KV group's LDS ring
 
-    __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGEB];
+    __shared__ __attribute__((aligned(1024))) char lds[KVG * GRPB];
 
-    const int tid = threadIdx.x;
     // readfirstlane: the compiler then knows the wave index (and every branch
-    // on it) is uniform, so those branches stay scalar
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // on it) is uniform, so those branches stay scalar.  KVG > 1: the
+    // workgroup is KVG groups of NW waves; group g runs the same columns as
+    // group 0 over the g-th part of the block's KV range, in its own LDS
+    // ring, and hands its (m, l, O) to group 0 at the end.
+    const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = KVG > 1 ? wave_all / NW : 0;
+    const int wave = KVG > 1 ? wave_all % NW : wave_all;
+    const int tid = KVG > 1 ? (int)threadIdx.x - grp * 64 * NW : (int)threadIdx.x;  // thread index within the group
+    const uint32_t grp_off = KVG > 1 ? (uint32_t)grp * GRPB : 0u;
     const int lane = tid & 63;
     const int lg = lane >> 4, li = lane & 15;
 
@@ -292,13 +306,17 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
     const uint32_t wg_t0 = qblock * WGT;
     const uint32_t kv_len = a.start + min(T, wg_t0 + WGT);
     const uint32_t n = (kv_len + kTile - 1) / kTile;
-    // this workgroup's tiles [t0, t1) of the block's n
-    const uint32_t ch_tiles = a.chunk_tiles ? a.chunk_tiles : n;
-    const uint32_t nchunks = (n + ch_tiles - 1) / ch_tiles;
+    // this workgroup's tiles [t0, t1) of the block's n (KVG > 1: this
+    // group's share, ceil(n / KVG) tiles, possibly none); every wave of the
+    // workgroup runs rounds 0 .. mr, the longest group's, so that all pass
+    // the same barriers
+    const uint32_t ch_tiles = KVG > 1 ? (n + KVG - 1) / KVG : (a.chunk_tiles ? a.chunk_tiles : n);
+    const uint32_t nchunks = KVG > 1 ? 1u : (n + ch_tiles - 1) / ch_tiles;
     const uint32_t chunk = blockIdx.y;
     if (chunk >= nchunks) return;  // uniform, before any barrier
-    const uint32_t t0 = chunk * ch_tiles, t1 = min(n, t0 + ch_tiles);
-    const uint32_t m = t1 - t0;
+    const uint32_t t0 = (KVG > 1 ? (uint32_t)grp : chunk) * ch_tiles, t1 = min(n, t0 + ch_tiles);
+    const uint32_t m = KVG == 1 || t1 > t0 ? t1 - t0 : 0u;
+    const uint32_t mr = KVG > 1 ? ch_tiles : m;
 
     // this wave's columns
     const int wslot = HEADS_PER_WAVE == 1 ? 0 : (NW == 8 ? 2 * (wave & 3) + (wave >> 2) : wave);
@@ -334,12 +352,14 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
     // tile the V halves of all slots are cleared first: stale LDS bits can
     // then never meet a zero probability as inf or NaN.
     if constexpr (DIRECT_V) {
-        if (t1 == n && kv_len % kTile != 0) {
+        // the condition is uniform over the workgroup (with KV groups, every
+        // group clears its own ring)
+        if ((KVG > 1 || t1 == n) && kv_len % kTile != 0) {
 #pragma unroll
             for (int sl = 0; sl < STAGES; ++sl)
 #pragma unroll
                 for (int k = 0; k < VTILEB / (64 * NW * 16); ++k)
-                    *reinterpret_cast<u32x4*>(lds + sl * STAGEB + KTILEB + (k * 64 * NW + tid) * 16) =
+                    *reinterpret_cast<u32x4*>(lds + grp_off + sl * STAGEB + KTILEB + (k * 64 * NW + tid) * 16) =
                         u32x4{0u, 0u, 0u, 0u};
             __syncthreads();
         }
@@ -391,7 +411,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
         // the slot offset passes through an empty asm so that the compiler
         // derives the eight LDS destinations in the round (scalar adds)
         // instead of keeping all of them live in SGPRs across the loop
-        uint32_t sb_off = (r % STAGES) * STAGEB;
+        uint32_t sb_off = grp_off + (r % STAGES) * STAGEB;
         asm volatile("" : "+s"(sb_off));
         char* sb = lds + sb_off;
         if (k_wave) {
@@ -458,7 +478,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
         constexpr int B0 = DO_PV ? 0 : NPV;          // first operand index
         constexpr int B1 = DO_QK ? NPV + NQK : NPV;  // one past the last
         constexpr int N = B1 - B0;
-        const char* st = lds + decltype(slot)::value * STAGEB;
+        const char* st = lds + grp_off + decltype(slot)::value * STAGEB;
         // operand i: PV (i < NPV): half = i / DTILES, dt = i % DTILES;
         //            QK: ks = (i - NPV) / 4, mt = (i - NPV) % 4
         auto read = [&](int i) -> u32x4 {
@@ -616,13 +636,16 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
         }
     };
 
-    // prologue: stage 0 complete (and stage 1 in flight with three stages)
-    issue_stage(0);
-    if constexpr (STAGES == 3) {
-        issue_stage(1);  // m >= 1: stage 1 exists
-        wait_vmcnt<LPW>();
-    } else {
-        wait_vmcnt<0>();
+    // prologue: stage 0 complete (and stage 1 in flight with three stages); a
+    // KV group with no tiles issues nothing
+    if (KVG == 1 || m > 0) {
+        issue_stage(0);
+        if constexpr (STAGES == 3) {
+            issue_stage(1);  // m >= 1: stage 1 exists
+            wait_vmcnt<LPW>();
+        } else {
+            wait_vmcnt<0>();
+        }
     }
     phase_barrier();
 
@@ -636,8 +659,10 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
         // Q.K that no softmax reads: one code path for every round the wave
         // takes part in.  A wave that runs ahead into this phase while its
         // SIMD partner is still in softmax takes issue priority.
+        // A KV group with no tiles has loaded no slot: it skips the phase
+        // (round 0's P = 0 would otherwise meet whatever the ring holds).
         __builtin_amdgcn_s_setprio(1);
-        if (r <= wave_m) mfma_phase(slot, std::true_type{}, std::true_type{});
+        if ((KVG == 1 || m > 0) && r <= wave_m) mfma_phase(slot, std::true_type{}, std::true_type{});
         __builtin_amdgcn_s_setprio(0);
         // stage r+1 complete; with three stages stage r+2 (issued above) may
         // still be in flight
@@ -648,12 +673,54 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : (HALVES == 2 ? 2 : 3)) void 
         // needs no second barrier)
         if (r < wave_m) softmax(t0 + r);
     };
-    // round r reads slot r % STAGES
-    for (uint32_t r = 0; r <= m; r += STAGES) {
+    // round r reads slot r % STAGES; rounds past this group's m only pass the
+    // barrier
+    for (uint32_t r = 0; r <= mr; r += STAGES) {
         round(r, std::integral_constant<int, 0>{});
-        if (r + 1 <= m) round(r + 1, std::integral_constant<int, 1>{});
+        if (r + 1 <= mr) round(r + 1, std::integral_constant<int, 1>{});
         if constexpr (STAGES == 3)
-            if (r + 2 <= m) round(r + 2, std::integral_constant<int, 2>{});
+            if (r + 2 <= mr) round(r + 2, std::integral_constant<int, 2>{});
+    }
+
+    if constexpr (KVG > 1) {
+        // Groups 1 .. KVG-1 leave (m, l, O) of their columns in their own
+        // ring (no group reads another's ring before this point, and every
+        // load and operand read of the rounds is done); group 0 merges them.
+        // Lane (lg, li) of wave w holds the same columns and dims in every
+        // group.
+        float* xo = reinterpret_cast<float*>(lds + grp_off);
+        float* xml = xo + NW * 2 * DTILES * 64 * 4;
+        if (grp > 0) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+                for (int dt = 0; dt < DTILES; ++dt)
+                    *reinterpret_cast<f32x4*>(xo + (((wave * 2 + nt) * DTILES + dt) * 64 + lane) * 4) = oacc[dt][nt];
+                xml[((wave * 2 + nt) * 64 + lane) * 2] = mrun[nt];
+                xml[((wave * 2 + nt) * 64 + lane) * 2 + 1] = lacc[nt][0];
+            }
+        }
+        __syncthreads();
+        if (grp > 0) return;
+#pragma unroll
+        for (int g = 1; g < KVG; ++g) {
+            const float* yo = reinterpret_cast<const float*>(lds + (uint32_t)g * GRPB);
+            const float* yml = yo + NW * 2 * DTILES * 64 * 4;
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const float m1 = yml[((wave * 2 + nt) * 64 + lane) * 2];
+                const float l1 = yml[((wave * 2 + nt) * 64 + lane) * 2 + 1];
+                const float mn = fmaxf(mrun[nt], m1);
+                const float f0 = fast_exp2((mrun[nt] - mn) * c), f1 = fast_exp2((m1 - mn) * c);
+                mrun[nt] = mn;
+                lacc[nt] = lacc[nt] * f0 + l1 * f1;
+#pragma unroll
+                for (int dt = 0; dt < DTILES; ++dt)
+                    oacc[dt][nt] = oacc[dt][nt] * f0 +
+                                   *reinterpret_cast<const f32x4*>(yo + (((wave * 2 + nt) * DTILES + dt) * 64 + lane) * 4) *
+                                       f1;
+            }
+        }
     }
 
     if (!wave_live) return;
@@ -785,6 +852,23 @@ bool prefill_pipe_supported(const ShapeDims& s) {
     return (s.head_dim == 128 && s.group == 8) || (s.head_dim == 64 && s.group == 2);
 }
 
+// KV groups per workgroup (Granite f16).  Instead of a grid split into KV
+// chunks that a second dispatch merges, each block's workgroup runs its KV
+// range as kvg groups of 4 waves with their own LDS rings, merged through
+// LDS at the end: no partials in HBM and no merge dispatch.  Measured (us per
+// call, alternating runs on one box): cfg 3's 2048-token prompt 31.7-32.3
+// with two chunks and the merge, 28.1-28.2 with two groups, 26.7-26.8 with
+// three (1.0 of 256 workgroups per CU, 12 waves each); a 512-token prompt
+// (64 blocks, not split) 14.6-14.7 alone, 13.8-14.0 with two groups, 14.9-15.5
+// with three.  A grouped workgroup takes a whole CU (96 or 144 KB of LDS),
+// so grids of more than 256 blocks, and prompts over long contexts that split
+// four or more ways, keep the chunked grid.
+static int pipe_kv_groups(bool direct_v, uint32_t blocks, uint32_t n_max, uint32_t chunks) {
+    if (!direct_v || n_max < 2 || blocks > 256) return 1;
+    if ((chunks == 2 || chunks == 3) && n_max >= 3 && blocks >= 192) return 3;
+    return chunks <= 2 ? 2 : 1;
+}
+
 hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t start, uint32_t tokens, const void* query,
                              int dtype, void* out, int out_dtype, void* workspace, hipStream_t st, int* dispatches) {
     *dispatches = 0;
@@ -843,16 +927,22 @@ hipError_t launch_prefill_pipe(const ShapeDims& s, const KvLayer& kv, uint32_t s
     a.part_o = a.part_ml + 2 * slots;
     // chunks of the longest block (the last one; with start it is the longest)
     const uint32_t chunks = a.chunk_tiles ? (tiles + a.chunk_tiles - 1) / a.chunk_tiles : 1;
-    dim3 grid(a.qblocks * s.kv_heads * halves, chunks);
+    const int kvg = pipe_kv_groups(direct_v, a.qblocks * s.kv_heads, tiles, chunks);
+    const bool kv_groups = kvg > 1;
+    dim3 grid(a.qblocks * s.kv_heads * halves, kv_groups ? 1 : chunks);
     if (s.head_dim == 128) {
         if (bf) hipLaunchKernelGGL((prefill_pipe_kernel<128, BF16, 1, 4, 2>), grid, dim3(256), 0, st, a);
         else hipLaunchKernelGGL((prefill_pipe_kernel<128, F16, 1, 4, 2>), grid, dim3(256), 0, st, a);
+    } else if (kvg == 2) {
+        hipLaunchKernelGGL((prefill_pipe_kernel<64, F16, 2, 4, 1, true, 2>), grid, dim3(512), 0, st, a);
+    } else if (kvg == 3) {
+        hipLaunchKernelGGL((prefill_pipe_kernel<64, F16, 2, 4, 1, true, 3>), grid, dim3(768), 0, st, a);
     } else {
         if (bf) hipLaunchKernelGGL((prefill_pipe_kernel<64, BF16, 2, 4>), grid, dim3(256), 0, st, a);
         else hipLaunchKernelGGL((prefill_pipe_kernel<64, F16, 2, 4, 1, true>), grid, dim3(256), 0, st, a);
     }
     *dispatches = direct_v ? 1 : 2;
-    if (chunks > 1) {
+    if (chunks > 1 && !kv_groups) {
         const uint32_t cpb = 256 / (s.head_dim / 4);
         dim3 cgrid(a.qblocks * s.kv_heads, pipe_columns(s) / cpb);
         if (s.head_dim == 128) hipLaunchKernelGGL((prefill_combine_kernel<128, 1, 8>), cgrid, dim3(256), 0, st, a);

@@ -256,11 +256,15 @@ TORCH = {abi.F32: torch.float32, abi.F16: torch.float16, abi.BF16: torch.bfloat1
 
 
 # Every prefill path, with the prompt ending inside a 64-position tile:
-# Granite f16 (V tiles read straight from the cache; one chunk, then two),
-# Granite bf16 and Qwen bf16 (V^T pre-pass), Fp32KFp16V (fp32 matrix-core
-# kernel; one chunk, then several) and a few rows (causal decode rows).
+# Granite f16 (V tiles read straight from the cache: workgroups of two KV
+# groups (300 rows; 100 rows after 1000, two groups where the grid would have
+# split in two), three groups (2000 rows, 256 blocks) and the chunked grid
+# with its merge (20 rows after 3000, six chunks)), Granite bf16 and Qwen
+# bf16 (V^T pre-pass), Fp32KFp16V (fp32 matrix-core kernel; one chunk, then
+# several) and a few rows (causal decode rows).
 @pytest.mark.parametrize("shape,kdt,vdt,start,T", [
     (abi.SHAPE_GRANITE, abi.F16, abi.F16, 0, 300), (abi.SHAPE_GRANITE, abi.F16, abi.F16, 1000, 100),
+    (abi.SHAPE_GRANITE, abi.F16, abi.F16, 0, 2000), (abi.SHAPE_GRANITE, abi.F16, abi.F16, 3000, 20),
     (abi.SHAPE_GRANITE, abi.BF16, abi.BF16, 0, 300), (abi.SHAPE_QWEN3, abi.BF16, abi.BF16, 0, 300),
     (abi.SHAPE_GRANITE, abi.F32, abi.F16, 0, 300), (abi.SHAPE_GRANITE, abi.F32, abi.F16, 1000, 100),
     (abi.SHAPE_GRANITE, abi.F16, abi.F16, 37, 6)])
