@@ -1,6 +1,7 @@
 // Causal prefill attention, pipelined (gfx950 MFMA, fp32 accumulate).
 //
-// Two kernels per call:
+// Up to two kernels per call (and a merge of split partials, prefill_split.h,
+// when a grid is split into chunks):
 //
 // 1. prefill_vt_kernel (bf16 caches, tiered values and Qwen-shape f16 caches):
 //    the layer's V rows [0, kv_len) of each kv head are rewritten once into
@@ -29,7 +30,8 @@
 //    SIMD, half a round apart, was 5% slower).  Overlap comes from several
 //    independent workgroups per CU instead: Qwen runs two 4-wave workgroups
 //    per query block (heads 0-3 and 4-7 of the group, 64 KB of LDS each, so
-//    two share a CU and drift against each other), Granite three.
+//    two share a CU and drift against each other), Granite three (or, with
+//    KV groups, the groups of one workgroup).
 //
 // KVG > 1 (Granite f16, grids of at most 256 blocks): a workgroup is KVG
 // groups of four waves, each over its share of the block's KV range with its
