@@ -137,10 +137,15 @@ __global__ __launch_bounds__(256) void qwen_norm_rope_append_kernel(KvLayer kv, 
 // head, so a prompt row repeats the same 32 (Granite) or 64 (Qwen) angles
 // once per head, and their loads are one element per lane.  Here a wave owns
 // a whole token row: each lane evaluates one angle, the lanes fetch the
-// values they need from each other (ds_bpermute), and a lane then works on
-// 8-element slices of both halves of a head (elements 8j..8j+7 and the
-// rotation partners half a head further on), so every load and store is
-// 16 bytes (two for fp32) and the rotation needs no exchange.  Same
+// angles they need from each other (ds_bpermute), and every load and store
+// is 16 bytes (two for fp32).  Qwen: a lane works on 8-element slices of
+// both halves of a head (elements 8j..8j+7 and the rotation partners half a
+// head further on), so the rotation needs no exchange and eight lanes cover
+// one 128-byte line of each half.  Granite (64-element heads, one 128-byte
+// line of 16-bit values): a lane works on one 8-element slice and takes its
+// rotation partner from another lane, so that eight lanes store a whole line
+// (cfg 3's 2048-row front end 5.30 -> 4.96 us against both halves per lane,
+// which wrote each line in two 64-byte halves from two instructions).  Same
 // arithmetic, element for element and in the same order, as the per-head
 // kernels: the results are identical bit for bit.
 // ---------------------------------------------------------------------------
@@ -198,65 +203,105 @@ __device__ __forceinline__ float lane_read(float v, int src_lane) {
     return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(v)));
 }
 
-// Granite (16 q + 8 k + 8 v heads of 64): lane = 4 hs + j, slice j of
-// head hs (task 0, a query head) and of head 16 + hs (task 1: key head hs,
-// or value head hs - 8).  Lanes 0..31 evaluate the consensus sin/cos of
-// pair `lane`.  grid ceil(rows / 4) x 256, rows = tokens x sequences.
+// Granite (16 q + 8 k + 8 v heads of 64): lane = 8 hs + j, slice j (8
+// elements, 8j..8j+7) of head hs in each of four head sets: query heads hs
+// and 8 + hs, key head hs, value head hs.  Eight lanes then cover a head's
+// whole 64 elements, so every load and store instruction moves whole
+// 128-byte lines (16-bit rows); the rotation partner of slice j is slice
+// j ^ 4, read from lane ^ 4 (ds_swizzle).  Lanes 0..31 evaluate the
+// consensus sin/cos of pair `lane`.  grid ceil(rows / 4) x 256, rows =
+// tokens x sequences.
+template <int IDT>
+__device__ __forceinline__ void load_slice_raw(const void* base, size_t idx, uint32_t (&w)[8]) {
+    if constexpr (IDT == F32) {
+        const float* p = reinterpret_cast<const float*>(base) + idx;
+        const u32x4 a = load16<true>(p), b = load16<true>(p + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w[i] = a[i];
+            w[4 + i] = b[i];
+        }
+    } else {
+        const u32x4 a = load16<true>(reinterpret_cast<const uint16_t*>(base) + idx);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = a[i];
+    }
+}
+template <int IDT> __device__ __forceinline__ void unpack_slice(const uint32_t (&w)[8], float (&v)[8]) {
+    if constexpr (IDT == F32) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w[i]);
+    } else {
+        Unpack<IDT>::run(u32x4{w[0], w[1], w[2], w[3]}, v);
+    }
+}
+// the words of lane ^ 4 (ds_swizzle bit mode: and 0x1f, or 0, xor 4)
+template <int IDT> __device__ __forceinline__ void partner_slice(const uint32_t (&w)[8], uint32_t (&o)[8]) {
+    constexpr int N = IDT == F32 ? 8 : 4;
+#pragma unroll
+    for (int i = 0; i < N; ++i) o[i] = (uint32_t)__builtin_amdgcn_ds_swizzle((int)w[i], 0x101F);
+}
+
 template <int IDT>
 __global__ __launch_bounds__(256) void granite_rope_append_rows_kernel(KvLayer kv, RopeAppendArgs a) {
-    constexpr int D = 64, P = 32, QH = 16, KVH = 8;
+    constexpr int D = 64, QH = 16, KVH = 8;
     const int lane = threadIdx.x & 63;
     const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= a.tokens * a.sequences) return;
     const uint32_t s = r / a.tokens, t = r - s * a.tokens;
     const uint32_t pos = a.start_position + t;
-    const int j = lane & 3, hs = lane >> 2;
+    const int j = lane & 7, hs = lane >> 3;
+    const bool hi = j >= 4;  // slice in the second half (y) of the head
+    const int pj = j & 3;    // pairs 8 pj .. 8 pj + 7
     const bool has_q = a.query_out != nullptr;
-    const bool is_k = hs < KVH;
-    const int kvh = is_k ? hs : hs - KVH;
-    const void* src1 = is_k ? a.key : a.value;
-    const bool do_v = !is_k && kv.values;  // null values: a tiered cache (tiered_v.hip)
-    const size_t qbase = ((size_t)r * QH + hs) * D, kvbase = ((size_t)r * KVH + kvh) * D;
-    float qx[8], qy[8], x1[8], y1[8];
+    const bool do_v = kv.values != nullptr;  // null values: a tiered cache (tiered_v.hip)
+    const size_t qbase = (size_t)r * QH * D + (size_t)hs * D + 8 * j, kvbase = ((size_t)r * KVH + hs) * D + 8 * j;
+    uint32_t wq0[8], wq1[8], wk[8], wv[8];
     if (has_q) {
-        load_row8<IDT>(a.query, qbase + 8 * j, qx);
-        load_row8<IDT>(a.query, qbase + P + 8 * j, qy);
+        load_slice_raw<IDT>(a.query, qbase, wq0);
+        load_slice_raw<IDT>(a.query, qbase + 8 * D, wq1);
     }
-    if (is_k || do_v) {
-        load_row8<IDT>(src1, kvbase + 8 * j, x1);
-        load_row8<IDT>(src1, kvbase + P + 8 * j, y1);
-    }
+    load_slice_raw<IDT>(a.key, kvbase, wk);
+    if (do_v) load_slice_raw<IDT>(a.value, kvbase, wv);
     float sn0 = 0.0f, cs0 = 0.0f;
-    if (lane < P) granite_rope_sin_cos(pos, (uint32_t)lane, sn0, cs0);  // positions <= 4096: always defined
-    float sn[8], cs[8];
+    if (lane < 32) granite_rope_sin_cos(pos, (uint32_t)lane, sn0, cs0);  // positions <= 4096: always defined
+    // x' = fma(-y, sin, x cos) (first half), y' = fma(y, cos, x sin) (second
+    // half), the operations of the per-head kernel in its order: o = fma(A,
+    // fb, x fd) with A = -y or y
+    float fb[8], fd[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        sn[i] = lane_read(sn0, 8 * j + i);
-        cs[i] = lane_read(cs0, 8 * j + i);
+        const float sn = lane_read(sn0, 8 * pj + i), cs = lane_read(cs0, 8 * pj + i);
+        fb[i] = hi ? cs : sn;
+        fd[i] = hi ? sn : cs;
     }
+    auto rotate = [&](const uint32_t (&w)[8], float (&o)[8]) __attribute__((always_inline)) {
+        uint32_t pw[8];
+        partner_slice<IDT>(w, pw);
+        float v[8], pv[8];
+        unpack_slice<IDT>(w, v);
+        unpack_slice<IDT>(pw, pv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float x = hi ? pv[i] : v[i], y = hi ? v[i] : -pv[i];
+            o[i] = __builtin_fmaf(y, fb[i], x * fd[i]);
+        }
+    };
     if (has_q) {
         float o0[8], o1[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            o0[i] = __builtin_fmaf(-qy[i], sn[i], qx[i] * cs[i]);
-            o1[i] = __builtin_fmaf(qy[i], cs[i], qx[i] * sn[i]);
-        }
-        store_row8(a.query_out, qbase + 8 * j, o0, a.output_dtype);
-        store_row8(a.query_out, qbase + P + 8 * j, o1, a.output_dtype);
+        rotate(wq0, o0);
+        rotate(wq1, o1);
+        store_row8(a.query_out, qbase, o0, a.output_dtype);
+        store_row8(a.query_out, qbase + 8 * D, o1, a.output_dtype);
     }
-    const size_t dst = (size_t)s * kv.sequence_stride + (size_t)kvh * kv.head_stride + (size_t)pos * D;
-    if (is_k) {
-        float o0[8], o1[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            o0[i] = __builtin_fmaf(-y1[i], sn[i], x1[i] * cs[i]);
-            o1[i] = __builtin_fmaf(y1[i], cs[i], x1[i] * sn[i]);
-        }
-        store_row8(kv.keys, dst + 8 * j, o0, kv.key_dtype);
-        store_row8(kv.keys, dst + P + 8 * j, o1, kv.key_dtype);
-    } else if (do_v) {
-        store_row8(kv.values, dst + 8 * j, x1, kv.value_dtype);
-        store_row8(kv.values, dst + P + 8 * j, y1, kv.value_dtype);
+    const size_t dst = (size_t)s * kv.sequence_stride + (size_t)hs * kv.head_stride + (size_t)pos * D + 8 * j;
+    float ok[8];
+    rotate(wk, ok);
+    store_row8(kv.keys, dst, ok, kv.key_dtype);
+    if (do_v) {
+        float v[8];
+        unpack_slice<IDT>(wv, v);
+        store_row8(kv.values, dst, v, kv.value_dtype);
     }
 }
 
