@@ -567,11 +567,34 @@ def bench_prefill(ctx, steps, warmup, shape_name):
     g.discard()
     ms_fe = timed(lambda: replay.launch(stream), max(3, steps // 2), 2, stream) / nsets
     del replay, sets, qos
+    # the floor of a one-shot read + write of the same bytes on this box: the
+    # library's copy probe over as many rotated sources, one graph, nontemporal
+    # and ordinary stores (the better of the two)
+    cp_bytes = -(-fe_in // 4096) * 4096
+    srcs = [torch.empty(cp_bytes, dtype=torch.uint8, device="cuda:0") for _ in range(nsets)]
+    dsts = [torch.empty(cp_bytes, dtype=torch.uint8, device="cuda:0") for _ in range(2)]
+    copy_us = {}
+    for nt in (True, False):
+        g = rt.Graph(ctx, stream)
+        g.capture_begin()
+        for i, src in enumerate(srcs):
+            rt.hbm_copy_probe(g, src, dsts[i & 1], nt)
+        replay = g.capture_end()
+        g.discard()
+        copy_us[nt] = timed(lambda: replay.launch(stream), max(3, steps // 2), 2, stream) / nsets * 1000.0
+        del replay
+    del srcs, dsts
+    copy_floor = min(copy_us.values())
     return {"us_per_prefill": ms * 1000.0, "tokens": T, "flop": flops,
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
                          "frac": round(tflops / peak, 4), "traffic": None},
             "frontend": {"us": round(ms_fe * 1000.0, 2), "bytes": fe_bytes,
                          "roofline": roofline_hbm(fe_bytes, ms_fe, load_traffic(f"{shape_name}_frontend")),
+                         "copy_floor": {"us": round(copy_floor, 2), "bytes": 2 * cp_bytes,
+                                        "nontemporal_us": round(copy_us[True], 2), "plain_us": round(copy_us[False], 2),
+                                        "frac": round(copy_floor / (ms_fe * 1000.0), 4),
+                                        "note": "qxh_encode_hbm_copy_probe: one launch reading and writing the front "
+                                                "end's bytes, replayed like it; frac = floor / front end"},
                          "note": "RoPE of q and k" + (" after per-head RMSNorm" if shape != abi.SHAPE_GRANITE else "") +
                                  ", K/V append of every prompt row, one launch (qxh_encode_rope_kv_batch); bytes = "
                                  f"q, k, v read + rotated q, cache K, cache V written; {nsets} input sets rotated "

@@ -418,6 +418,13 @@ extern "C" {
         sink: *mut u32,
         blocks: u32,
     ) -> i32;
+    pub fn qxh_encode_hbm_copy_probe(
+        graph: *mut QxhGraph,
+        src: *const c_void,
+        dst: *mut c_void,
+        bytes: u64,
+        nontemporal: i32,
+    ) -> i32;
     pub fn qxh_encode_kv_fill_normal(graph: *mut QxhGraph, cache: *mut QxhKvCache, seed: u64, length: u32) -> i32;
     pub fn qxh_encode_consensus_conformance(
         graph: *mut QxhGraph,

@@ -557,6 +557,14 @@ QXH_API int32_t qxh_encode_fill_normal(qxh_graph* graph, void* data, int32_t dty
  * written for real data; it keeps the loads from being optimised away. */
 QXH_API int32_t qxh_encode_hbm_read_probe(qxh_graph* graph, const void* data, uint64_t bytes, uint32_t* sink,
                                           uint32_t blocks);
+/* Copy probe: `bytes` (a positive multiple of 4096; 16-byte aligned,
+ * non-overlapping buffers) from `src` to `dst` in one launch, a wave per
+ * 4 KB row whose loads all precede its stores, stores nontemporal when
+ * `nontemporal` is nonzero.  The floor of a one-shot kernel that reads and
+ * writes that many bytes (the bench's reference for the prompt front ends).
+ * Like the read probe, a bench helper with no counterpart in the reference. */
+QXH_API int32_t qxh_encode_hbm_copy_probe(qxh_graph* graph, const void* src, void* dst, uint64_t bytes,
+                                          int32_t nontemporal);
 /* Fill rows [0, length) of every (layer, sequence, kv_head) cache with
  * N(0,1) values and set every cursor to `length`. */
 QXH_API int32_t qxh_encode_kv_fill_normal(qxh_graph* graph, qxh_kv_cache* cache, uint64_t seed, uint32_t length);

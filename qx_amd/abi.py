@@ -156,6 +156,7 @@ SIGNATURES = {
                                              c_int32, c_void_p]),
     "qxh_encode_fill_normal": (c_int32, [c_void_p, c_void_p, c_int32, c_uint64, c_uint64, c_float]),
     "qxh_encode_hbm_read_probe": (c_int32, [c_void_p, c_void_p, c_uint64, c_void_p, c_uint32]),
+    "qxh_encode_hbm_copy_probe": (c_int32, [c_void_p, c_void_p, c_void_p, c_uint64, c_int32]),
     "qxh_encode_kv_fill_normal": (c_int32, [c_void_p, c_void_p, c_uint64, c_uint32]),
     "qxh_encode_consensus_conformance": (c_int32, [c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p,
                                                    c_void_p, c_void_p]),

@@ -78,6 +78,7 @@ hipError_t launch_tiered_value_fill(const ShapeDims& s, const KvLayer& kv_all_la
                                     uint32_t sequences, uint32_t length, uint64_t seed, hipStream_t st);
 // probe.hip: plain streaming read of `bytes` (a multiple of 16) over `blocks` workgroups
 hipError_t launch_hbm_read_probe(const void* data, uint64_t bytes, uint32_t* sink, uint32_t blocks, hipStream_t st);
+hipError_t launch_hbm_copy_probe(const void* src, void* dst, uint64_t bytes, bool nontemporal, hipStream_t st);
 // decode_attention.hip: Granite RoPE + append + attention of one token, one dispatch
 hipError_t launch_decode_step(const ShapeDims& s, const KvLayer& kv, const float* query, const float* key,
                               const float* value, float* query_out, uint32_t position, void* out, int out_dtype,

@@ -256,15 +256,23 @@ __global__ __launch_bounds__(256) void granite_rope_append_rows_kernel(KvLayer k
     const bool has_q = a.query_out != nullptr;
     const bool do_v = kv.values != nullptr;  // null values: a tiered cache (tiered_v.hip)
     const size_t qbase = (size_t)r * QH * D + (size_t)hs * D + 8 * j, kvbase = ((size_t)r * KVH + hs) * D + 8 * j;
+    // The inverse frequency is loaded first: loads return in order, so the
+    // angle waits for it alone and is evaluated while the rows are in
+    // flight.  All four row loads are unconditional, so none waits behind a
+    // branch: a query or value row that is not wanted is read from the key
+    // row (never stored).
+    const uint32_t inv_bits = kGraniteInvFreqBits[lane & 31];
+    __builtin_amdgcn_sched_barrier(0);  // keep it ahead of the row loads
     uint32_t wq0[8], wq1[8], wk[8], wv[8];
-    if (has_q) {
-        load_slice_raw<IDT>(a.query, qbase, wq0);
-        load_slice_raw<IDT>(a.query, qbase + 8 * D, wq1);
-    }
+    load_slice_raw<IDT>(has_q ? a.query : a.key, has_q ? qbase : kvbase, wq0);
+    load_slice_raw<IDT>(has_q ? a.query : a.key, has_q ? qbase + 8 * D : kvbase, wq1);
     load_slice_raw<IDT>(a.key, kvbase, wk);
-    if (do_v) load_slice_raw<IDT>(a.value, kvbase, wv);
-    float sn0 = 0.0f, cs0 = 0.0f;
-    if (lane < 32) granite_rope_sin_cos(pos, (uint32_t)lane, sn0, cs0);  // positions <= 4096: always defined
+    load_slice_raw<IDT>(do_v ? a.value : a.key, kvbase, wv);
+    // granite_rope_sin_cos's operations, (float)position * inverse then
+    // consensus_sin_cos, for pair lane & 31 (lanes 32..63 repeat lanes
+    // 0..31: no branch, and no cost on a 64-lane SIMD)
+    float sn0, cs0;
+    consensus_sin_cos((float)pos * bits_f(inv_bits), sn0, cs0);  // positions <= 4096: always defined
     // x' = fma(-y, sin, x cos) (first half), y' = fma(y, cos, x sin) (second
     // half), the operations of the per-head kernel in its order: o = fma(A,
     // fb, x fd) with A = -y or y
@@ -305,12 +313,26 @@ __global__ __launch_bounds__(256) void granite_rope_append_rows_kernel(KvLayer k
     }
 }
 
+// Unit norm weights: the rows read these when a call passes no norm, so the
+// weight loads are unconditional (a load under a branch is waited for
+// inside the branch).
+struct UnitNorm128 {
+    float v[128];
+    constexpr UnitNorm128() : v() {
+        for (int i = 0; i < 128; ++i) v[i] = 1.0f;
+    }
+};
+__device__ __attribute__((aligned(16))) const UnitNorm128 kUnitNorm{};
+
 // Qwen (32 q + 4 k + 4 v heads of 128): five waves per token row, wave
 // task 0..3 the query heads 8 task + hs, task 4 the key heads (hs < 4) and
 // value heads (hs - 4); lane = 8 hs + j works on slice j of head hs.  Each
 // wave evaluates the row's 64 angles itself, one per lane (one task per wave
 // measured 30.4 against 36.0 us for all five tasks in one wave, cfg 5b's
-// 8192-row prompt: the smaller waves keep more of the row in flight).
+// 8192-row prompt: the smaller waves keep more of the row in flight).  The
+// inverse frequency is loaded first and every row and weight load is
+// unconditional, so the angle waits for its own load alone and no load
+// waits behind a branch.
 template <int IDT>
 __global__ __launch_bounds__(256) void qwen_norm_rope_append_rows_kernel(KvLayer kv, RopeAppendArgs a) {
     constexpr int D = 128, P = 64, QH = 32, KVH = 4;
@@ -328,22 +350,36 @@ __global__ __launch_bounds__(256) void qwen_norm_rope_append_rows_kernel(KvLayer
     const bool is_k = !is_q && hs < KVH;
     const int kvh = is_k ? hs : hs - KVH;
     const bool do_v = !is_q && !is_k && kv.values;
-    const void* src = is_q ? a.query : (is_k ? a.key : a.value);
+    const float inv_freq = a.qwen_inv_freq[lane];
+    __builtin_amdgcn_sched_barrier(0);  // keep it ahead of the row loads
+    // a value row that is not appended (tiered cache) reads the key row instead
+    const void* src = is_q ? a.query : (is_k || !do_v ? a.key : a.value);
     const size_t base = is_q ? ((size_t)r * QH + 8 * task + hs) * D : ((size_t)r * KVH + kvh) * D;
     float x[8], y[8];
-    if (is_q || is_k || do_v) {
-        load_row8<IDT>(src, base + 8 * j, x);
-        load_row8<IDT>(src, base + P + 8 * j, y);
-    }
+    load_row8<IDT>(src, base + 8 * j, x);
+    load_row8<IDT>(src, base + P + 8 * j, y);
+    // global-address-space pointers: a generic one (either source) would make
+    // these flat loads, which the compiler waits for together with every
+    // older load
+    typedef const __attribute__((address_space(1))) u32x4 gvec;
     const float* norm = is_q ? a.query_norm : a.key_norm;
+    if (!norm) norm = kUnitNorm.v;
     float nl[8], nr[8];
+    {
+        const u32x4 n0 = *(gvec*)(norm + 8 * j);
+        const u32x4 n1 = *(gvec*)(norm + 8 * j + 4);
+        const u32x4 n2 = *(gvec*)(norm + P + 8 * j);
+        const u32x4 n3 = *(gvec*)(norm + P + 8 * j + 4);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        nl[i] = norm ? norm[8 * j + i] : 1.0f;
-        nr[i] = norm ? norm[P + 8 * j + i] : 1.0f;
+        for (int i = 0; i < 4; ++i) {
+            nl[i] = __uint_as_float(n0[i]);
+            nl[4 + i] = __uint_as_float(n1[i]);
+            nr[i] = __uint_as_float(n2[i]);
+            nr[4 + i] = __uint_as_float(n3[i]);
+        }
     }
     float sn0, cs0;
-    sincosf((float)pos * a.qwen_inv_freq[lane], &sn0, &cs0);
+    sincosf((float)pos * inv_freq, &sn0, &cs0);
     float sn[8], cs[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -549,7 +585,7 @@ hipError_t launch_rope_append(const ShapeDims& s, const KvLayer& kv, const RopeA
     // strides are multiples of 8 elements)
     const bool rows_ok = rows >= kRowKernelMinRows && rows * 5 < (1ull << 31) && a.mode != 2 && aligned16(a.query) &&
                          aligned16(a.key) && aligned16(a.value) && aligned16(a.query_out) && aligned16(kv.keys) &&
-                         aligned16(kv.values);
+                         aligned16(kv.values) && aligned16(a.query_norm) && aligned16(a.key_norm);
     if (rows_ok) {
         const dim3 grid((unsigned)((rows + 3) / 4));       // Granite: a wave per row
         const dim3 qgrid((unsigned)((rows * 5 + 3) / 4));  // Qwen: five waves per row

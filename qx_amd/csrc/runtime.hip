@@ -1536,6 +1536,22 @@ extern "C" int32_t qxh_encode_hbm_read_probe(qxh_graph* g, const void* data, uin
     return QXH_OK;
 }
 
+extern "C" int32_t qxh_encode_hbm_copy_probe(qxh_graph* g, const void* src, void* dst, uint64_t bytes,
+                                             int32_t nontemporal) {
+    int32_t r = check_graph(g);
+    if (r) return r;
+    QXH_REQUIRE(src && dst, QXH_ERR_INVALID_ARGUMENT, "hbm_copy_probe: null argument");
+    QXH_REQUIRE(bytes > 0 && bytes % 4096 == 0 && ((uintptr_t)src & 15) == 0 && ((uintptr_t)dst & 15) == 0,
+                QXH_ERR_INVALID_ARGUMENT,
+                "hbm_copy_probe: bytes must be a positive multiple of 4096 at 16-byte aligned addresses");
+    const uintptr_t s = (uintptr_t)src, d = (uintptr_t)dst;
+    QXH_REQUIRE(s + bytes <= d || d + bytes <= s, QXH_ERR_INVALID_ARGUMENT, "hbm_copy_probe: buffers overlap");
+    hipError_t e = launch_hbm_copy_probe(src, dst, bytes, nontemporal != 0, g->stream);
+    if (e != hipSuccess) return hip_fail(e, "hbm_copy_probe launch");
+    g->dispatches += 1;
+    return QXH_OK;
+}
+
 extern "C" int32_t qxh_encode_kv_fill_normal(qxh_graph* g, qxh_kv_cache* c, uint64_t seed, uint32_t length) {
     int32_t r = check_graph(g);
     if (r) return r;

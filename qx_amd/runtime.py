@@ -453,6 +453,14 @@ def hbm_read_probe(graph: Graph, data, sink, blocks: int = 0):
                                           blocks))
 
 
+def hbm_copy_probe(graph: Graph, src, dst, nontemporal: bool = True):
+    """One plain copy of `src` into `dst` (the bench's one-shot read + write floor)."""
+    n = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() < n:
+        raise ValueError("hbm_copy_probe: destination smaller than the source")
+    check(lib().qxh_encode_hbm_copy_probe(graph.handle, _ptr(src), _ptr(dst), n, 1 if nontemporal else 0))
+
+
 class QwenQ4Layer:
     """Q4 weights of one Qwen attention half: fp32 input norm [2048], Q4Matrix
     q (4096x2048), k, v (512x2048), fp32 q/k head norms [128], Q4Matrix o
