@@ -414,12 +414,12 @@ __global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs 
     const uint32_t kvh = blockIdx.x;
     const uint32_t pos = a.position;
 
-    // RoPE once per workgroup, through LDS: 32 threads evaluate the consensus
-    // sin/cos of the pairs; then one thread per element rotates q (G heads) and
-    // k (d < P: fma(-y, s, x c); d >= P: fma(y, c, x s) with x = v[d mod P],
-    // y = v[d mod P + P], granite_rope_pair), rounds k and v to the cache
-    // dtype, and stores the appended row and query_out.
-    __shared__ float sm_sin[P], sm_cos[P];
+    // RoPE once per workgroup: one thread per element of q (G heads), k and v
+    // loads its pair (x = v[d mod P], y = v[d mod P + P]) and the pair's
+    // inverse frequency at once, evaluates the consensus sin/cos itself,
+    // rotates (d < P: fma(-y, s, x c); d >= P: fma(y, c, x s),
+    // granite_rope_pair), rounds k and v to the cache dtype, and the rows go
+    // through LDS to the appended row, query_out and the attention below.
     __shared__ float sm_q[G][D], sm_k[D], sm_v[D];
     const int tid = threadIdx.x;
     const size_t head_off = (size_t)kvh * a.head_stride;
@@ -427,19 +427,23 @@ __global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs 
         if (tid < G * D) sm_q[tid / D][tid % D] = load_any(a.query, (size_t)kvh * G * D + tid, a.query_dtype);
         __syncthreads();
     } else {
-        if (tid < P) granite_rope_sin_cos(pos, (uint32_t)tid, sm_sin[tid], sm_cos[tid]);
-        __syncthreads();
+        // every load unconditional (threads past the rows read the value row
+        // again), so none waits behind a branch
+        const int row = tid / D, d = tid % D, i = d % P;
+        const uint32_t inv_bits = kGraniteInvFreqBits[i];
+        const float* v = row < G ? a.query + ((size_t)kvh * G + row) * D
+                                 : (row == G ? a.key : a.value) + (size_t)kvh * D;
+        const float x = v[i], y = v[i + P];
+        // granite_rope_sin_cos's operations: (float)position * inverse, consensus_sin_cos
+        float sn, cs;
+        consensus_sin_cos((float)pos * bits_f(inv_bits), sn, cs);
         if (tid < (G + 2) * D) {
-            const int row = tid / D, d = tid % D, i = d % P;
-            const float sn = sm_sin[i], cs = sm_cos[i];
             if (row < G + 1) {
-                const float* v = row < G ? a.query + ((size_t)kvh * G + row) * D : a.key + (size_t)kvh * D;
-                const float x = v[i], y = v[i + P];
                 const float r = d < P ? __builtin_fmaf(-y, sn, x * cs) : __builtin_fmaf(y, cs, x * sn);
                 if (row < G) sm_q[row][d] = r;
                 else sm_k[d] = round_to<KDT>(r);
             } else {
-                sm_v[d] = round_to<VDT>(a.value[(size_t)kvh * D + d]);
+                sm_v[d] = round_to<VDT>(d < P ? x : y);
             }
         }
         __syncthreads();  // every raw q/k/v read is done before query_out (may alias query) is written
@@ -812,6 +816,9 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
         if (n > 0) {
             u32x4 kr0[2][KSTEPS], vr0[VCH], kr1[2][KSTEPS], vr1[VCH];
             float vs_unused[VCH];
+            // (the query's loads first and two tiles requested before the
+            // first wait measured cfg 5a unchanged and cfg 4 305-320 -> 316-332
+            // us per layer-step)
             bload_tile(wave, kr0, vr0);
             load_q();  // after the first tile's loads: the query's latency hides under theirs
             for (uint32_t j = 0; j < n; j += 2) {

@@ -34,13 +34,16 @@ __device__ __forceinline__ f32x4 ldg4_nt(const float* p) {
 // fma, consensus rsqrt(mean + eps), y = x * scale * w.
 // The norm weights are loaded with the hidden slices, before the reduction,
 // so both requests are in flight together.
-__device__ __forceinline__ void normalize_slices(const float* hidden, const float* weight, int lane, f32x4 (&n)[4]) {
-    f32x4 x[4], w[4];
+__device__ __forceinline__ void load_slices(const float* hidden, const float* weight, int lane, f32x4 (&x)[4],
+                                            f32x4 (&w)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         x[i] = ldg4(hidden + 256 * i + 4 * lane);
         w[i] = ldg4(weight + 256 * i + 4 * lane);
     }
+}
+
+__device__ __forceinline__ void normalize_loaded(const f32x4 (&x)[4], const f32x4 (&w)[4], f32x4 (&n)[4]) {
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -81,16 +84,25 @@ __global__ __launch_bounds__(256) void granite_qkv_rope_kernel(KvLayer kv, Grani
         w = a.wv;
         head = hb - 24;
     }
-    // the two weight rows are requested first: their HBM latency overlaps
-    // the loads and the reduction of the norm
+    // Loads complete in order: the pair's inverse frequency and the hidden
+    // state and norm weights (every wave reads them, from L2) go first, the
+    // two weight rows from HBM last, so the angle and the norm are computed
+    // while the weight rows are in flight.
+    const uint32_t inv_bits = kGraniteInvFreqBits[p];
+    f32x4 hx[4], hw[4];
+    load_slices(a.hidden_in, a.input_norm, lane, hx, hw);
     f32x4 wx[4], wy[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         wx[i] = ldg4_nt(w + (size_t)(head * 64 + p) * kHidden + 256 * i + 4 * lane);
         wy[i] = ldg4_nt(w + (size_t)(head * 64 + 32 + p) * kHidden + 256 * i + 4 * lane);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    // granite_rope_sin_cos's operations: (float)position * inverse, consensus_sin_cos
+    float sn, cs;
+    consensus_sin_cos((float)a.position * bits_f(inv_bits), sn, cs);
     f32x4 n[4];
-    normalize_slices(a.hidden_in, a.input_norm, lane, n);
+    normalize_loaded(hx, hw, n);
     const float x = row_dot_loaded(wx, n);
     const float y = row_dot_loaded(wy, n);
     if (lane != 0) return;
@@ -105,8 +117,6 @@ __global__ __launch_bounds__(256) void granite_qkv_rope_kernel(KvLayer kv, Grani
         }
         return;
     }
-    float sn, cs;
-    granite_rope_sin_cos(a.position, (uint32_t)p, sn, cs);
     const float first = __builtin_fmaf(-y, sn, x * cs);
     const float second = __builtin_fmaf(y, cs, x * sn);
     if (hb < 16) {

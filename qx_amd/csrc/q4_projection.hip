@@ -129,18 +129,27 @@ __global__ __launch_bounds__(256) void granite_q4_qkv_rope_kernel(KvLayer kv, Gr
         head = hb - 24;
     }
     const int row = head * 64 + 32 * half + p;
-    const u32x4 grp = *reinterpret_cast<const u32x4*>(m.packed + (size_t)row * (kHidden / 2) + l * 16);
-    const float scale = f16_bits_to_float(m.scales[row * (kHidden / 32) + l]);
+    // Loads complete in order: the pair's inverse frequency and the hidden
+    // state and norm weights (from L2) first, the Q4 row from HBM last, so
+    // the angle and the norm are computed while the row is in flight.
+    const uint32_t inv_bits = kGraniteInvFreqBits[p];
     float x[4], w[4];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
         x[b] = a.hidden_in[t + 256 * b];
         w[b] = a.input_norm[t + 256 * b];
     }
-    s_codes[wave][lane] = grp;
+    const u32x4 grp = *reinterpret_cast<const u32x4*>(m.packed + (size_t)row * (kHidden / 2) + l * 16);
+    const uint16_t scale_bits = m.scales[row * (kHidden / 32) + l];
+    __builtin_amdgcn_sched_barrier(0);
+    // granite_rope_sin_cos's operations: (float)position * inverse, consensus_sin_cos
+    float sn, cs;
+    consensus_sin_cos((float)a.position * bits_f(inv_bits), sn, cs);
     const float inv = inverse_rms(square_sum_256(x, group_sums));
 #pragma unroll
     for (int b = 0; b < 4; ++b) s_in[t + 256 * b] = x[b] * inv * w[b];
+    s_codes[wave][lane] = grp;
+    const float scale = f16_bits_to_float(scale_bits);
     __syncthreads();
     const float sum = ordered_sum32(
         q4_fold32(reinterpret_cast<const uint8_t*>(&s_codes[wave][lane & 32]), scale, s_in, l, 0.0f));
@@ -157,8 +166,6 @@ __global__ __launch_bounds__(256) void granite_q4_qkv_rope_kernel(KvLayer kv, Gr
         }
         return;
     }
-    float sn, cs;
-    granite_rope_sin_cos(a.position, (uint32_t)p, sn, cs);
     const float first = __builtin_fmaf(-yr, sn, xr * cs);
     const float second = __builtin_fmaf(yr, cs, xr * sn);
     if (hb < 16) {
