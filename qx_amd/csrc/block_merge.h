@@ -82,4 +82,62 @@ __device__ __forceinline__ void merge_granite_attention(const float* ml, const f
     *dst = A * (1.0f / L);
 }
 
+// The same merge in two halves, so a caller can request its own HBM rows
+// between them: loads complete in order, so rows requested after the
+// partials let the fold run while the rows are still in flight.  The
+// result is merge_granite_attention's, bit for bit (the same loads, the same
+// fold in the same order).  splits == 1 reads `direct` into the first entry.
+struct MergeLoads {
+    float m[kBlockMergeMaxSplits], l[kBlockMergeMaxSplits];
+    merge_v4 a[kBlockMergeMaxSplits];
+};
+
+__device__ __forceinline__ void merge_granite_load(const float* ml, const float* acc, uint32_t splits,
+                                                   const float* direct, MergeLoads& x) {
+    const int t = threadIdx.x & 255;
+    const uint32_t hq = (uint32_t)t >> 4, d0 = ((uint32_t)t & 15u) * 4;
+    const uint32_t p0 = (hq >> 1) * splits * 2 + (hq & 1u);
+#pragma unroll
+    for (uint32_t i = 0; i < kBlockMergeMaxSplits; ++i) {
+        const uint32_t p = p0 + 2 * min(i, splits - 1);
+        const float* mp = splits == 1 ? direct : ml + 2 * p;  // splits == 1: any valid address
+        const float2 v = *reinterpret_cast<const float2*>(mp);
+        x.m[i] = v.x;
+        x.l[i] = v.y;
+        x.a[i] = *reinterpret_cast<const merge_v4*>(splits == 1 ? direct + hq * 64 + d0 : acc + (size_t)p * 64 + d0);
+    }
+}
+
+__device__ __forceinline__ void merge_granite_finish(MergeLoads& x, uint32_t splits, float* s_att) {
+    const int t = threadIdx.x;
+    if (t >= 256) return;
+    const uint32_t hq = (uint32_t)t >> 4, d0 = ((uint32_t)t & 15u) * 4;
+    merge_v4* dst = reinterpret_cast<merge_v4*>(s_att + hq * 64 + d0);
+    if (splits == 1) {
+        *dst = x.a[0];
+        return;
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kBlockMergeMaxSplits; ++i) {
+        if (i >= splits) {
+            x.m[i] = -1.0e30f;
+            x.l[i] = 0.0f;
+            x.a[i] = merge_v4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    float M = -1.0e30f;
+#pragma unroll
+    for (uint32_t i = 0; i < kBlockMergeMaxSplits; ++i) M = fmaxf(M, x.m[i]);
+    float L = 0.0f;
+    merge_v4 A = merge_v4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (uint32_t i = 0; i < kBlockMergeMaxSplits; ++i) {
+        const float f = fast_exp2(x.m[i] - M);  // 0 for the padding entries
+        L = __builtin_fmaf(x.l[i], f, L);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) A[j] = __builtin_fmaf(x.a[i][j], f, A[j]);
+    }
+    *dst = A * (1.0f / L);
+}
+
 }  // namespace qxh

@@ -145,20 +145,26 @@ __global__ __launch_bounds__(256) void granite_out_residual_kernel(GraniteBlockA
 // fp32 and mixed caches: the attention launch left split partials; every
 // workgroup merges them (block_merge.h) before its rows.  grid 1024 / (4 RPW)
 // workgroups x 4 waves, wave w of workgroup b owns rows 4 RPW b + RPW w .. +
-// RPW - 1; its weights are requested before the merge so the two latencies
-// overlap.
+// RPW - 1.  The partials (L2) are requested first and the weight rows (HBM)
+// behind them: loads complete in order, so the fold runs while the rows are
+// in flight.
 template <int RPW>
 __global__ __launch_bounds__(256) void granite_out_merge_residual_kernel(GraniteBlockArgs a) {
     __shared__ __attribute__((aligned(16))) float s_att[kHidden];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row0 = blockIdx.x * 4 * RPW + wave * RPW;
+    MergeLoads parts;
+    merge_granite_load(a.parts.ml, a.parts.acc, a.parts.splits, a.attention, parts);
+    const float resid_all = a.hidden_in[row0 + (lane < RPW ? lane : 0)];
+    __builtin_amdgcn_sched_barrier(0);  // the partials' requests stay ahead of the rows'
     f32x4 w[RPW][4];
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[r][i] = ldg4_nt(a.wo + (size_t)(row0 + r) * kHidden + 256 * i + 4 * lane);
-    const float resid = lane < RPW ? a.hidden_in[row0 + lane] : 0.0f;
-    merge_granite_attention(a.parts.ml, a.parts.acc, a.parts.splits, a.attention, s_att);
+    __builtin_amdgcn_sched_barrier(0);  // every request out before the fold
+    const float resid = lane < RPW ? resid_all : 0.0f;
+    merge_granite_finish(parts, a.parts.splits, s_att);
     __syncthreads();
     if (blockIdx.x == 0 && a.parts.splits > 1)
         for (int o = threadIdx.x; o < kHidden; o += 256) a.attention[o] = s_att[o];

@@ -206,6 +206,11 @@ __global__ __launch_bounds__(64 * WAVES) void granite_q4_out_merge_residual_kern
     __shared__ u32x4 s_codes[WAVES][64];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, l = lane & 31;
     const int row = blockIdx.x * 2 * WAVES + 2 * wave + (lane >> 5);
+    // The Q4 row is requested and stored to LDS before the partials are
+    // requested.  Measured (cfg2q4, us per token): this order 371-373, the
+    // partials first 383-384, both in flight together with the row's LDS
+    // store after the fold 384-386 (the fp32 kernel gains from the
+    // partials-first order).
     const u32x4 grp = *reinterpret_cast<const u32x4*>(a.wo.packed + (size_t)row * (kHidden / 2) + l * 16);
     const float scale = f16_bits_to_float(a.wo.scales[row * (kHidden / 32) + l]);
     const float resid = a.hidden_in[row];

@@ -74,23 +74,34 @@ __global__ __launch_bounds__(256) void qwen_norm_qkv_kernel(QwenBlockArgs a) {
         out = a.value;
     }
     constexpr int kGroups = kQwenHidden / 32;  // 64
+    // Loads complete in order: the hidden state and norm weights (L2) first,
+    // then the Q4 row from HBM, so the norm, its LDS stores and the barrier
+    // run while the row is in flight (the compiler's own order put the norm
+    // weights last, so the norm waited for the row).
+    uint16_t xb[8];
+    float w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        xb[k] = a.hidden[t + 256 * k];
+        w[k] = a.input_norm[t + 256 * k];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     const uint8_t* codes = m.packed + (size_t)row * (kQwenHidden / 2);
     const u32x4 g0 = *reinterpret_cast<const u32x4*>(codes + l * 16);
     const u32x4 g1 = *reinterpret_cast<const u32x4*>(codes + (l + 32) * 16);
-    float sc[kGroups / 32];
-    sc[0] = f16_bits_to_float(m.scales[row * kGroups + l]);
-    sc[1] = f16_bits_to_float(m.scales[row * kGroups + l + 32]);
-    float x[8], w[8];
+    const uint16_t sb0 = m.scales[row * kGroups + l], sb1 = m.scales[row * kGroups + l + 32];
+    __builtin_amdgcn_sched_barrier(0);
+    float x[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        x[k] = f16_bits_to_float(a.hidden[t + 256 * k]);
-        w[k] = a.input_norm[t + 256 * k];
-    }
-    s_codes[wave][half][l] = g0;
-    s_codes[wave][half][l + 32] = g1;
+    for (int k = 0; k < 8; ++k) x[k] = f16_bits_to_float(xb[k]);
     const float inv = qwen_inverse_rms(square_sum_256(x, wave_sums));
 #pragma unroll
     for (int k = 0; k < 8; ++k) s_in[t + 256 * k] = round_f16(x[k] * inv * w[k]);
+    s_codes[wave][half][l] = g0;
+    s_codes[wave][half][l + 32] = g1;
+    float sc[kGroups / 32];
+    sc[0] = f16_bits_to_float(sb0);
+    sc[1] = f16_bits_to_float(sb1);
     __syncthreads();
     const float sum = ordered_sum32(
         q4_fold_n<kGroups>(reinterpret_cast<const uint8_t*>(&s_codes[wave][half][0]), sc, s_in, l, 0.0f));
