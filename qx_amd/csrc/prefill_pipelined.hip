@@ -115,15 +115,41 @@ struct VtArgs {
 // One workgroup of D threads per (tile, kv head).  Thread (half, g, dg) reads
 // the eight positions whose probabilities a lane group leaves in one P^T
 // operand (4g..4g+3 and 16+4g..16+4g+3 of its 32-position half), 8 dims each
-// (one 16-byte load per position, consecutive threads on consecutive dims),
-// transposes the 8 x 8 block of 16-bit values in registers and writes the
-// 8 dims' 16-byte slot groups.
+// (one 16-byte load per position), transposes the 8 x 8 block of 16-bit
+// values in registers and writes the 8 dims' 16-byte slot groups.  Thread
+// index 8 dg + 4 half + g: eight consecutive threads read 128 contiguous
+// bytes of a V row and write one whole 128-byte V^T row (all 64 slots of
+// one dim), so every load and store instruction moves whole lines (the
+// mapping with consecutive threads on consecutive dims wrote each V^T row
+// as two 64-byte halves from two waves).
+__device__ __forceinline__ void vt_thread(int tid, int& dg, int& g, int& half) {
+    g = tid & 3;
+    half = (tid >> 2) & 1;
+    dg = tid >> 3;
+}
+
+// the 8 dims' 16-byte slot groups of a thread's transposed 8 x 8 block
+template <int D>
+__device__ __forceinline__ void vt_store(const u32x4 (&row)[8], uint16_t* vt_tile, int dg, int g, int half) {
+    uint16_t* dst = vt_tile + 32 * half + 8 * g;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int w = k >> 1;
+        u32x4 o;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t x = row[2 * q][w], y = row[2 * q + 1][w];
+            o[q] = (k & 1) ? (x >> 16) | (y & 0xffff0000u) : (x & 0xffffu) | (y << 16);
+        }
+        *reinterpret_cast<u32x4*>(dst + (size_t)(dg * 8 + k) * kTile) = o;
+    }
+}
 template <int D, int DT>
 __global__ __launch_bounds__(D) void prefill_vt_kernel(VtArgs a) {
-    constexpr int DG = D / 8;
     const uint32_t t = blockIdx.x, h = blockIdx.y;
     const int tid = threadIdx.x;
-    const int dg = tid % DG, g = (tid / DG) % 4, half = tid / (DG * 4);
+    int dg, g, half;
+    vt_thread(tid, dg, g, half);
     const char* vbase = reinterpret_cast<const char*>(a.values) + (size_t)h * a.head_stride * 2;
     u32x4 row[8];
     bool ovf = false;
@@ -149,20 +175,10 @@ __global__ __launch_bounds__(D) void prefill_vt_kernel(VtArgs a) {
         }
         row[j] = v;
     }
+    // the tile's stores go out before the flag's barrier
+    vt_store<D>(row, a.vt + ((size_t)h * a.vt_tiles + t) * D * kTile, dg, g, half);
     ovf = __syncthreads_or(ovf);
     if (tid == 0) a.flags[(size_t)h * a.vt_tiles + t] = ovf ? 1u : 0u;
-    uint16_t* dst = a.vt + ((size_t)h * a.vt_tiles + t) * D * kTile + 32 * half + 8 * g;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const int w = k >> 1;
-        u32x4 o;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t x = row[2 * q][w], y = row[2 * q + 1][w];
-            o[q] = (k & 1) ? (x >> 16) | (y & 0xffff0000u) : (x & 0xffffu) | (y << 16);
-        }
-        *reinterpret_cast<u32x4*>(dst + (size_t)(dg * 8 + k) * kTile) = o;
-    }
 }
 
 // The same V^T tiles from a tiered value cache: rows below the boundary are
@@ -185,48 +201,50 @@ struct TieredVtArgs {
 
 template <int D>
 __global__ __launch_bounds__(D) void prefill_vt_tiered_kernel(TieredVtArgs a) {
-    constexpr int DG = D / 8;
     const uint32_t t = blockIdx.x, h = blockIdx.y;
     const int tid = threadIdx.x;
-    const int dg = tid % DG, g = (tid / DG) % 4, half = tid / (DG * 4);
+    int dg, g, half;
+    vt_thread(tid, dg, g, half);
     const int8_t* codes = a.codes + (size_t)h * a.head_stride;
     const uint16_t* scales = a.scales + (size_t)h * a.head_stride / kTierBlock;
     const uint16_t* ring = a.ring + (size_t)h * a.ring_head_stride;
+    // Every row's codes, scale and window slot are requested unconditionally
+    // (the codes of any cache row and the slot of any position are valid
+    // addresses) and the tier picked afterwards: a load under a branch is
+    // waited for inside the branch, which made the eight rows eight round
+    // trips.  The window rows read from the ring are few and hot in L2.
+    uint32_t c0[8], c1[8];
+    uint16_t sb[8];
+    u32x4 rw[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t pos = t * kTile + 32 * half + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
+        const uint32_t src = min(pos, a.kv_len - 1);
+        const size_t e = (size_t)src * D + dg * 8;
+        const tv_u32x2 cw = *reinterpret_cast<const tv_u32x2*>(codes + e);
+        c0[j] = cw[0];
+        c1[j] = cw[1];
+        sb[j] = scales[e / kTierBlock];
+        rw[j] = *reinterpret_cast<const u32x4*>(ring + (size_t)(src & a.window_mask) * D + dg * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every request out before the first use
     u32x4 row[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const uint32_t pos = t * kTile + 32 * half + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
         const uint32_t src = min(pos, a.kv_len - 1);
-        if (src < a.tier) {
-            const size_t e = (size_t)src * D + dg * 8;
-            const uint32_t* cw = reinterpret_cast<const uint32_t*>(codes + e);
-            const uint32_t c0 = cw[0], c1 = cw[1];
-            const float sc = half_bits_to_f32(scales[e / kTierBlock]);
-            u32x4 v;
+        const float sc = half_bits_to_f32(sb[j]);
+        u32x4 v;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t w = (i < 2 ? c0 : c1) >> (16 * (i & 1));
-                const float lo = fminf(fmaxf((float)(int8_t)(w & 0xffu) * sc, -65504.0f), 65504.0f);
-                const float hi = fminf(fmaxf((float)(int8_t)((w >> 8) & 0xffu) * sc, -65504.0f), 65504.0f);
-                v[i] = (uint32_t)f32_to_half_bits(lo) | ((uint32_t)f32_to_half_bits(hi) << 16);
-            }
-            row[j] = v;
-        } else {
-            row[j] = *reinterpret_cast<const u32x4*>(ring + (size_t)(src & a.window_mask) * D + dg * 8);
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w = (i < 2 ? c0[j] : c1[j]) >> (16 * (i & 1));
+            const float lo = fminf(fmaxf((float)(int8_t)(w & 0xffu) * sc, -65504.0f), 65504.0f);
+            const float hi = fminf(fmaxf((float)(int8_t)((w >> 8) & 0xffu) * sc, -65504.0f), 65504.0f);
+            v[i] = (uint32_t)f32_to_half_bits(lo) | ((uint32_t)f32_to_half_bits(hi) << 16);
         }
+        row[j] = src < a.tier ? v : rw[j];
     }
-    uint16_t* dst = a.vt + ((size_t)h * a.vt_tiles + t) * D * kTile + 32 * half + 8 * g;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const int w = k >> 1;
-        u32x4 o;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t x = row[2 * q][w], y = row[2 * q + 1][w];
-            o[q] = (k & 1) ? (x >> 16) | (y & 0xffff0000u) : (x & 0xffffu) | (y << 16);
-        }
-        *reinterpret_cast<u32x4*>(dst + (size_t)(dg * 8 + k) * kTile) = o;
-    }
+    vt_store<D>(row, a.vt + ((size_t)h * a.vt_tiles + t) * D * kTile, dg, g, half);
 }
 
 // ---------------------------------------------------------------------------
