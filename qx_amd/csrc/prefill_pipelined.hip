@@ -805,16 +805,21 @@ static uint32_t pipe_columns(const ShapeDims& s) { return 32 * pipe_waves(s); }
 // kMaxPipeChunks); prefill_combine_kernel merges the chunks' partials.  The
 // chunk floor keeps a block's partials (per query column: m, l and D floats;
 // 256 columns for Qwen, 128 for Granite) small next to the K/V tiles a chunk
-// reads: 8 tiles for Granite, 32 for Qwen, whose 8 query heads per kv head
+// reads: 8 tiles for Granite, 16 for Qwen, whose 8 query heads per kv head
 // make its partials 8 times larger per tile.  Measured at start 0 (us per
 // prefill; no split / two chunks / four chunks): Granite f16 T=512 12.9 /
 // 14.3 / 14.4, T=1024 19.5 / 18.1 / 22.2, T=2048 32.8 / 32.3 / 35.3; Qwen bf16
 // T=1024 32.3 / 42.9 / 46.6, T=2048 58.6 / 76.5 / 90.  Long contexts are where
 // splitting pays: a 64-token Qwen prompt over 32704 cached positions is 16
-// workgroups of 513 rounds each without it.
+// workgroups of 513 rounds each without it.  Qwen floors of 32 / 16 / 8
+// tiles, prompts over cached positions (us per prefill, start + T): 2048 +
+// 512 59.3 / 48.1 / 42.9, 3000 + 1024 88 / 77.5 / 77, 4000 + 96 51.2 / 37.0 /
+// 33.1, 6000 + 192 56.9 / 45.4 / 51.9, 8000 + 64 63.4 / 40.8 / 34.5, 12000 +
+// 256 72.8 / 70.1 / 69.8; at start 0 T=1024 32.6 / 32.6 / 40.0 and T=2048 the
+// same for all three.  16 is never the slower of the first two.
 constexpr uint32_t kTargetWgs = 512;
 static uint32_t pipe_wgs_per_block(const ShapeDims& s) { return s.head_dim == 128 ? 2u : 1u; }
-static uint32_t min_chunk_tiles(const ShapeDims& s) { return s.head_dim == 128 ? 32u : 8u; }
+static uint32_t min_chunk_tiles(const ShapeDims& s) { return s.head_dim == 128 ? 16u : 8u; }
 
 static uint32_t pipe_blocks(const ShapeDims& s, uint32_t tokens) {
     const uint32_t wgt = pipe_tokens_per_wg(s);

@@ -79,10 +79,12 @@ def test_granite_prefill_fp16(ctx, T, start):
     assert e <= TOL_16
 
 
-# (40, 8150) and (300, 8000): the pipelined kernel with each block's KV range
-# split into 4 chunks; (9, 8150) and (4, 32764): causal rows on the MFMA
-# decode kernel (64 splits per row at 32768 positions)
-@pytest.mark.parametrize("T,start", [(8192, 0), (300, 0), (129, 64), (40, 8150), (300, 8000), (9, 8150), (4, 32764)])
+# (40, 8150), (300, 8000) and (512, 2048): the pipelined kernel with each
+# block's KV range split into chunks of at least 16 tiles (8, 7 and 2
+# chunks); (9, 8150) and (4, 32764): causal rows on the MFMA decode kernel
+# (64 splits per row at 32768 positions)
+@pytest.mark.parametrize("T,start", [(8192, 0), (300, 0), (129, 64), (40, 8150), (300, 8000), (512, 2048), (9, 8150),
+                                     (4, 32764)])
 def test_qwen_prefill_bf16(ctx, T, start):
     log("qwen prefill", T, start)
     rng = np.random.default_rng(T + 7 * start)
