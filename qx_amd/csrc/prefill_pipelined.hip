@@ -885,11 +885,15 @@ bool prefill_pipe_supported(const ShapeDims& s) {
 // with two chunks and the merge, 28.1-28.2 with two groups, 26.7-26.8 with
 // three (1.0 of 256 workgroups per CU, 12 waves each); a 512-token prompt
 // (64 blocks, not split) 14.6-14.7 alone, 13.8-14.0 with two groups, 14.9-15.5
-// with three.  A grouped workgroup takes a whole CU (96 or 144 KB of LDS),
-// so grids of more than 256 blocks, and prompts over long contexts that split
-// four or more ways, keep the chunked grid.
+// with three.  A grouped workgroup takes a whole CU (96 or 144 KB of LDS):
+// grids of 257-512 blocks (prompts of 2056-4096 tokens, the longest blocks
+// first) run as two rounds of workgroups with three groups each (a 4096-token
+// prompt 71.2 us unsplit, 58.5 with two groups, 56.0 with three), and
+// prompts over long contexts that split four or more ways keep the chunked
+// grid.
 static int pipe_kv_groups(bool direct_v, uint32_t blocks, uint32_t n_max, uint32_t chunks) {
-    if (!direct_v || n_max < 2 || blocks > 256) return 1;
+    if (!direct_v || n_max < 2 || blocks > 512) return 1;
+    if (blocks > 256) return 3;
     if ((chunks == 2 || chunks == 3) && n_max >= 3 && blocks >= 192) return 3;
     return chunks <= 2 ? 2 : 1;
 }

@@ -40,9 +40,12 @@ def bits(t):
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-# (20, 3000): the pipelined kernel with the KV range split into 5 chunks;
-# (6, 3000): causal rows on the MFMA decode kernel, split over the context
-@pytest.mark.parametrize("T,start", [(2048, 0), (100, 0), (77, 30), (1, 5), (33, 0), (200, 900), (20, 3000), (6, 3000)])
+# (2048, 0): 256 blocks, three KV groups per workgroup; (3000, 500): 376
+# blocks, two rounds of workgroups with three KV groups each; (20, 3000):
+# the pipelined kernel with the KV range split into 5 chunks; (6, 3000):
+# causal rows on the MFMA decode kernel, split over the context
+@pytest.mark.parametrize("T,start", [(2048, 0), (3000, 500), (100, 0), (77, 30), (1, 5), (33, 0), (200, 900), (20, 3000),
+                                     (6, 3000)])
 def test_granite_prefill_fp16(ctx, T, start):
     log("granite prefill", T, start)
     rng = np.random.default_rng(T * 31 + start)
