@@ -1175,7 +1175,16 @@ static DecodeArgs decode_args(const ShapeDims& s, const KvLayer& kv, const Decod
 // One sequence of a Granite fp32 or mixed cache at a short context: the
 // attention-only form of the step kernel, one workgroup per kv head, in one
 // dispatch (the split path needs a combine dispatch from 128 positions on).
-constexpr uint32_t kShortAttentionMax = 1024;
+// Eight workgroups pull the context slowly, so the split path takes over
+// past 320 positions.  Measured per layer (us, fp32 K/V, batch 1, 24 layers
+// rotated so the KV comes from the memory-side cache / 256 layers so it comes
+// from HBM; one dispatch / split path): 256 positions 4.8 / 5.3 against 5.9
+// / 6.2, 384 6.1 / 7.6 against 6.2 / 6.2, 512 6.7 / 9.0 against 6.3 / 6.2,
+// 1024 9.3 / 12.4 against 6.6 / 6.4.  One layer replayed from L2 (the
+// reference's isolated-attention case) still favours the one dispatch at 512
+// positions (7.6 against 9.0 us GPU median), which no multi-layer decode
+// sees.
+constexpr uint32_t kShortAttentionMax = 320;
 
 static bool short_attention(const ShapeDims& s, const KvLayer& kv, uint32_t sequences, uint32_t length) {
     return sequences == 1 && length <= kShortAttentionMax && s.head_dim == 64 && s.group == 2 &&

@@ -216,13 +216,14 @@ def test_mixed_kv_leaf_and_verification_hashes(ctx, shape, kdt, vdt):
 
 @pytest.mark.parametrize("kdt,vdt", [(abi.F32, abi.F32)] + MIXED)
 def test_short_single_sequence_attention(ctx, kdt, vdt):
-    """One sequence at contexts up to 1024 positions takes the one-dispatch
-    attention (one workgroup per kv head, 4, 8 or 16 waves by length): every
-    length class against the oracle at the fp32 bar, a 16-bit query and a
-    bf16 output once each, and the split path (the same sequence inside a
+    """One sequence at contexts up to 320 positions takes the one-dispatch
+    attention (one workgroup per kv head, 4 or 8 waves by length), longer
+    ones the split path: every length class and both sides of the 320
+    boundary against the oracle at the fp32 bar, a 16-bit query and a bf16
+    output once each, and the split path (the same sequence inside a
     two-sequence call) within the bar of it."""
     rng = np.random.default_rng(100 + 5 * kdt + vdt)
-    for length in (1, 37, 128, 129, 500, 768, 769, 1024):
+    for length in (1, 37, 128, 129, 320, 321, 500, 1024):
         arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 2, 1024, kdt, vdt)
         with rt.Graph(ctx) as g:
             arena.fill_normal(g, seed=length, length=length)
