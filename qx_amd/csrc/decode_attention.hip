@@ -1011,8 +1011,19 @@ bool decode_dtypes_supported(const ShapeDims& s, int key_dtype, int value_dtype)
     return s.head_dim == 64 && s.group == 2 && (key_dtype == F32 || value_dtype == F32);
 }
 
-static uint32_t qwen_min_chunk(int key_dtype, int value_dtype) {
-    return key_dtype == value_dtype && (key_dtype == F16 || key_dtype == BF16) ? 512u : 256u;
+// Qwen split floor: 512 positions on 16-bit caches (256 on the others),
+// halved down to one 32-position tile per wave while the grid would leave CUs
+// idle (fewer than 256 workgroups), which short contexts do.  Measured, bf16,
+// us per layer with the KV from HBM (fixed floor of 512 / adaptive): one
+// sequence at 1024 positions 11.7 / 8.2, 4096 12.2 / 8.8, 8192 12.6 / 10.1,
+// 16384 13.4 / 11.6, 32768 16.9 / 16.9; four sequences at 2048 12.8 / 10.3.
+constexpr uint32_t kDecodeCus = 256;
+static uint32_t qwen_min_chunk(int key_dtype, int value_dtype, uint32_t units, uint32_t length) {
+    const bool mfma16 = key_dtype == value_dtype && (key_dtype == F16 || key_dtype == BF16);
+    uint32_t floor = mfma16 ? 512u : 256u;
+    const uint32_t least = mfma16 ? (uint32_t)kWaves * 32u : floor;
+    while (floor > least && (uint64_t)units * ((length + floor - 1) / floor) < kDecodeCus) floor /= 2;
+    return floor;
 }
 
 DecodePlan plan_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t sequences, uint32_t length) {
@@ -1032,8 +1043,8 @@ DecodePlan plan_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint3
     // small next to the KV bytes it summarises (batch-1 Qwen3 decode at 32768
     // positions, bf16: 18.8 us per layer at 512, 19.1 at 256, 22.8 at 1024;
     // tiered: 18.0 us at 256, 20.2 at 512)
-    if (s.group >= 8 && min_chunk < qwen_min_chunk(key_dtype, value_dtype))
-        min_chunk = qwen_min_chunk(key_dtype, value_dtype);
+    if (s.group >= 8 && min_chunk < qwen_min_chunk(key_dtype, value_dtype, units, length))
+        min_chunk = qwen_min_chunk(key_dtype, value_dtype, units, length);
     uint32_t want = (target_wgs + units - 1) / units;
     uint32_t cap = (length + min_chunk - 1) / min_chunk;
     uint32_t splits = want < cap ? want : cap;
@@ -1313,9 +1324,11 @@ uint64_t decode_causal_workspace_bound(const ShapeDims& s, int key_dtype, int va
     const uint32_t units = tokens * (uint32_t)s.kv_heads;
     const bool valu = valu_path(key_dtype, value_dtype);
     const uint32_t rpw = (uint32_t)rows_per_wave_load(s.head_dim, key_dtype);
+    // the least floor any length up to the capacity can take (the floor
+    // shrinks for short contexts)
     uint32_t min_chunk = valu ? kWaves * rpw * kUnroll : kWaves * 32;
-    if (s.group >= 8 && min_chunk < qwen_min_chunk(key_dtype, value_dtype))
-        min_chunk = qwen_min_chunk(key_dtype, value_dtype);
+    if (s.group >= 8 && min_chunk < qwen_min_chunk(key_dtype, value_dtype, 0, capacity))
+        min_chunk = qwen_min_chunk(key_dtype, value_dtype, 0, capacity);
     const uint32_t want = (2048 + units - 1) / units;
     const uint32_t cap = (capacity + min_chunk - 1) / min_chunk;
     uint32_t bound = want < cap ? want : cap;
