@@ -361,13 +361,18 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillPipeArgs a) 
 // ---------------------------------------------------------------------------
 // Split KV: a prompt whose query blocks give fewer than kF32TargetWgs
 // workgroups cuts each block's KV range into chunks of at least
-// kF32MinChunkTiles tiles.  The kernel is bound by the fp32 matrix cores, so
-// the longest block's chain of tiles sets the time unless it is cut short.
+// f32_min_chunk_tiles tiles.  The kernel is bound by the fp32 matrix cores
+// (a 64-position tile is about 4 us of one wave's matrix-core time), so the
+// longest block's chain of tiles sets the time unless it is cut short.
 // Measured, Granite 2048-token prompt at start 0 (Fp32KFp16V / fp32 K/V, us):
 // 512 workgroups and chunks of 8 tiles or more 160 / 159, 1024 and 4 tiles
 // 129 / 128, 1024 and 2 tiles 130 / 127, 2048 and 4 tiles 119.5 / 117.5.
+// Floors of 4 / 2 / 1 tiles, Fp32KFp16V (us per prefill, start + T): 0 + 128
+// 16.3 / 16.2 / 14.4, 0 + 256 25.4 / 19.6 / 15.7, 0 + 512 31.0 / 23.3 / 25.3,
+// 0 + 1024 51.7 / 49.3 / 54.6, 1000 + 100 30.7 / 20.3 / 24.3, 2048 tokens and
+// more the same: one tile for prompts of at most four, two otherwise.
 constexpr uint32_t kF32TargetWgs = 2048;
-constexpr uint32_t kF32MinChunkTiles = 4;
+static uint32_t f32_min_chunk_tiles(uint32_t n_max) { return n_max <= 4 ? 1u : 2u; }
 constexpr uint32_t kF32MaxChunks = 32;
 constexpr uint32_t kF32Columns = 128;
 
@@ -389,7 +394,7 @@ static uint32_t f32_max_chunks(const ShapeDims& s, uint32_t tokens, uint32_t cap
     if (wgs >= kF32TargetWgs) return 1;
     uint32_t want = (kF32TargetWgs + wgs - 1) / wgs;
     if (want > kF32MaxChunks) want = kF32MaxChunks;
-    const uint32_t fit = (capacity + kPrefillTile - 1) / kPrefillTile / kF32MinChunkTiles;
+    const uint32_t fit = (capacity + kPrefillTile - 1) / kPrefillTile;  // the one-tile floor
     if (want > fit) want = fit;
     return want < 1 ? 1 : want;
 }
@@ -397,7 +402,7 @@ static uint32_t f32_max_chunks(const ShapeDims& s, uint32_t tokens, uint32_t cap
 static uint32_t f32_chunk_tiles(const ShapeDims& s, uint32_t start, uint32_t tokens, uint32_t capacity) {
     const uint32_t want = f32_max_chunks(s, tokens, capacity);
     const uint32_t n_max = (start + tokens + kPrefillTile - 1) / kPrefillTile;
-    const uint32_t fit = n_max / kF32MinChunkTiles;
+    const uint32_t fit = n_max / f32_min_chunk_tiles(n_max);
     const uint32_t chunks = want < fit ? want : fit;
     if (chunks <= 1) return 0;
     return (n_max + chunks - 1) / chunks;
