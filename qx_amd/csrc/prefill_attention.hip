@@ -38,34 +38,51 @@ constexpr uint32_t kExactPassWgs = 256;
 // at 8188, 42 / 56 for 16 rows; at 32764, 19 / 71 for one row, 71 / 71 for 8,
 // 142 / 69 for 16.  Granite f16 at 3840: 18 / 17 for 16 rows, 48 / 20 for 63.
 // Rows run on the decode kernels up to 8 of them, or while rows x context
-// stays under the measured crossover (about 150000 for Qwen, 40000 for
-// Granite, whose rows are cheaper per position than its pipelined call).
+// stays under the measured crossover with the kernel the call would take
+// otherwise: about 150000 for Qwen, 70000 for the Granite fp32 matrix-core
+// kernel (fp32 and mixed caches), 14000 for Granite f16 (the pipelined kernel
+// reading V straight from the cache, one dispatch: there rows also need at
+// most 16 of them and 64 cached positions), 40000 for the other Granite plans.
+// Measured (us, rows / tiled, 9-63 rows at 0-4000 cached positions):
+// Fp32KFp16V 4000 + 16 19.6 / 22.1, 1500 + 48 23.9 / 21.5; Granite f16
+// 500 + 16 10.0 / 11.1, 500 + 32 12.8 / 11.6, 500 + 63 18.2 / 12.1, 1500 + 9
+// 11.1 / 12.4, 0 + 16 7.0 / 6.0, 0 + 63 7.1 / 6.4; Qwen bf16 16000 + 9 37.1 /
+// 44.6, 16000 + 16 57.4 / 43.9, 4000 + 32 31.9 / 38.8, 4000 + 48 45.2 / 34.6.
 // The former short-prompt kernel, one 8-head workgroup per kv head, took
 // 1.31 ms for 1-16 rows at 32764 Qwen positions.
 constexpr uint32_t kDecodeRowsAlways = 8;
-static uint64_t decode_rows_budget(const ShapeDims& s) { return s.group >= 8 ? 150000u : 40000u; }
+static uint64_t decode_rows_budget(const ShapeDims& s, int key_dtype, int value_dtype) {
+    if (s.group >= 8) return 150000u;
+    if (prefill_f32_supported(s, key_dtype, value_dtype)) return 70000u;
+    if (key_dtype == F16 && value_dtype == F16) return 14000u;
+    return 40000u;
+}
 
-static bool rows_on_decode(const ShapeDims& s, uint32_t start, uint32_t tokens) {
-    return tokens <= kDecodeRowsAlways ||
-           (tokens < 64 && (uint64_t)tokens * (start + tokens) <= decode_rows_budget(s));
+static bool rows_on_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t start, uint32_t tokens) {
+    if (tokens <= kDecodeRowsAlways) return true;
+    if (tokens >= 64 || (uint64_t)tokens * (start + tokens) > decode_rows_budget(s, key_dtype, value_dtype)) return false;
+    const bool granite_f16 = s.group < 8 && key_dtype == F16 && value_dtype == F16;
+    return !granite_f16 || (tokens <= 16 && start >= 64);
 }
 
 static bool prefill_on_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t start, uint32_t tokens) {
-    return key_dtype == F32 || key_dtype != value_dtype || !prefill_pipe_supported(s) || rows_on_decode(s, start, tokens);
+    return key_dtype == F32 || key_dtype != value_dtype || !prefill_pipe_supported(s) ||
+           rows_on_decode(s, key_dtype, value_dtype, start, tokens);
 }
 
 // fp32 and mixed K/V caches at the Granite shape beyond a few rows take the
 // fp32 matrix-core kernel (prefill_f32.hip); Qwen-shape fp32 caches and
 // tiered values stay on causal decode rows.
 static bool prefill_on_f32(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t start, uint32_t tokens) {
-    return prefill_f32_supported(s, key_dtype, value_dtype) && !rows_on_decode(s, start, tokens);
+    return prefill_f32_supported(s, key_dtype, value_dtype) && !rows_on_decode(s, key_dtype, value_dtype, start, tokens);
 }
 
 // Tiered values with 16-bit keys take the pipelined MFMA prefill when the
 // rows would (its V^T pre-pass reading the tiers); the others stay on the
 // decode kernels.
 static bool tiered_on_pipe(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t start, uint32_t tokens) {
-    return value_dtype == I8T && key_dtype != F32 && prefill_pipe_supported(s) && !rows_on_decode(s, start, tokens);
+    return value_dtype == I8T && key_dtype != F32 && prefill_pipe_supported(s) &&
+           !rows_on_decode(s, key_dtype, value_dtype, start, tokens);
 }
 
 // Covers every start position: below 64 rows a call may take either path.
