@@ -1045,7 +1045,27 @@ DecodePlan plan_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint3
     // tiered: 18.0 us at 256, 20.2 at 512)
     if (s.group >= 8 && min_chunk < qwen_min_chunk(key_dtype, value_dtype, units, length))
         min_chunk = qwen_min_chunk(key_dtype, value_dtype, units, length);
-    uint32_t want = (target_wgs + units - 1) / units;
+    // Granite on the MFMA kernel: a split adds the combine dispatch (about
+    // 2.5 us), which a short context never wins back, so one chunk per head up
+    // to 768 positions, or up to 2048 once the heads alone make 128 or more
+    // workgroups.  Measured, f16, us per layer (split to 2048 workgroups / one
+    // chunk): one sequence at 256 positions 5.9 / 3.5, at 768 6.0 / 5.8, at
+    // 1024 6.3 / 7.3; 16 sequences at 1024 13.1 / 9.1, at 2048 15.8 (split to
+    // 256) / 15.6; 64 sequences at 512 20.4 / 12.7.
+    if (!valu && s.group < 8 && (length <= 768 || (units >= 128 && length <= 2048)) && length > min_chunk)
+        min_chunk = length;
+    // Split count: toward 2048 workgroups on the VALU kernel; on the MFMA
+    // kernel at most 256 (one a CU), rounded down, since each split costs a
+    // share of the combine's workspace round trip and a count rounded up past
+    // 256 workgroups leaves a second round on some CUs.  Measured, us per
+    // layer, KV from HBM (toward 2048 / up to 256, rounded up / rounded
+    // down): Granite f16, 4 sequences at 4096 positions 13.0 / 10.4 / 10.4,
+    // 5 at 4096 14.6 / 15.1 / 11.9; Qwen bf16, 24 sequences at 16384
+    // 146.3 / 173.7 / 130.0, 16 at 32768 177.4 / 166.5 / 166.5; causal rows
+    // of one Qwen sequence, 9 over 32000 positions 89.6 / 90.3 / 53.5, 24
+    // over 16000 88.6 / 117.1 / 78.5.  The VALU kernel (Granite fp32) is
+    // faster toward 2048.
+    uint32_t want = valu ? (target_wgs + units - 1) / units : (units < 256 ? 256 / units : 1u);
     uint32_t cap = (length + min_chunk - 1) / min_chunk;
     uint32_t splits = want < cap ? want : cap;
     if (splits < 1) splits = 1;

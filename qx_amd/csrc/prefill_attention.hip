@@ -37,32 +37,34 @@ constexpr uint32_t kExactPassWgs = 256;
 // Qwen bf16 at 1020 cached positions 14 / 31 for 1-8 rows, 31 / 32 for 63;
 // at 8188, 42 / 56 for 16 rows; at 32764, 19 / 71 for one row, 71 / 71 for 8,
 // 142 / 69 for 16.  Granite f16 at 3840: 18 / 17 for 16 rows, 48 / 20 for 63.
-// Rows run on the decode kernels up to 8 of them, or while rows x context
-// stays under the measured crossover with the kernel the call would take
-// otherwise: about 150000 for Qwen, 70000 for the Granite fp32 matrix-core
-// kernel (fp32 and mixed caches), 14000 for Granite f16 (the pipelined kernel
-// reading V straight from the cache, one dispatch: there rows also need at
-// most 16 of them and 64 cached positions), 40000 for the other Granite plans.
-// Measured (us, rows / tiled, 9-63 rows at 0-4000 cached positions):
-// Fp32KFp16V 4000 + 16 19.6 / 22.1, 1500 + 48 23.9 / 21.5; Granite f16
-// 500 + 16 10.0 / 11.1, 500 + 32 12.8 / 11.6, 500 + 63 18.2 / 12.1, 1500 + 9
-// 11.1 / 12.4, 0 + 16 7.0 / 6.0, 0 + 63 7.1 / 6.4; Qwen bf16 16000 + 9 37.1 /
-// 44.6, 16000 + 16 57.4 / 43.9, 4000 + 32 31.9 / 38.8, 4000 + 48 45.2 / 34.6.
+// Rows run on the decode kernels up to 8 of them, or, below 64, while
+// (rows - c) x context stays under the crossover measured against the kernel
+// the call would take otherwise (rows / tiled, us, 9-63 rows over 0-32000
+// cached positions, each case timed both ways in one process):
+// - Qwen (c = 6, 126000): 4000 + 32 29.0 / 38.7, 4000 + 48 41.0 / 34.1,
+//   16000 + 12 40.2 / 43.9, 16000 + 16 45.4 / 43.8, 32000 + 9 53.2 / 59.3,
+//   32000 + 12 69.3 / 59.3;
+// - Granite f16 (c = 0, 70000, and at least 64 cached positions; the
+//   pipelined kernel reads V straight from the cache, one dispatch):
+//   2000 + 32 12.1 / 13.2, 1500 + 48 17.2 / 14.4, 4000 + 9 12.2 / 13.7,
+//   4000 + 12 15.4 / 13.7, 0 + 9 7.7 / 5.9;
+// - Granite bf16 (c = 0, 90000): 3000 + 32 17.1 / 19.1, 2000 + 48 21.7 /
+//   18.2, 8000 + 9 18.5 / 24.5, 8000 + 16 25.3 / 24.2;
+// - the Granite fp32 matrix-core kernel (fp32 and mixed caches; c = 0,
+//   70000): Fp32KFp16V 4000 + 16 19.6 / 22.1, 1500 + 48 23.9 / 21.5;
+// - the other Granite plans (tiered values): c = 0, 40000.
 // The former short-prompt kernel, one 8-head workgroup per kv head, took
 // 1.31 ms for 1-16 rows at 32764 Qwen positions.
 constexpr uint32_t kDecodeRowsAlways = 8;
-static uint64_t decode_rows_budget(const ShapeDims& s, int key_dtype, int value_dtype) {
-    if (s.group >= 8) return 150000u;
-    if (prefill_f32_supported(s, key_dtype, value_dtype)) return 70000u;
-    if (key_dtype == F16 && value_dtype == F16) return 14000u;
-    return 40000u;
-}
-
 static bool rows_on_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t start, uint32_t tokens) {
     if (tokens <= kDecodeRowsAlways) return true;
-    if (tokens >= 64 || (uint64_t)tokens * (start + tokens) > decode_rows_budget(s, key_dtype, value_dtype)) return false;
-    const bool granite_f16 = s.group < 8 && key_dtype == F16 && value_dtype == F16;
-    return !granite_f16 || (tokens <= 16 && start >= 64);
+    if (tokens >= 64) return false;
+    const uint64_t length = (uint64_t)start + tokens;
+    if (s.group >= 8) return (tokens - 6) * length <= 126000u;
+    if (prefill_f32_supported(s, key_dtype, value_dtype)) return tokens * length <= 70000u;
+    if (key_dtype == F16 && value_dtype == F16) return start >= 64 && tokens * length <= 70000u;
+    if (key_dtype == BF16 && value_dtype == BF16) return tokens * length <= 90000u;
+    return tokens * length <= 40000u;
 }
 
 static bool prefill_on_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t start, uint32_t tokens) {

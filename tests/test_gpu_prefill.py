@@ -41,11 +41,11 @@ def bits(t):
 
 
 # (2048, 0): 256 blocks, three KV groups per workgroup; (3000, 500): 376
-# blocks, two rounds of workgroups with three KV groups each; (20, 3000):
-# the pipelined kernel with the KV range split into 5 chunks; (6, 3000):
-# causal rows on the MFMA decode kernel, split over the context
-@pytest.mark.parametrize("T,start", [(2048, 0), (3000, 500), (100, 0), (77, 30), (1, 5), (33, 0), (200, 900), (20, 3000),
-                                     (6, 3000)])
+# blocks, two rounds of workgroups with three KV groups each; (40, 3000):
+# the pipelined kernel with the KV range split into 6 chunks; (6, 3000) and
+# (20, 3000): causal rows on the MFMA decode kernel, split over the context
+@pytest.mark.parametrize("T,start", [(2048, 0), (3000, 500), (100, 0), (77, 30), (1, 5), (33, 0), (200, 900), (40, 3000),
+                                     (6, 3000), (20, 3000)])
 def test_granite_prefill_fp16(ctx, T, start):
     log("granite prefill", T, start)
     rng = np.random.default_rng(T * 31 + start)
@@ -264,12 +264,12 @@ TORCH = {abi.F32: torch.float32, abi.F16: torch.float16, abi.BF16: torch.bfloat1
 # Granite f16 (V tiles read straight from the cache: workgroups of two KV
 # groups (300 rows; 100 rows after 1000, two groups where the grid would have
 # split in two), three groups (2000 rows, 256 blocks) and the chunked grid
-# with its merge (20 rows after 3000, six chunks)), Granite bf16 and Qwen
+# with its merge (40 rows after 3000, six chunks)), Granite bf16 and Qwen
 # bf16 (V^T pre-pass), Fp32KFp16V (fp32 matrix-core kernel; one chunk, then
 # several) and a few rows (causal decode rows).
 @pytest.mark.parametrize("shape,kdt,vdt,start,T", [
     (abi.SHAPE_GRANITE, abi.F16, abi.F16, 0, 300), (abi.SHAPE_GRANITE, abi.F16, abi.F16, 1000, 100),
-    (abi.SHAPE_GRANITE, abi.F16, abi.F16, 0, 2000), (abi.SHAPE_GRANITE, abi.F16, abi.F16, 3000, 20),
+    (abi.SHAPE_GRANITE, abi.F16, abi.F16, 0, 2000), (abi.SHAPE_GRANITE, abi.F16, abi.F16, 3000, 40),
     (abi.SHAPE_GRANITE, abi.BF16, abi.BF16, 0, 300), (abi.SHAPE_QWEN3, abi.BF16, abi.BF16, 0, 300),
     (abi.SHAPE_GRANITE, abi.F32, abi.F16, 0, 300), (abi.SHAPE_GRANITE, abi.F32, abi.F16, 1000, 100),
     (abi.SHAPE_GRANITE, abi.F16, abi.F16, 37, 6)])

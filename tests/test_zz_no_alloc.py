@@ -64,14 +64,15 @@ def test_no_alloc_matches_workspace_entry_on_two_calls(ctx):
 
 
 def test_no_alloc_refuses_partials_beyond_the_scratch(ctx):
-    # 511 Qwen sequences at 1024 positions: 2044 units x 2 splits (of 512
+    # 511 Qwen sequences at 1024 positions on fp32 caches (the VALU kernel,
+    # which splits toward 2048 workgroups): 2044 units x 2 splits (of 512
     # positions) x 8 heads x 130 floats = 17.0 MB of partials, above the
     # 16 MiB scratch
     log("no-alloc: oversize request")
-    arena = rt.KvArena(ctx, abi.SHAPE_QWEN3, 1, 511, 1024, abi.BF16)
+    arena = rt.KvArena(ctx, abi.SHAPE_QWEN3, 1, 511, 1024, abi.F32)
     arena.set_len(1024)
     assert rt.attention_workspace_bytes(arena, 511, 1024) > SCRATCH_BYTES
-    q = torch.zeros((511, 32, 128), dtype=torch.bfloat16, device="cuda:0")
+    q = torch.zeros((511, 32, 128), device="cuda:0")
     out = torch.empty_like(q)
     g = rt.Graph(ctx)
     with pytest.raises(abi.QxhError, match="device scratch") as ei:
