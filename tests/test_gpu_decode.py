@@ -112,6 +112,54 @@ def test_granite_decode_lengths_and_dtypes(ctx, kdt, length):
             assert e <= tol, (s, e)
 
 
+# The MFMA decode plan's boundaries (16-bit caches): Granite keeps one chunk
+# per head up to 768 positions, or up to 2048 once the heads make 128 or more
+# workgroups; past that, and for Qwen, the split count is at most 256
+# workgroups' worth, rounded down (3 sequences = 24 Granite units: 7 splits
+# at 769 positions, 8 at 4096; 16 sequences = 128 units: 2 at 2049; 3 Qwen
+# sequences = 12 units: 19 at 16384).  Each case against the oracle, and the
+# plan's shape read from its workspace size (zero for one chunk).
+@pytest.mark.parametrize("shape,kdt,S,L,single", [
+    (abi.SHAPE_GRANITE, abi.F16, 3, 768, True), (abi.SHAPE_GRANITE, abi.F16, 3, 769, False),
+    (abi.SHAPE_GRANITE, abi.BF16, 3, 4096, False), (abi.SHAPE_GRANITE, abi.F16, 16, 2048, True),
+    (abi.SHAPE_GRANITE, abi.BF16, 16, 2049, False), (abi.SHAPE_QWEN3, abi.BF16, 3, 16384, False)])
+def test_mfma_decode_plan_boundaries(ctx, shape, kdt, S, L, single):
+    log("mfma decode plan boundary", shape, kdt, S, L)
+    info = rt.shape_info(shape)
+    arena = rt.KvArena(ctx, shape, 1, S, L, kdt)
+    dt = rt.torch_dtype(kdt)
+    q = torch.empty((S, info.q_heads, info.head_dim), dtype=dt, device="cuda:0")
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=S * 131 + L, length=L)
+        rt.fill_normal(g, q, seed=L + 5)
+    ws = rt.attention_workspace_bytes(arena, S, L)
+    units = S * info.kv_heads
+    partial = units * (info.q_heads // info.kv_heads) * (info.head_dim + 2) * 4
+    if single:
+        assert ws == 0
+    else:
+        assert ws > 0 and ws % partial == 0
+        splits = ws // partial
+        assert splits >= 2 and units * splits <= 256, splits
+    with rt.Graph(ctx) as g:
+        out = rt.attention(g, arena, 0, q, L, out_dtype=torch.float32)
+    tobits = lambda t: t.contiguous().view(torch.int16).cpu().numpy().ravel().view(np.uint16)
+    worst = 0.0
+    for s in range(S):
+        with rt.Graph(ctx) as g:
+            kk, vv = arena.gather(g, 0, s, 0, L)
+        if shape == abi.SHAPE_GRANITE:
+            ref_cache = O.KvCache(L)
+            ref_cache.extend(kk.float().cpu().numpy(), vv.float().cpu().numpy())
+            r = O.granite_attend(q[s].float().cpu().numpy().ravel(), ref_cache, L)
+        else:
+            _, r = O.qwen_gqa_attention(tobits(q[s]), tobits(kk), tobits(vv), O.BF16, want_f32=True)
+        e = rel_err(out[s].cpu().numpy().ravel(), r)
+        worst = max(worst, e)
+        assert e <= TOL_16, (s, e)
+    log(f"  workspace {ws} B, worst max-abs/rms {worst:.3e} over {S} sequences")
+
+
 def fp32_cases(ctx, S, L, seed):
     """GPU decode of S fp32 sequences at length L; per sequence (gpu, oracle, exact)."""
     arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, S, L, abi.F32)
