@@ -1064,8 +1064,11 @@ DecodePlan plan_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint3
     // 146.3 / 173.7 / 130.0, 16 at 32768 177.4 / 166.5 / 166.5; causal rows
     // of one Qwen sequence, 9 over 32000 positions 89.6 / 90.3 / 53.5, 24
     // over 16000 88.6 / 117.1 / 78.5.  The VALU kernel (Granite fp32) is
-    // faster toward 2048.
-    uint32_t want = valu ? (target_wgs + units - 1) / units : (units < 256 ? 256 / units : 1u);
+    // faster toward 2048, and so are tiered values on the MFMA kernel, whose
+    // splits of 256 positions beat 512 (Qwen at 32768 positions 16.7 against
+    // 19.1 us per layer).
+    const bool cap256 = !valu && !tiered_on_mfma(s, key_dtype, value_dtype);
+    uint32_t want = cap256 ? (units < 256 ? 256 / units : 1u) : (target_wgs + units - 1) / units;
     uint32_t cap = (length + min_chunk - 1) / min_chunk;
     uint32_t splits = want < cap ? want : cap;
     if (splits < 1) splits = 1;

@@ -52,7 +52,9 @@ constexpr uint32_t kExactPassWgs = 256;
 //   18.2, 8000 + 9 18.5 / 24.5, 8000 + 16 25.3 / 24.2;
 // - the Granite fp32 matrix-core kernel (fp32 and mixed caches; c = 0,
 //   70000): Fp32KFp16V 4000 + 16 19.6 / 22.1, 1500 + 48 23.9 / 21.5;
-// - the other Granite plans (tiered values): c = 0, 40000.
+// - the other Granite plans (tiered values): c = 0, 40000;
+// - Qwen with tiered values (c = 0, 150000), whose decode rows keep splits
+//   toward 2048 workgroups.
 // The former short-prompt kernel, one 8-head workgroup per kv head, took
 // 1.31 ms for 1-16 rows at 32764 Qwen positions.
 constexpr uint32_t kDecodeRowsAlways = 8;
@@ -60,7 +62,8 @@ static bool rows_on_decode(const ShapeDims& s, int key_dtype, int value_dtype, u
     if (tokens <= kDecodeRowsAlways) return true;
     if (tokens >= 64) return false;
     const uint64_t length = (uint64_t)start + tokens;
-    if (s.group >= 8) return (tokens - 6) * length <= 126000u;
+    if (s.group >= 8)
+        return value_dtype == I8T ? tokens * length <= 150000u : (tokens - 6) * length <= 126000u;
     if (prefill_f32_supported(s, key_dtype, value_dtype)) return tokens * length <= 70000u;
     if (key_dtype == F16 && value_dtype == F16) return start >= 64 && tokens * length <= 70000u;
     if (key_dtype == BF16 && value_dtype == BF16) return tokens * length <= 90000u;
