@@ -156,6 +156,22 @@ template <int N> __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Per-head RMSNorm and RoPE of one Qwen head row (128 dims) held by the 64
+// lanes of a wave as (x[lane], x[64 + lane]), norm weights (nl, nr), rotation
+// (cs, sn) of pair `lane` (qx_qwen_qk_norm_rope, kernels/qwen_attention.metal:
+// 138-177).  One definition for every kernel that rotates a single token's
+// heads, so they agree bit for bit.
+__device__ __forceinline__ void qwen_head_norm_rope(float xl, float xr, float nl, float nr, float cs, float sn,
+                                                    float& o_l, float& o_r) {
+    float ss = xl * xl + xr * xr;
+    ss = group_sum<64>(ss);
+    const float inv_rms = 1.0f / __builtin_sqrtf(ss / 128.0f + 1.0e-6f);
+    const float left = xl * inv_rms * nl;
+    const float right = xr * inv_rms * nr;
+    o_l = left * cs - right * sn;
+    o_r = right * cs + left * sn;
+}
+
 // Exchange with lane ^ mask for power-of-two masks.
 __device__ __forceinline__ float lane_xor(float v, int mask) {
     if (mask == 1) return dpp_quad_xor1(v);

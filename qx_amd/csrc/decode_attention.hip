@@ -59,6 +59,11 @@ struct DecodeArgs {
 
 constexpr float kNegBig = -1.0e30f;
 
+template <int DT> __device__ __forceinline__ uint16_t bits16(float x) {
+    if constexpr (DT == F16) return __builtin_bit_cast(uint16_t, (half_t)x);
+    else return f32_to_bf16_bits(x);
+}
+
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 template <bool NT> __device__ __forceinline__ u32x2 load8(const void* p) {
@@ -608,8 +613,8 @@ __global__ __launch_bounds__(64 * WAVES) void decode_step_kernel(DecodeStepArgs 
 // rounded to f16) below the boundary and from the f16 window above it, each
 // wave's rows cut at the boundary into two passes; P.V then runs in f16
 // whatever the key dtype, since the tile holds f16 values.
-template <int D, int G, int KDT, int WAVES, bool TV = false>
-__global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
+template <int D, int G, int KDT, int WAVES, bool TV, bool FRONT>
+__device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a, const QwenFrontArgs* fr) {
     using M = MfmaT<KDT>;
     using vec = typename M::vec;
     using MV = MfmaT<TV ? F16 : KDT>;  // P.V operands
@@ -624,6 +629,9 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
     __shared__ float sm_m[WAVES][G];
     __shared__ float sm_l[WAVES][G];
     __shared__ __attribute__((aligned(16))) float sm_acc[WAVES][G][D];
+    // front end: rotated query heads, and the new key and value rows
+    __shared__ __attribute__((aligned(16))) uint16_t sm_q[FRONT ? G : 1][FRONT ? D : 8];
+    __shared__ __attribute__((aligned(16))) uint16_t sm_kv[FRONT ? 2 : 1][FRONT ? D : 8];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int lg = lane >> 4, li = lane & 15;
@@ -634,6 +642,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
     const uint32_t r0 = split * a.chunk;
     const uint32_t r1 = min(length, r0 + a.chunk);
     const float c = a.qscale;  // softmax scale * log2(e), applied to q.k in fp32
+    static_assert(!(FRONT && TV), "the front end serves 16-bit caches only");
+    // front end: the new position, and whether this workgroup's range holds it
+    const uint32_t new_pos = a.length - 1;
+    const bool has_new = FRONT && r0 <= new_pos && new_pos < r1;
 
     const size_t head_off = (size_t)seq * a.seq_stride + (size_t)kvh * a.head_stride;
     const char* kb = reinterpret_cast<const char*>(a.keys) + head_off * 2;
@@ -646,6 +658,22 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
     // Q^T operand: lane (g, i) supplies head i (zero for i >= G), dims 32ks + 8g..
     vec qop[KSTEPS];
     auto load_q = [&]() __attribute__((always_inline)) {
+        if constexpr (FRONT) {
+            // the rotated f16 heads the front end left in LDS
+            const int h = li < G ? li : 0;
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks) {
+                const u32x4 raw = *reinterpret_cast<const u32x4*>(&sm_q[h][32 * ks + 8 * lg]);
+                if constexpr (KDT == F16) {
+                    qop[ks] = __builtin_bit_cast(vec, li < G ? raw : u32x4{0u, 0u, 0u, 0u});
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        qop[ks][j] = M::cvt(li < G ? half_bits_to_f32((uint16_t)(raw[j >> 1] >> (16 * (j & 1)))) : 0.0f);
+                }
+            }
+            return;
+        }
         const size_t qrow = ((size_t)seq * hkv * G + kvh * G + (li < G ? li : 0)) * D;
         if (a.query_dtype == KDT) {
             u32x4 raw[KSTEPS];
@@ -706,6 +734,19 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
     auto compute = [&](uint32_t base, uint32_t end, auto mode, u32x4 (&kr)[2][KSTEPS], u32x4 (&vr)[VCH],
                        float (&vs)[VCH]) __attribute__((always_inline)) {
         constexpr int MODE = decltype(mode)::value;
+        if constexpr (FRONT) {
+            // the new position's key row: the front end's copy, not the
+            // cache's (the workgroup stores it there, but its loads of the
+            // tile may have gone out first)
+            if (has_new && new_pos - base < 32u) {
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+                    if (base + 16 * mt + li == new_pos)
+#pragma unroll
+                        for (int ks = 0; ks < KSTEPS; ++ks)
+                            kr[mt][ks] = *reinterpret_cast<const u32x4*>(&sm_kv[0][32 * ks + 8 * lg]);
+            }
+        }
         // S^T = K . Q^T
         f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -730,6 +771,13 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
                 }
             }
             *reinterpret_cast<u32x4*>(vl + row * VROWB + col * 16) = w;
+        }
+        if constexpr (FRONT) {
+            // likewise the new position's value row (same wave, so these LDS
+            // stores land after the tile's)
+            if (has_new && new_pos - base < 32u && lane < D / 8)
+                *reinterpret_cast<u32x4*>(vl + (new_pos - base) * VROWB + lane * 16) =
+                    *reinterpret_cast<const u32x4*>(&sm_kv[1][8 * lane]);
         }
         // online softmax of head `li` over this tile's 32 positions
         float sv[8];
@@ -813,7 +861,81 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
         };
         const uint32_t ntiles = (r1 - r0 + 31) / 32;
         const uint32_t n = ntiles > (uint32_t)wave ? (ntiles - wave + WAVES - 1) / WAVES : 0u;
-        if (n > 0) {
+        if constexpr (FRONT) {
+            u32x4 kr0[2][KSTEPS], vr0[VCH], kr1[2][KSTEPS], vr1[VCH];
+            float vs_unused[VCH];
+            // Front end.  Its loads go out first (L2-resident: the projection's
+            // f16 heads, the norm weights, the pair's inverse frequency), then
+            // the first tile's (past the range: zeros, no request), so the
+            // rotation waits for its own loads only.  Null norm weights read a
+            // stand-in row and weigh by 1.  Wave w rotates query heads 2w and
+            // 2w + 1 of the group; wave 0 of the workgroup holding the new
+            // position also rotates the key head and stores the key and value
+            // rows.
+            const uint16_t* qsrc = fr->query + ((size_t)kvh * G + 2 * wave) * D;
+            const uint16_t* ksrc = fr->key + (size_t)kvh * D;
+            const uint16_t* vsrc = fr->value + (size_t)kvh * D;
+            const float* qn = fr->query_norm ? fr->query_norm : reinterpret_cast<const float*>(fr->query);
+            const float* kn = fr->key_norm ? fr->key_norm : reinterpret_cast<const float*>(fr->query);
+            const uint16_t xq0 = qsrc[lane], xq1 = qsrc[64 + lane], xq2 = qsrc[D + lane], xq3 = qsrc[D + 64 + lane];
+            const uint16_t xk0 = ksrc[lane], xk1 = ksrc[64 + lane], xv0 = vsrc[lane], xv1 = vsrc[64 + lane];
+            const float nq0 = qn[lane], nq1 = qn[64 + lane], nk0 = kn[lane], nk1 = kn[64 + lane];
+            const float freq = fr->inv_freq[lane];
+            __builtin_amdgcn_sched_barrier(0);
+            bload_tile(wave, kr0, vr0);
+            __builtin_amdgcn_sched_barrier(0);
+            float sn, cs;
+            sincosf((float)new_pos * freq, &sn, &cs);
+            const bool qn_on = fr->query_norm != nullptr, kn_on = fr->key_norm != nullptr;
+            float o_l, o_r;
+            qwen_head_norm_rope(half_bits_to_f32(xq0), half_bits_to_f32(xq1), qn_on ? nq0 : 1.0f, qn_on ? nq1 : 1.0f,
+                                cs, sn, o_l, o_r);
+            const uint16_t a_l = bits16<F16>(o_l), a_r = bits16<F16>(o_r);
+            qwen_head_norm_rope(half_bits_to_f32(xq2), half_bits_to_f32(xq3), qn_on ? nq0 : 1.0f, qn_on ? nq1 : 1.0f,
+                                cs, sn, o_l, o_r);
+            const uint16_t b_l = bits16<F16>(o_l), b_r = bits16<F16>(o_r);
+            sm_q[2 * wave][lane] = a_l;
+            sm_q[2 * wave][64 + lane] = a_r;
+            sm_q[2 * wave + 1][lane] = b_l;
+            sm_q[2 * wave + 1][64 + lane] = b_r;
+            if (split == 0) {
+                uint16_t* qo = fr->query_out + ((size_t)kvh * G + 2 * wave) * D;
+                qo[lane] = a_l;
+                qo[64 + lane] = a_r;
+                qo[D + lane] = b_l;
+                qo[D + 64 + lane] = b_r;
+            }
+            if (has_new && wave == 0) {
+                qwen_head_norm_rope(half_bits_to_f32(xk0), half_bits_to_f32(xk1), kn_on ? nk0 : 1.0f,
+                                    kn_on ? nk1 : 1.0f, cs, sn, o_l, o_r);
+                const uint16_t k_l = bits16<KDT>(o_l), k_r = bits16<KDT>(o_r);
+                const uint16_t v_l = bits16<KDT>(half_bits_to_f32(xv0)), v_r = bits16<KDT>(half_bits_to_f32(xv1));
+                uint16_t* kd = reinterpret_cast<uint16_t*>(const_cast<char*>(kb)) + (size_t)new_pos * D;
+                uint16_t* vd = reinterpret_cast<uint16_t*>(const_cast<char*>(vb)) + (size_t)new_pos * D;
+                kd[lane] = k_l;
+                kd[64 + lane] = k_r;
+                vd[lane] = v_l;
+                vd[64 + lane] = v_r;
+                sm_kv[0][lane] = k_l;
+                sm_kv[0][64 + lane] = k_r;
+                sm_kv[1][lane] = v_l;
+                sm_kv[1][64 + lane] = v_r;
+            }
+            __syncthreads();
+            if (n > 0) {
+                load_q();
+                for (uint32_t j = 0; j < n; j += 2) {
+                    const uint32_t t = wave + j * WAVES;
+                    bload_tile(t + WAVES, kr1, vr1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    compute(r0 + 32 * t, r1, std::integral_constant<int, 0>{}, kr0, vr0, vs_unused);
+                    bload_tile(t + 2 * WAVES, kr0, vr0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (j + 1 < n)
+                        compute(r0 + 32 * (t + WAVES), r1, std::integral_constant<int, 0>{}, kr1, vr1, vs_unused);
+                }
+            }
+        } else if (n > 0) {
             u32x4 kr0[2][KSTEPS], vr0[VCH], kr1[2][KSTEPS], vr1[VCH];
             float vs_unused[VCH];
             // (the query's loads first and two tiles requested before the
@@ -873,6 +995,17 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
             if (d == 0) *reinterpret_cast<float2*>(a.ws_ml + 2 * pidx) = float2{Mx, L};
         }
     }
+}
+
+template <int D, int G, int KDT, int WAVES, bool TV = false>
+__global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(DecodeArgs a) {
+    decode_mfma_body<D, G, KDT, WAVES, TV, false>(a, nullptr);
+}
+
+// The Qwen block's decode with its front end folded in (QwenFrontArgs).
+template <int KDT>
+__global__ __launch_bounds__(256) void decode_mfma_front_kernel(DecodeArgs a, QwenFrontArgs f) {
+    decode_mfma_body<128, 8, KDT, 4, false, true>(a, &f);
 }
 
 // Reduce the per-split partials: out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
@@ -1266,6 +1399,30 @@ hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const 
     }
     DecodeArgs a = decode_args(s, kv, p, length, query, query_dtype, out, out_dtype);
     return launch_decode_impl(s, kv, p, a, sequences, workspace, st, dispatches);
+}
+
+hipError_t launch_decode_attention_qwen_front(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p,
+                                              uint32_t length, const QwenFrontArgs& f, void* out, int out_dtype,
+                                              void* workspace, hipStream_t st, int* dispatches) {
+    static_assert(kWaves == 4, "decode_mfma_front_kernel is built for four waves");
+    const int kd = kv.key_dtype;
+    if (s.head_dim != 128 || s.group != 8 || kd != kv.value_dtype || (kd != F16 && kd != BF16) || length == 0 ||
+        f.position + 1 != length)
+        return hipErrorNotSupported;
+    DecodeArgs a = decode_args(s, kv, p, length, f.query_out, F16, out, out_dtype);
+    if (p.splits > 1) {
+        const uint64_t parts = (uint64_t)s.kv_heads * p.splits * s.group;
+        a.ws_ml = reinterpret_cast<float*>(workspace);
+        a.ws_acc = a.ws_ml + 2 * parts;
+    }
+    const dim3 grid(p.splits, s.kv_heads, 1);
+    if (kd == F16) hipLaunchKernelGGL((decode_mfma_front_kernel<F16>), grid, dim3(64 * kWaves), 0, st, a, f);
+    else hipLaunchKernelGGL((decode_mfma_front_kernel<BF16>), grid, dim3(64 * kWaves), 0, st, a, f);
+    if (p.splits > 1)
+        hipLaunchKernelGGL((decode_combine_kernel<128, 8>), dim3(s.q_heads * (128 / kCombineDims), 1),
+                           dim3(kCombineThreads), 0, st, a);
+    *dispatches = p.splits > 1 ? 2 : 1;
+    return hipGetLastError();
 }
 
 // Granite attention block, fp32 and mixed caches: at most 16 splits of 8

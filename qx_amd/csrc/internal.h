@@ -113,6 +113,29 @@ struct DecodePlan {
 // fp32 with a 16-bit partner (the Granite KV plans) for the Granite shape.
 bool decode_dtypes_supported(const ShapeDims& s, int key_dtype, int value_dtype);
 DecodePlan plan_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint32_t sequences, uint32_t length);
+
+// The Qwen block's front end folded into its decode launch: every workgroup
+// normalises and rotates its group's query heads from the q projection's f16
+// output (qwen_norm_rope_append's arithmetic: per-head RMSNorm, RoPE at
+// `position`, f16 rounding), and the workgroup whose range holds `position`
+// normalises and rotates the new key head, stores it and the value row into
+// the cache, and uses its own copy of that row for the position.
+struct QwenFrontArgs {
+    const uint16_t* query;    // f16 [q_heads][128], before the head norm
+    const uint16_t* key;      // f16 [kv_heads][128]
+    const uint16_t* value;    // f16 [kv_heads][128]
+    const float* query_norm;  // [128] or null
+    const float* key_norm;    // [128] or null
+    uint16_t* query_out;      // f16 [q_heads][128]: the rotated query (split 0 writes it)
+    uint32_t position;
+    float inv_freq[64];
+};
+// One sequence's decode at `length` = position + 1 on an equal-dtype 16-bit
+// Qwen cache (no tiered values), its front end folded in; the plan is
+// plan_decode's for one sequence.
+hipError_t launch_decode_attention_qwen_front(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p,
+                                              uint32_t length, const QwenFrontArgs& f, void* out, int out_dtype,
+                                              void* workspace, hipStream_t st, int* dispatches);
 hipError_t launch_decode_attention(const ShapeDims& s, const KvLayer& kv, const DecodePlan& p, uint32_t sequences,
                                    uint32_t length, const void* query, int query_dtype, void* out, int out_dtype,
                                    void* workspace, hipStream_t st, int* dispatches);

@@ -6,8 +6,10 @@
 //
 //   kernel 1  rms_norm(hidden) -> f16 -> Q4 q (4096 rows), k, v (512 rows each)
 //             over 2048 columns -> f16 q/k/v in the workspace
-//   then      the fused Qwen front end (per-head q/k RMSNorm + RoPE, K/V
-//             append; rope_append.hip) and split-K decode attention
+//   then      the Qwen front end (per-head q/k RMSNorm + RoPE, K/V append)
+//             and split-K decode attention: on equal 16-bit caches one
+//             launch (decode_mfma_front_kernel, decode_attention.hip), else
+//             rope_append.hip's kernel, then the decode
 //   kernel 3  Q4 o projection (2048 rows over 4096 columns) -> f16
 //   kernel 4  hidden_after = f16(hidden + o); moe_input = f16(rms_norm(hidden_after))
 //

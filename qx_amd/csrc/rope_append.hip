@@ -95,16 +95,11 @@ __device__ __forceinline__ void qwen_norm_rope_append(const KvLayer& kv, const R
     const float* norm = is_q ? a.query_norm : a.key_norm;
     const float nl = norm ? norm[lane] : 1.0f;
     const float nr = norm ? norm[P + lane] : 1.0f;
-    float ss = xl * xl + xr * xr;
-    ss = group_sum<64>(ss);
-    const float inv_rms = 1.0f / __builtin_sqrtf(ss / 128.0f + 1.0e-6f);
-    const float left = xl * inv_rms * nl;
-    const float right = xr * inv_rms * nr;
     const float angle = (float)pos * freq;
     float sn, cs;
     sincosf(angle, &sn, &cs);
-    const float o_l = left * cs - right * sn;
-    const float o_r = right * cs + left * sn;
+    float o_l, o_r;
+    qwen_head_norm_rope(xl, xr, nl, nr, cs, sn, o_l, o_r);
     if (is_q) {
         store_any(a.query_out, base + lane, o_l, a.output_dtype);
         store_any(a.query_out, base + P + lane, o_r, a.output_dtype);

@@ -1359,6 +1359,31 @@ extern "C" int32_t qxh_encode_qwen_attention_block(qxh_graph* g, qxh_kv_cache* c
     if (c->tiered()) kv.values = nullptr;  // the value row goes through the tiered append below
     hipError_t e = launch_qwen_norm_qkv(a, g->stream);
     if (e != hipSuccess) return hip_fail(e, "qwen norm + qkv launch");
+    int dispatches = 0;
+    const int kd = c->desc.key_dtype;
+    if (!c->tiered() && kd == c->desc.value_dtype && (kd == QXH_F16 || kd == QXH_BF16)) {
+        // equal 16-bit caches: the per-head norm, RoPE and K/V append run
+        // inside the attention launch (no front-end dispatch)
+        QwenFrontArgs f{};
+        f.query = a.query;
+        f.key = a.key;
+        f.value = a.value;
+        f.query_norm = w->query_norm;
+        f.key_norm = w->key_norm;
+        f.query_out = query_rot;
+        f.position = position;
+        qwen_inverse_frequencies(f.inv_freq);
+        e = launch_decode_attention_qwen_front(c->dims, kv, p, length, f, attention, QXH_F16, attn_ws, g->stream,
+                                               &dispatches);
+        if (e != hipSuccess) return hip_fail(e, "qwen attention launch");
+        e = launch_qwen_out(a, g->stream);
+        if (e != hipSuccess) return hip_fail(e, "qwen o projection launch");
+        e = launch_qwen_residual_norm(a, g->stream);
+        if (e != hipSuccess) return hip_fail(e, "qwen residual norm launch");
+        g->dispatches += 3 + dispatches;
+        advance(c, layer, 0, 1, 1);
+        return QXH_OK;
+    }
     RopeAppendArgs ra{};
     ra.query = a.query;
     ra.key = a.key;
@@ -1381,7 +1406,6 @@ extern "C" int32_t qxh_encode_qwen_attention_block(qxh_graph* g, qxh_kv_cache* c
     }
     kv = kv_layer(c, layer, 0);  // the boundary the attention reads
     if (e != hipSuccess) return hip_fail(e, "qwen rope + append launch");
-    int dispatches = 0;
     e = launch_decode_attention(c->dims, kv, p, 1, length, query_rot, QXH_F16, attention, QXH_F16, attn_ws, g->stream,
                                 &dispatches);
     if (e != hipSuccess) return hip_fail(e, "qwen attention launch");

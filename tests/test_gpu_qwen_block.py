@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from qx_amd import abi
+from qx_amd import abi, api
 from qx_amd import runtime as rt
 from tests.helpers import TOL_16, log
 
@@ -118,6 +118,59 @@ def test_qwen_block_stages(ctx, pos):
     # the update has passed four f16 stages on each side
     assert e_upd <= 2 * TOL_16 and e_moe <= TOL_16
     assert err16(f16(after), st["hidden_after_attention"].astype(np.float32)) <= TOL_16
+
+
+def bf16_bits_of(x32):
+    """float32 -> bfloat16 bits, round to nearest even (no NaNs here)."""
+    u = np.asarray(x32, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+# On equal 16-bit caches the block's per-head norm, RoPE and K/V append run
+# inside its attention launch.  Position 0 (one row), 700 (six splits, the
+# new row in a partial last tile) and 32767 (64 splits, the last row of the
+# cache).
+@pytest.mark.parametrize("kdt,pos", [(abi.F16, 0), (abi.F16, 700), (abi.BF16, 3000), (abi.F16, 32767)])
+def test_qwen_block_front_end_inside_the_attention_launch(ctx, kdt, pos):
+    """The rotated query matches the standalone front end
+    (qxh_run_qwen_qk_norm_rope) bit for bit, and so does the stored key on an
+    f16 cache (a bf16 cache rounds the same float once to bf16: within one
+    bf16 step of the f16 value); the stored value row is the projection's;
+    and the attention equals the plain decode of that rotated query over the
+    cache as stored, bit for bit, so the launch used the row it stored."""
+    log("qwen block front end in the attention launch", kdt, pos)
+    rng = np.random.default_rng(pos + 17 * kdt)
+    _, norms, layer = weights(rng)
+    arena = rt.KvArena(ctx, abi.SHAPE_QWEN3, 1, 1, pos + 1, kdt)
+    if pos:
+        with rt.Graph(ctx) as g:
+            arena.fill_normal(g, seed=pos + 1, length=pos)
+    h = rng.standard_normal(HID).astype(np.float16)
+    after = torch.empty(HID, dtype=torch.int16, device="cuda:0")
+    moe = torch.empty_like(after)
+    wsp = torch.zeros(rt.qwen_block_workspace_bytes(arena, pos + 1), dtype=torch.uint8, device="cuda:0")
+    with rt.Graph(ctx) as g:
+        rt.qwen_attention_block(g, arena, 0, pos, layer, dev(h.view(np.int16)), after, moe, wsp)
+        kk, vv = arena.gather(g, 0, 0, pos, 1)
+    q, k, v, qrot, att, _ = workspace_stages(wsp)
+    qo, ko = api.run_qwen_qk_norm_rope(q.cpu().numpy().view(np.uint16), k.cpu().numpy().view(np.uint16), norms[1],
+                                       norms[2], pos, O.F16)
+    assert np.array_equal(qrot.cpu().numpy().view(np.uint16), qo)
+    k_row = kk.contiguous().view(torch.int16).cpu().numpy().ravel().view(np.uint16)
+    v_row = vv.contiguous().view(torch.int16).cpu().numpy().ravel().view(np.uint16)
+    v16 = v.cpu().numpy().view(np.uint16)
+    if kdt == abi.F16:
+        assert np.array_equal(k_row, ko)
+        assert np.array_equal(v_row, v16)
+    else:
+        kf = ko.view(np.float16).astype(np.float32)
+        kb = (k_row.astype(np.uint32) << 16).view(np.float32)
+        assert np.all(np.abs(kb - kf) <= np.abs(kf) * 2.0 ** -8 + 1e-30)
+        assert np.array_equal(v_row, bf16_bits_of(v16.view(np.float16).astype(np.float32)))
+    qt = qrot.view(torch.float16).reshape(1, 32, 128).contiguous()
+    with rt.Graph(ctx) as g:
+        plain = rt.attention(g, arena, 0, qt, pos + 1, out_dtype=torch.float16)
+    assert torch.equal(plain.reshape(-1).view(torch.int16), att)
 
 
 def test_qwen_block_graph_replay_is_deterministic(ctx):
