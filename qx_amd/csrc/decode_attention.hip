@@ -1178,15 +1178,20 @@ DecodePlan plan_decode(const ShapeDims& s, int key_dtype, int value_dtype, uint3
     // tiered: 18.0 us at 256, 20.2 at 512)
     if (s.group >= 8 && min_chunk < qwen_min_chunk(key_dtype, value_dtype, units, length))
         min_chunk = qwen_min_chunk(key_dtype, value_dtype, units, length);
-    // Granite on the MFMA kernel: a split adds the combine dispatch (about
-    // 2.5 us), which a short context never wins back, so one chunk per head up
+    // On the MFMA kernel a split adds the combine dispatch (about 2.5 us),
+    // which a short context never wins back, so one chunk per head: Granite up
     // to 768 positions, or up to 2048 once the heads alone make 128 or more
-    // workgroups.  Measured, f16, us per layer (split to 2048 workgroups / one
-    // chunk): one sequence at 256 positions 5.9 / 3.5, at 768 6.0 / 5.8, at
-    // 1024 6.3 / 7.3; 16 sequences at 1024 13.1 / 9.1, at 2048 15.8 (split to
-    // 256) / 15.6; 64 sequences at 512 20.4 / 12.7.
-    if (!valu && s.group < 8 && (length <= 768 || (units >= 128 && length <= 2048)) && length > min_chunk)
-        min_chunk = length;
+    // workgroups; Qwen, whose position costs four times the matrix work, up
+    // to 256, or 512 from 64 workgroups (tiered values keep their splits).
+    // Measured, us per layer (split / one chunk): Granite f16, one sequence
+    // at 256 positions 5.9 / 3.5, at 768 6.0 / 5.8, at 1024 6.3 / 7.3; 16
+    // sequences at 1024 13.1 / 9.1, at 2048 15.8 / 15.6; 64 sequences at 512
+    // 20.4 / 12.7; Qwen bf16, one sequence at 256 8.1 / 6.4, at 512 8.1 /
+    // 8.7; 16 sequences at 512 11.2 / 10.0, at 768 11.7 / 12.8.
+    const bool one_chunk = s.group < 8 ? length <= 768 || (units >= 128 && length <= 2048)
+                                       : !tiered_on_mfma(s, key_dtype, value_dtype) &&
+                                             (length <= 256 || (units >= 64 && length <= 512));
+    if (!valu && one_chunk && length > min_chunk) min_chunk = length;
     // Split count: toward 2048 workgroups on the VALU kernel; on the MFMA
     // kernel at most 256 (one a CU), rounded down, since each split costs a
     // share of the combine's workspace round trip and a count rounded up past

@@ -114,15 +114,19 @@ def test_granite_decode_lengths_and_dtypes(ctx, kdt, length):
 
 # The MFMA decode plan's boundaries (16-bit caches): Granite keeps one chunk
 # per head up to 768 positions, or up to 2048 once the heads make 128 or more
-# workgroups; past that, and for Qwen, the split count is at most 256
-# workgroups' worth, rounded down (3 sequences = 24 Granite units: 7 splits
-# at 769 positions, 8 at 4096; 16 sequences = 128 units: 2 at 2049; 3 Qwen
-# sequences = 12 units: 19 at 16384).  Each case against the oracle, and the
-# plan's shape read from its workspace size (zero for one chunk).
+# workgroups; Qwen up to 256, or 512 from 64 workgroups; past that the split
+# count is at most 256 workgroups' worth, rounded down (3 sequences = 24
+# Granite units: 7 splits at 769 positions, 8 at 4096; 16 sequences = 128
+# units: 2 at 2049; Qwen, one sequence = 4 units: 3 at 257; 16 sequences = 64
+# units: 3 at 513; 3 sequences = 12 units: 19 at 16384).  Each case against
+# the oracle, and the plan's shape read from its workspace size (zero for
+# one chunk).
 @pytest.mark.parametrize("shape,kdt,S,L,single", [
     (abi.SHAPE_GRANITE, abi.F16, 3, 768, True), (abi.SHAPE_GRANITE, abi.F16, 3, 769, False),
     (abi.SHAPE_GRANITE, abi.BF16, 3, 4096, False), (abi.SHAPE_GRANITE, abi.F16, 16, 2048, True),
-    (abi.SHAPE_GRANITE, abi.BF16, 16, 2049, False), (abi.SHAPE_QWEN3, abi.BF16, 3, 16384, False)])
+    (abi.SHAPE_GRANITE, abi.BF16, 16, 2049, False), (abi.SHAPE_QWEN3, abi.BF16, 1, 256, True),
+    (abi.SHAPE_QWEN3, abi.F16, 1, 257, False), (abi.SHAPE_QWEN3, abi.BF16, 16, 512, True),
+    (abi.SHAPE_QWEN3, abi.BF16, 16, 513, False), (abi.SHAPE_QWEN3, abi.BF16, 3, 16384, False)])
 def test_mfma_decode_plan_boundaries(ctx, shape, kdt, S, L, single):
     log("mfma decode plan boundary", shape, kdt, S, L)
     info = rt.shape_info(shape)
@@ -153,7 +157,8 @@ def test_mfma_decode_plan_boundaries(ctx, shape, kdt, S, L, single):
             ref_cache.extend(kk.float().cpu().numpy(), vv.float().cpu().numpy())
             r = O.granite_attend(q[s].float().cpu().numpy().ravel(), ref_cache, L)
         else:
-            _, r = O.qwen_gqa_attention(tobits(q[s]), tobits(kk), tobits(vv), O.BF16, want_f32=True)
+            _, r = O.qwen_gqa_attention(tobits(q[s]), tobits(kk), tobits(vv), O.F16 if kdt == abi.F16 else O.BF16,
+                                        want_f32=True)
         e = rel_err(out[s].cpu().numpy().ravel(), r)
         worst = max(worst, e)
         assert e <= TOL_16, (s, e)
