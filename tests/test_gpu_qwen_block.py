@@ -127,10 +127,12 @@ def bf16_bits_of(x32):
 
 
 # On equal 16-bit caches the block's per-head norm, RoPE and K/V append run
-# inside its attention launch.  Position 0 (one row), 700 (six splits, the
-# new row in a partial last tile) and 32767 (64 splits, the last row of the
-# cache).
-@pytest.mark.parametrize("kdt,pos", [(abi.F16, 0), (abi.F16, 700), (abi.BF16, 3000), (abi.F16, 32767)])
+# inside its attention launch.  Position 0 (one row), 31 (the last row of a
+# full tile), 32 (the first row of wave 1's tile), 512 (the lone row of the
+# last of five 128-position splits), 700 (six splits, the new row in a
+# partial last tile) and 32767 (64 splits, the last row of the cache).
+@pytest.mark.parametrize("kdt,pos", [(abi.F16, 0), (abi.F16, 31), (abi.BF16, 32), (abi.F16, 512), (abi.F16, 700),
+                                     (abi.BF16, 3000), (abi.F16, 32767)])
 def test_qwen_block_front_end_inside_the_attention_launch(ctx, kdt, pos):
     """The rotated query matches the standalone front end
     (qxh_run_qwen_qk_norm_rope) bit for bit, and so does the stored key on an
