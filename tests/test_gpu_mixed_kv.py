@@ -160,6 +160,43 @@ def test_granite_block_on_fp32k_fp16v_cache(ctx):
     assert rel_err(vv.float().cpu().numpy(), ref.values()) <= TOL_16
 
 
+# The fp32-weight block on equal 16-bit caches runs its attention on the MFMA
+# decode: one chunk at 701 positions, split past 768 (1001 and 2501).
+@pytest.mark.parametrize("kdt,position", [(abi.F16, 700), (abi.F16, 1000), (abi.BF16, 2500)])
+def test_granite_block_on_16bit_cache(ctx, kdt, position):
+    """The block output against the oracle's block over a cache with the same
+    store rounding, and its attention (the workspace's merged attention for
+    its own rotated query) against granite_attend over the rows the cache
+    holds, at the 16-bit bar."""
+    log("granite block on a 16-bit cache", kdt, position)
+    rng = np.random.default_rng(63 + position)
+    nw, ws = granite_weights(rng)
+    layer = rt.GraniteLayer(dev(nw), *[dev(w) for w in ws])
+    L = position + 1
+    arena = rt.KvArena(ctx, abi.SHAPE_GRANITE, 1, 1, L, kdt)
+    with rt.Graph(ctx) as g:
+        arena.fill_normal(g, seed=position, length=position)
+    h = rng.standard_normal(1024, dtype=np.float32)
+    out = torch.empty(1024, device="cuda:0")
+    wsp = torch.zeros(rt.granite_block_workspace_bytes(arena, L), dtype=torch.uint8, device="cuda:0")
+    with rt.Graph(ctx) as g:
+        rt.granite_attention_block(g, arena, 0, position, layer, dev(h), out, wsp)
+        kk, vv = arena.gather(g, 0, 0, 0, L)
+    kf, vf = kk.float().cpu().numpy(), vv.float().cpu().numpy()
+    fmt = O.F16 if kdt == abi.F16 else O.BF16
+    ref = O.KvCache(L, fmt, fmt)
+    ref.extend(kf[:position], vf[:position])
+    r = O.granite_attention_block(h, nw, *ws, position, ref)
+    assert rel_err(out.cpu().numpy(), r) <= TOL_16
+    w = wsp[:2 * 1024 * 4].view(torch.float32).cpu().numpy()
+    q_rot, att = w[:1024], w[1024:]
+    held = O.KvCache(L, fmt, fmt)
+    held.extend(kf, vf)
+    e = rel_err(att, O.granite_attend(q_rot, held, L))
+    log(f"  attention vs oracle {e:.3e}")
+    assert e <= TOL_16
+
+
 def test_q4_block_on_fp32k_fp16v_cache(ctx):
     """The Q4 attention block on the canonical KV plan: K rows (norm, Q4
     projection, RoPE) and fp16-rounded V rows bit for bit."""
